@@ -1,0 +1,124 @@
+/*
+ * crispybits_hip.h -- C ABI of the MI355X (gfx950) packed W2/W3/W4 linear kernels.
+ *
+ * This is the drop-in boundary that replaces the reference's pybind11 module
+ * `crispybits_kernels._C` (/root/reference/Crispybits/Kernel/csrc/bindings.cpp:32-40).
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (as void*),
+ * launches asynchronously on that stream and returns a status code; no torch types
+ * cross this boundary.  The Python host layer (crispybits_kernels/_C.py) binds it
+ * with ctypes and keeps the reference's argument order and error behaviour.
+ *
+ * Conventions shared by all entry points
+ *   - dtype: CBK_F16 / CBK_BF16 / CBK_F32 is the type of x, scales, zeros, bias and
+ *     out (host_utils.h:60,84 require them to match).
+ *   - packed: int32 [N, ceil(K/32)*bits] row-major, LSB-first bitstream, rows padded
+ *     to 32-code chunks; base alignment 16/4/8 bytes for W4/W3/W2 (host_utils.h:63-68).
+ *   - scales / zeros: [N, ceil(K/group_size)] row-major; zeros hold exact integers.
+ *   - bias: [N] or NULL ("no bias" is an empty tensor in the reference, host_utils.h:80-81).
+ *   - act: CBK_ACT_NONE / CBK_ACT_RELU / CBK_ACT_SILU (ops.py:24, common.cuh:10).
+ *   - rho <= 0: one workgroup per job; rho > 0: min(jobs, rho * CUs) persistent
+ *     workgroups (host_utils.h:90-93).
+ *   - workspace: the caller's int32[2] job-queue word pair (host_utils.h:38-47).  Jobs are
+ *     distributed statically here, so the workspace is accepted, never written, and its
+ *     [0,0] contract holds trivially.  May be NULL.
+ *   - partial: fp32 scratch of cbk_gemv_partial_floats(...) elements, required only when
+ *     that query returns a positive count (split-K partial sums, packed_gemv.cu:193-199).
+ *   - device: HIP device ordinal the pointers live on (the reference's CUDAGuard,
+ *     packed_gemv.cu:259); the calling thread's current device is restored on return.
+ *   - return: CBK_OK, or an error code with a message from cbk_last_error().
+ */
+#ifndef CRISPYBITS_HIP_H
+#define CRISPYBITS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { CBK_F16 = 0, CBK_BF16 = 1, CBK_F32 = 2 };
+enum { CBK_ACT_NONE = 0, CBK_ACT_RELU = 1, CBK_ACT_SILU = 2 };
+enum { CBK_MODE_GEMV = 0, CBK_MODE_QKV = 1, CBK_MODE_GATEUP = 2 };
+enum { CBK_OK = 0, CBK_EINVAL = 1, CBK_EHIP = 2 };
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* cbk_last_error(void);
+
+/* ABI revision; bumped when a signature changes. */
+int cbk_abi_version(void);
+
+/* Compute units of `device` (replaces crispybits_sm_count, packed_gemv.cu:339). */
+int cbk_sm_count(int device, int* out);
+
+/* Virtual output rows per decode job tile -- the B_N of the split-K policy
+ * (replaces crispybits_tile_n, packed_gemv.cu:340). */
+int cbk_tile_n(void);
+
+/* Occupancy-limited resident decode workgroups per CU of the fp16 kernel for `bits`
+ * and `mode` (replaces crispybits_max_rho_mode, packed_gemv.cu:343-347). */
+int cbk_max_rho(int device, int bits, int mode, int* out);
+
+/* fp32 elements of `partial` that a decode call with these arguments needs
+ * (0 = none).  `V` is the number of virtual rows (N, nq+nk+nv or 2N). */
+int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int group_size,
+                                int split_k);
+
+/* out[M,N] = act(x[M,K] . W-hat^T + bias) on the decode path
+ * (replaces packed_gemv_cuda, packed_gemv.cu:252-269; bindings.cpp:4-6). */
+int cbk_packed_gemv(const void* x, int dtype, int64_t M, int64_t K,
+                    const int32_t* packed, const void* scales, const void* zeros, const void* bias,
+                    int64_t N, int bits, int group_size, int split_k, int rho, int act,
+                    int32_t* workspace, float* partial, void* out, int device, void* stream);
+
+/* out[M,N] = silu(x . G-hat^T) * (x . U-hat^T) with gate and up read in one pass
+ * (replaces fused_gate_up_cuda, packed_gemv.cu:317-337; bindings.cpp:10-13). */
+int cbk_fused_gate_up(const void* x, int dtype, int64_t M, int64_t K,
+                      const int32_t* wg, const void* sg, const void* zg,
+                      const int32_t* wu, const void* su, const void* zu,
+                      int64_t N, int bits, int group_size, int split_k, int rho,
+                      int32_t* workspace, float* partial, void* out, int device, void* stream);
+
+/* Fused Q/K/V decode with per-projection bias and optional in-kernel RoPE on
+ * pair-interleaved Q/K rows (replaces fused_qkv_cuda, packed_gemv.cu:271-315;
+ * bindings.cpp:14-20).  rope_cos / rope_sin: fp32 [M, head_dim] or NULL.
+ * perm_hd: head_dim the Q/K rows are stored permuted with (0 = not permuted). */
+int cbk_fused_qkv(const void* x, int dtype, int64_t M, int64_t K,
+                  const int32_t* wq, const void* sq, const void* zq, const void* bq, int64_t nq,
+                  const int32_t* wk, const void* sk, const void* zk, const void* bk, int64_t nk,
+                  const int32_t* wv, const void* sv, const void* zv, const void* bv, int64_t nv,
+                  const float* rope_cos, const float* rope_sin, int head_dim, int perm_hd,
+                  int bits, int group_size, int split_k, int rho,
+                  int32_t* workspace, float* partial, void* out_q, void* out_k, void* out_v,
+                  int device, void* stream);
+
+/* Additive: fused Q/K/V with one bit-width per projection.  No counterpart in the
+ * reference (its fused_qkv takes one `bits`, ops.py:240-241); used when a block's
+ * projections were quantized to different widths. */
+int cbk_fused_qkv_mixed(const void* x, int dtype, int64_t M, int64_t K,
+                        const int32_t* wq, const void* sq, const void* zq, const void* bq, int64_t nq,
+                        const int32_t* wk, const void* sk, const void* zk, const void* bk, int64_t nk,
+                        const int32_t* wv, const void* sv, const void* zv, const void* bv, int64_t nv,
+                        const float* rope_cos, const float* rope_sin, int head_dim, int perm_hd,
+                        int bits_q, int bits_k, int bits_v, int group_size, int split_k, int rho,
+                        int32_t* workspace, float* partial, void* out_q, void* out_k, void* out_v,
+                        int device, void* stream);
+
+/* Prefill: out[M,N] = act(x . W-hat^T + bias).  With use_matrix_cores and fp16/bf16 x,
+ * W-hat = RN_T((q - z) * s) runs on MFMA; otherwise an fp32 VALU kernel computes it
+ * unrounded (replaces packed_gemm_cuda, packed_gemm.cu:182-203; bindings.cpp:7-9). */
+int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K,
+                    const int32_t* packed, const void* scales, const void* zeros, const void* bias,
+                    int64_t N, int bits, int group_size, int act, int use_matrix_cores,
+                    void* out, int device, void* stream);
+
+/* Additive test hook: codes[N,K] (int32) of a packed matrix, for the bit-exact
+ * code check.  No counterpart in the reference's _C (reference.py:58-67 is its
+ * CPU equivalent). */
+int cbk_unpack_codes(const int32_t* packed, int64_t N, int64_t K, int bits, int32_t* codes,
+                     int device, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CRISPYBITS_HIP_H */

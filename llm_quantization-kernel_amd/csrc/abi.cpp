@@ -1,0 +1,423 @@
+// abi.cpp -- the extern "C" entry points of libcrispybits_hip.so (include/crispybits_hip.h).
+//
+// Replaces the reference's host glue: argument checks of host_utils.h:49-93,
+// launch planning of packed_gemv.cu:182-238 / packed_gemm.cu:158-203, and the
+// module exports of bindings.cpp:32-40.  Every check runs before the first HIP
+// call, so invalid arguments are reported without touching a device.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/crispybits_hip.h"
+#include "cbk_kernels.hpp"
+
+using namespace cbk;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(CBK_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Switches to `device` for the duration of a call (the reference's CUDAGuard).
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceGuard(int device) {
+        err = hipGetDevice(&prev);
+        if (err == hipSuccess && prev != device) err = hipSetDevice(device);
+        else if (err != hipSuccess) prev = -1;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+constexpr int MAX_DEVICES = 64;
+int g_cu[MAX_DEVICES];
+std::once_flag g_cu_once[MAX_DEVICES];
+
+int cu_count(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return 0;
+    std::call_once(g_cu_once[device], [device] {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) v = 0;
+        g_cu[device] = v;
+    });
+    return g_cu[device];
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+constexpr int MFMA_TILE = 16;          // virtual rows per MFMA decode job
+constexpr int LDS_BUDGET = 96 * 1024;  // dynamic LDS per decode workgroup
+constexpr int WAVES_PER_CU = 8;        // decode occupancy target
+
+bool valid_dtype(int dt) { return dt == CBK_F16 || dt == CBK_BF16 || dt == CBK_F32; }
+
+int check_weight(const int32_t* packed, const void* scales, const void* zeros, int64_t n, int bits,
+                 int group_size, const char* name) {
+    if (!packed || !scales || !zeros) return fail(CBK_EINVAL, "%s: packed/scales/zeros must be non-null", name);
+    if (n <= 0) return fail(CBK_EINVAL, "%s: out_features must be positive", name);
+    if (n > (1 << 30)) return fail(CBK_EINVAL, "%s: out_features too large", name);
+    if (bits != 2 && bits != 3 && bits != 4) return fail(CBK_EINVAL, "%s: bits must be 2/3/4", name);
+    if (group_size <= 0 || group_size % 32 != 0)
+        return fail(CBK_EINVAL, "%s: group_size must be a positive multiple of 32", name);
+    const uintptr_t align = bits == 4 ? 16 : (bits == 2 ? 8 : 4);
+    if (reinterpret_cast<uintptr_t>(packed) % align != 0)
+        return fail(CBK_EINVAL, "%s: packed storage must be %d-byte aligned for vector loads", name, (int)align);
+    return CBK_OK;
+}
+
+int check_x(const void* x, int dtype, int64_t M, int64_t K) {
+    if (!valid_dtype(dtype)) return fail(CBK_EINVAL, "x must be fp16/bf16/fp32");
+    if (M < 0) return fail(CBK_EINVAL, "x must be [B,K] with B >= 0");
+    if (K <= 0 || K > (1 << 24)) return fail(CBK_EINVAL, "in_features must be in [1, 2^24]");
+    if (M > 0 && !x) return fail(CBK_EINVAL, "x must be non-null");
+    if (M > (1 << 24)) return fail(CBK_EINVAL, "too many rows in x");
+    return CBK_OK;
+}
+
+// ----------------------------------------------------------------------------- decode plan
+struct Plan {
+    bool mfma = false;
+    int P = 1, ntiles = 0, mtiles = 0, jobs = 0, grid = 0;
+    int nw = 1, units = 0, xs_bytes = 0, red_off = 0, lds = 0;
+};
+
+int mfma_lds(int64_t units, int P, int mt, int nw, int* xs_bytes, int* red_off) {
+    const int64_t nu = ceil_div(units, P);
+    const int64_t xs = nu * 256 * mt;
+    const int64_t xsum = nu * 16 * 4;
+    const int64_t red = std::max<int64_t>(nu * 4 * mt * 4, (int64_t)std::max(nw - 1, 1) * 1024);
+    if (xs_bytes) *xs_bytes = (int)xs;
+    if (red_off) *red_off = (int)(xs + xsum);
+    return (int)(xs + xsum + red);
+}
+
+Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int split_k, int rho, int cus, bool mfma_ok) {
+    Plan pl;
+    const int64_t C = ceil_div(K, 32);
+    pl.mfma = mfma_ok && dtype == CBK_F16 && gs % 128 == 0;
+    const int64_t sm = std::max(cus, 1);
+    if (pl.mfma) {
+        pl.units = (int)ceil_div(C, 4);
+        const int mt = (int)std::min<int64_t>(16, std::max<int64_t>(M, 1));
+        pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, pl.units));
+        while (pl.P < pl.units && mfma_lds(pl.units, pl.P, mt, 8, nullptr, nullptr) > LDS_BUDGET) ++pl.P;
+        pl.ntiles = (int)ceil_div(V, MFMA_TILE);
+        pl.mtiles = (int)ceil_div(std::max<int64_t>(M, 1), 16);
+        const int64_t jobs = (int64_t)pl.mtiles * pl.ntiles * pl.P;
+        pl.jobs = (int)jobs;
+        pl.grid = (int)(rho > 0 ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm)) : jobs);
+        const int64_t min_units = pl.units / pl.P;
+        int64_t nw = ceil_div((int64_t)WAVES_PER_CU * sm, pl.grid);
+        nw = std::max<int64_t>(1, std::min<int64_t>({nw, 8, std::max<int64_t>(min_units, 1)}));
+        pl.nw = (int)nw;
+        pl.lds = mfma_lds(pl.units, pl.P, mt, pl.nw, &pl.xs_bytes, &pl.red_off);
+    } else {
+        pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, C));
+        pl.ntiles = (int)ceil_div(V, GENERIC_ROWS);
+        pl.mtiles = (int)std::max<int64_t>(M, 1);
+        const int64_t jobs = (int64_t)pl.mtiles * pl.ntiles * pl.P;
+        pl.jobs = (int)jobs;
+        pl.grid = (int)(rho > 0 ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm)) : jobs);
+    }
+    return pl;
+}
+
+std::mutex g_attr_mu;
+
+hipError_t ensure_lds(const void* f, int bytes) {
+    if (bytes <= 64 * 1024) return hipSuccess;
+    std::lock_guard<std::mutex> lk(g_attr_mu);
+    return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
+// Common body of the three decode entry points.
+int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rho, float* partial, int device,
+               void* stream) {
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    const int cus = cu_count(device);
+    if (cus <= 0) return fail(CBK_EHIP, "cannot query the compute-unit count of device %d", device);
+    const bool mfma_ok = !mixed || (A.p[0].n % MFMA_TILE == 0 && A.p[1].n % MFMA_TILE == 0);
+    const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, split_k, rho, cus, mfma_ok);
+    A.P = pl.P;
+    A.ntiles = pl.ntiles;
+    A.mtiles = pl.mtiles;
+    A.jobs = pl.jobs;
+    A.nw = pl.nw;
+    A.units = pl.units;
+    A.xs_bytes = pl.xs_bytes;
+    A.red_off = pl.red_off;
+    A.lds_bytes = pl.lds;
+    if (A.P > 1) {
+        if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
+        A.partial = partial;
+    } else {
+        A.partial = nullptr;
+    }
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (pl.mfma) {
+        const void* f = gemv_mfma_kernel_for(mode, A.p[0].bits, mixed, A.M);
+        e = ensure_lds(f, pl.lds);
+        if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
+        void* args[] = {&A};
+        e = hipLaunchKernel(f, dim3(pl.grid), dim3(64 * pl.nw), args, (size_t)pl.lds, s);
+    } else {
+        e = launch_gemv_generic(A, dtype, mode, pl.grid, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
+    if (A.P > 1) {
+        e = launch_gemv_reduce(A, dtype, mode, s);
+        if (e != hipSuccess) return hip_fail(e, "packed_gemv: reduce launch");
+    }
+    return CBK_OK;
+}
+
+Proj make_proj(const int32_t* w, const void* s, const void* z, const void* b, void* out, int64_t n, int bits,
+               int64_t K) {
+    Proj p{};
+    p.w = reinterpret_cast<const uint32_t*>(w);
+    p.s = s;
+    p.z = z;
+    p.b = b;
+    p.out = out;
+    p.n = (int)n;
+    p.bits = bits;
+    p.wpr = (int)(ceil_div(K, 32) * bits);
+    return p;
+}
+
+GemvArgs base_args(const void* x, int64_t M, int64_t K, int gs) {
+    GemvArgs A;
+    std::memset(&A, 0, sizeof(A));
+    A.x = x;
+    A.M = (int)M;
+    A.K = (int)K;
+    A.C = (int)ceil_div(K, 32);
+    A.G = (int)ceil_div(K, gs);
+    A.gs = gs;
+    return A;
+}
+
+int qkv_common(const void* x, int dtype, int64_t M, int64_t K, const int32_t* wq, const void* sq, const void* zq,
+               const void* bq, int64_t nq, const int32_t* wk, const void* sk, const void* zk, const void* bk,
+               int64_t nk, const int32_t* wv, const void* sv, const void* zv, const void* bv, int64_t nv,
+               const float* rope_cos, const float* rope_sin, int head_dim, int perm_hd, int bits_q, int bits_k,
+               int bits_v, int group_size, int split_k, int rho, float* partial, void* out_q, void* out_k,
+               void* out_v, int device, void* stream) {
+    int rc = check_x(x, dtype, M, K);
+    if (rc) return rc;
+    if ((rc = check_weight(wq, sq, zq, nq, bits_q, group_size, "fused_qkv(q)"))) return rc;
+    if ((rc = check_weight(wk, sk, zk, nk, bits_k, group_size, "fused_qkv(k)"))) return rc;
+    if ((rc = check_weight(wv, sv, zv, nv, bits_v, group_size, "fused_qkv(v)"))) return rc;
+    if (split_k < 1) return fail(CBK_EINVAL, "split_k must be >= 1");
+    if (!out_q || !out_k || !out_v) return fail(CBK_EINVAL, "fused_qkv: outputs must be non-null");
+    if (perm_hd < 0 || head_dim < 0) return fail(CBK_EINVAL, "head_dim must be >= 0");
+    if (perm_hd > 0) {
+        if (perm_hd % 2) return fail(CBK_EINVAL, "perm head_dim must be even");
+        if (nq % perm_hd || nk % perm_hd) return fail(CBK_EINVAL, "Q/K widths must be multiples of head_dim");
+    }
+    const bool rope = rope_cos != nullptr;
+    if (rope) {
+        if (!rope_sin) return fail(CBK_EINVAL, "cos/sin shape mismatch");
+        if (!(perm_hd > 0 && perm_hd == head_dim))
+            return fail(CBK_EINVAL,
+                        "fused RoPE needs Q/K weights stored pair-interleaved with the same head_dim "
+                        "(ops.permute_for_rope / install_bitmap(fuse_rope=True))");
+    }
+    if (M == 0) return CBK_OK;
+    GemvArgs A = base_args(x, M, K, group_size);
+    A.p[0] = make_proj(wq, sq, zq, bq, out_q, nq, bits_q, K);
+    A.p[1] = make_proj(wk, sk, zk, bk, out_k, nk, bits_k, K);
+    A.p[2] = make_proj(wv, sv, zv, bv, out_v, nv, bits_v, K);
+    A.V = (int)(nq + nk + nv);
+    A.perm_hd = perm_hd;
+    if (rope) {
+        A.rope_cos = rope_cos;
+        A.rope_sin = rope_sin;
+        A.head_dim = head_dim;
+    }
+    const bool mixed = !(bits_q == bits_k && bits_k == bits_v);
+    return run_decode(A, dtype, CBK_MODE_QKV, mixed, split_k, rho, partial, device, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cbk_last_error(void) { return g_err.c_str(); }
+
+int cbk_abi_version(void) { return 1; }
+
+int cbk_sm_count(int device, int* out) {
+    if (!out) return fail(CBK_EINVAL, "out must be non-null");
+    const int c = cu_count(device);
+    if (c <= 0) return fail(CBK_EHIP, "cannot query the compute-unit count of device %d", device);
+    *out = c;
+    return CBK_OK;
+}
+
+int cbk_tile_n(void) { return MFMA_TILE; }
+
+int cbk_max_rho(int device, int bits, int mode, int* out) {
+    if (!out) return fail(CBK_EINVAL, "out must be non-null");
+    if (bits != 2 && bits != 3 && bits != 4) return fail(CBK_EINVAL, "bits must be 2/3/4");
+    if (mode < 0 || mode > 2) return fail(CBK_EINVAL, "kind must be 'gemv', 'qkv' or 'gate_up'");
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    // fp16 decode of a 4096-wide row at batch 1 with 4 waves per workgroup
+    const void* f = gemv_mfma_kernel_for(mode, bits, false, 1);
+    const int lds = mfma_lds(32, 1, 1, 4, nullptr, nullptr);
+    int blocks = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, 256, (size_t)lds);
+    if (e != hipSuccess) return hip_fail(e, "max_rho: occupancy query");
+    *out = blocks;
+    return CBK_OK;
+}
+
+int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int group_size, int split_k) {
+    if (M <= 0 || V <= 0 || K <= 0 || group_size <= 0 || split_k < 1) return 0;
+    int P = 1;
+    for (bool mf : {true, false}) {
+        const Plan pl = plan_gemv(dtype, M, V, K, group_size, split_k, 0, 256, mf);
+        P = std::max(P, pl.P);
+    }
+    return P > 1 ? (int64_t)P * M * V : 0;
+}
+
+int cbk_packed_gemv(const void* x, int dtype, int64_t M, int64_t K, const int32_t* packed, const void* scales,
+                    const void* zeros, const void* bias, int64_t N, int bits, int group_size, int split_k, int rho,
+                    int act, int32_t* workspace, float* partial, void* out, int device, void* stream) {
+    (void)workspace;
+    int rc = check_x(x, dtype, M, K);
+    if (rc) return rc;
+    if ((rc = check_weight(packed, scales, zeros, N, bits, group_size, "packed_gemv"))) return rc;
+    if (split_k < 1) return fail(CBK_EINVAL, "split_k must be >= 1");
+    if (act < 0 || act > 2) return fail(CBK_EINVAL, "act must be 0 (none), 1 (relu) or 2 (silu)");
+    if (!out) return fail(CBK_EINVAL, "packed_gemv: out must be non-null");
+    if (M == 0) return CBK_OK;
+    GemvArgs A = base_args(x, M, K, group_size);
+    A.p[0] = make_proj(packed, scales, zeros, bias, out, N, bits, K);
+    A.p[1] = A.p[0];
+    A.p[2] = A.p[0];
+    A.V = (int)N;
+    A.act = act;
+    return run_decode(A, dtype, CBK_MODE_GEMV, false, split_k, rho, partial, device, stream);
+}
+
+int cbk_fused_gate_up(const void* x, int dtype, int64_t M, int64_t K, const int32_t* wg, const void* sg,
+                      const void* zg, const int32_t* wu, const void* su, const void* zu, int64_t N, int bits,
+                      int group_size, int split_k, int rho, int32_t* workspace, float* partial, void* out,
+                      int device, void* stream) {
+    (void)workspace;
+    int rc = check_x(x, dtype, M, K);
+    if (rc) return rc;
+    if ((rc = check_weight(wg, sg, zg, N, bits, group_size, "fused_gate_up(gate)"))) return rc;
+    if ((rc = check_weight(wu, su, zu, N, bits, group_size, "fused_gate_up(up)"))) return rc;
+    if (split_k < 1) return fail(CBK_EINVAL, "split_k must be >= 1");
+    if (!out) return fail(CBK_EINVAL, "fused_gate_up: out must be non-null");
+    if (2 * N > (1 << 30)) return fail(CBK_EINVAL, "fused_gate_up: out_features too large");
+    if (M == 0) return CBK_OK;
+    GemvArgs A = base_args(x, M, K, group_size);
+    A.p[0] = make_proj(wg, sg, zg, nullptr, out, N, bits, K);
+    A.p[1] = make_proj(wu, su, zu, nullptr, out, N, bits, K);
+    A.p[2] = A.p[0];
+    A.V = (int)(2 * N);
+    return run_decode(A, dtype, CBK_MODE_GATEUP, false, split_k, rho, partial, device, stream);
+}
+
+int cbk_fused_qkv(const void* x, int dtype, int64_t M, int64_t K, const int32_t* wq, const void* sq, const void* zq,
+                  const void* bq, int64_t nq, const int32_t* wk, const void* sk, const void* zk, const void* bk,
+                  int64_t nk, const int32_t* wv, const void* sv, const void* zv, const void* bv, int64_t nv,
+                  const float* rope_cos, const float* rope_sin, int head_dim, int perm_hd, int bits, int group_size,
+                  int split_k, int rho, int32_t* workspace, float* partial, void* out_q, void* out_k, void* out_v,
+                  int device, void* stream) {
+    (void)workspace;
+    return qkv_common(x, dtype, M, K, wq, sq, zq, bq, nq, wk, sk, zk, bk, nk, wv, sv, zv, bv, nv, rope_cos, rope_sin,
+                      head_dim, perm_hd, bits, bits, bits, group_size, split_k, rho, partial, out_q, out_k, out_v,
+                      device, stream);
+}
+
+int cbk_fused_qkv_mixed(const void* x, int dtype, int64_t M, int64_t K, const int32_t* wq, const void* sq,
+                        const void* zq, const void* bq, int64_t nq, const int32_t* wk, const void* sk, const void* zk,
+                        const void* bk, int64_t nk, const int32_t* wv, const void* sv, const void* zv, const void* bv,
+                        int64_t nv, const float* rope_cos, const float* rope_sin, int head_dim, int perm_hd,
+                        int bits_q, int bits_k, int bits_v, int group_size, int split_k, int rho, int32_t* workspace,
+                        float* partial, void* out_q, void* out_k, void* out_v, int device, void* stream) {
+    (void)workspace;
+    return qkv_common(x, dtype, M, K, wq, sq, zq, bq, nq, wk, sk, zk, bk, nk, wv, sv, zv, bv, nv, rope_cos, rope_sin,
+                      head_dim, perm_hd, bits_q, bits_k, bits_v, group_size, split_k, rho, partial, out_q, out_k,
+                      out_v, device, stream);
+}
+
+int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K, const int32_t* packed, const void* scales,
+                    const void* zeros, const void* bias, int64_t N, int bits, int group_size, int act,
+                    int use_matrix_cores, void* out, int device, void* stream) {
+    int rc = check_x(x, dtype, M, K);
+    if (rc) return rc;
+    if ((rc = check_weight(packed, scales, zeros, N, bits, group_size, "packed_gemm"))) return rc;
+    if (act < 0 || act > 2) return fail(CBK_EINVAL, "act must be 0 (none), 1 (relu) or 2 (silu)");
+    if (!out) return fail(CBK_EINVAL, "packed_gemm: out must be non-null");
+    if (M == 0) return CBK_OK;
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    GemmArgs A{};
+    A.x = x;
+    A.w = reinterpret_cast<const uint32_t*>(packed);
+    A.s = scales;
+    A.z = zeros;
+    A.b = bias;
+    A.out = out;
+    A.M = (int)M;
+    A.N = (int)N;
+    A.K = (int)K;
+    A.C = (int)ceil_div(K, 32);
+    A.G = (int)ceil_div(K, group_size);
+    A.gs = group_size;
+    A.wpr = (int)(A.C * bits);
+    A.bits = bits;
+    A.act = act;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const bool mc = use_matrix_cores && (dtype == CBK_F16 || dtype == CBK_BF16);
+    const hipError_t e = mc ? launch_gemm_mfma(A, dtype, s) : launch_gemm_valu(A, dtype, s);
+    if (e != hipSuccess) return hip_fail(e, "packed_gemm: launch");
+    return CBK_OK;
+}
+
+int cbk_unpack_codes(const int32_t* packed, int64_t N, int64_t K, int bits, int32_t* codes, int device,
+                     void* stream) {
+    if (!packed || !codes) return fail(CBK_EINVAL, "unpack_codes: pointers must be non-null");
+    if (bits != 2 && bits != 3 && bits != 4) return fail(CBK_EINVAL, "unpack_codes: bits must be 2/3/4");
+    if (N < 0 || K <= 0 || N > (1 << 30) || K > (1 << 24)) return fail(CBK_EINVAL, "unpack_codes: bad shape");
+    if (N == 0) return CBK_OK;
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    const hipError_t e = launch_unpack(reinterpret_cast<const uint32_t*>(packed), (int)N, (int)K, bits, codes,
+                                       reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "unpack_codes: launch");
+    return CBK_OK;
+}
+
+}  // extern "C"

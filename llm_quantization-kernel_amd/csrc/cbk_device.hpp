@@ -1,0 +1,174 @@
+// cbk_device.hpp -- device helpers shared by the gfx950 packed-linear kernels.
+//
+// Covers the reference's device helpers (Kernel/csrc/common.cuh:10-70 and
+// bitpack.cuh:10-46) re-designed for CDNA4: storage-type conversion, epilogue
+// activations, the virtual-row map of the fused modes, RoPE un-permutation, and
+// scalar code extraction for the VALU kernels.  The packed-fp16 MFMA decode lives
+// in cbk_decode.hpp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cbk {
+
+enum { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+enum { ACT_NONE = 0, ACT_RELU = 1, ACT_SILU = 2 };
+enum { MODE_GEMV = 0, MODE_QKV = 1, MODE_GATEUP = 2 };
+
+// ---------------------------------------------------------------- storage types
+template <int DT> struct Dt;
+
+template <> struct Dt<DT_F16> {
+    using S = _Float16;
+    static __device__ __forceinline__ float to_f(S v) { return (float)v; }
+    static __device__ __forceinline__ S from_f(float f) { return (S)f; }      // v_cvt_f16_f32, RNE
+};
+
+template <> struct Dt<DT_BF16> {
+    using S = uint16_t;
+    static __device__ __forceinline__ float to_f(S v) { return __uint_as_float((uint32_t)v << 16); }
+    static __device__ __forceinline__ S from_f(float f) {                     // RNE, quiet NaN
+        uint32_t u = __float_as_uint(f);
+        if ((u & 0x7fffffffu) > 0x7f800000u) return (S)((u >> 16) | 0x40u);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        return (S)(u >> 16);
+    }
+};
+
+template <> struct Dt<DT_F32> {
+    using S = float;
+    static __device__ __forceinline__ float to_f(S v) { return v; }
+    static __device__ __forceinline__ S from_f(float f) { return f; }
+};
+
+template <int DT>
+__device__ __forceinline__ float load_f(const void* p, long i) {
+    return Dt<DT>::to_f(reinterpret_cast<const typename Dt<DT>::S*>(p)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void store_f(void* p, long i, float v) {
+    reinterpret_cast<typename Dt<DT>::S*>(p)[i] = Dt<DT>::from_f(v);
+}
+
+// ---------------------------------------------------------------- epilogue math
+// SiLU uses the device exp (v_exp_f32 path); checked against float64 SiLU in the tests.
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+    if (act == ACT_RELU) return v > 0.f ? v : 0.f;
+    if (act == ACT_SILU) return silu(v);
+    return v;
+}
+
+// Stored (pair-interleaved) row r of a head -> original row (the inverse of
+// ops.rope_row_order; same map as common.cuh:66-70).
+__device__ __forceinline__ int rope_unperm(int r, int hd) {
+    if (hd <= 0) return r;
+    const int head = r / hd, p = r - head * hd;
+    return head * hd + ((p & 1) ? (p >> 1) + (hd >> 1) : (p >> 1));
+}
+
+// ---------------------------------------------------------------- decode-call arguments
+struct Proj {
+    const uint32_t* w;   // packed [n, wpr]
+    const void* s;       // scales [n, G]
+    const void* z;       // zeros  [n, G]
+    const void* b;       // bias [n] or nullptr
+    void* out;           // [M, n]
+    int n;               // rows
+    int bits;            // 2 / 3 / 4
+    int wpr;             // words per row = C * bits
+    int pad_;
+};
+
+struct GemvArgs {
+    Proj p[3];
+    const void* x;         // [M, K]
+    float* partial;        // [P, M, V] fp32 when P > 1
+    const float* rope_cos; // [M, head_dim] or nullptr
+    const float* rope_sin;
+    int M, K, V;           // batch rows, in_features, virtual rows
+    int C, G, gs;          // 32-code chunks per row, groups per row, group size
+    int P, act;            // K splits, activation (GEMV mode)
+    int head_dim, perm_hd;
+    int ntiles, mtiles, jobs;
+    int nw;                // waves per workgroup (MFMA kernel)
+    int units;             // 128-code units per row (MFMA kernel)
+    int xs_bytes;          // LDS bytes of the staged activation (MFMA kernel)
+    int red_off;           // LDS offset of the chunk-sum / cross-wave reduction area
+    int lds_bytes;         // dynamic LDS bytes per workgroup
+};
+
+// Projection field select without dynamic indexing of the kernel-argument struct.
+#define CBK_SEL(A, proj, field) \
+    ((proj) == 0 ? (A).p[0].field : ((proj) == 1 ? (A).p[1].field : (A).p[2].field))
+
+// Virtual row v -> (projection, local row): QKV concatenates [q; k; v], gate-up
+// interleaves gate row n -> 2n and up row n -> 2n+1 (packed_gemv.cu:33-42).
+template <int MODE>
+__device__ __forceinline__ void vmap(const GemvArgs& A, int v, int& proj, int& r) {
+    if constexpr (MODE == MODE_GATEUP) {
+        proj = v & 1; r = v >> 1;
+    } else if constexpr (MODE == MODE_QKV) {
+        const int n0 = A.p[0].n, n1 = A.p[1].n;
+        if (v < n0) { proj = 0; r = v; }
+        else if (v < n0 + n1) { proj = 1; r = v - n0; }
+        else { proj = 2; r = v - n0 - n1; }
+    } else {
+        proj = 0; r = v;
+    }
+}
+
+// Final value of virtual row v for batch row b.  `partner` is the fp32 sum of row
+// v ^ 1 (the up row of a gate row; the RoPE partner of a Q/K row), before bias.
+template <int DT, int MODE>
+__device__ __forceinline__ void epilogue(const GemvArgs& A, int b, int v, float mine, float partner) {
+    int proj, r;
+    vmap<MODE>(A, v, proj, r);
+    if constexpr (MODE == MODE_GEMV) {
+        const float bias = A.p[0].b ? load_f<DT>(A.p[0].b, r) : 0.f;
+        store_f<DT>(A.p[0].out, (long)b * A.p[0].n + r, apply_act(mine + bias, A.act));
+    } else if constexpr (MODE == MODE_GATEUP) {
+        if (proj != 0) return;
+        store_f<DT>(A.p[0].out, (long)b * A.p[0].n + r, silu(mine) * partner);
+    } else {
+        const void* bias = CBK_SEL(A, proj, b);
+        void* out = CBK_SEL(A, proj, out);
+        const int n = CBK_SEL(A, proj, n);
+        float y = mine + (bias ? load_f<DT>(bias, r) : 0.f);
+        const int hd = proj < 2 ? A.perm_hd : 0;
+        const int orig = rope_unperm(r, hd);
+        if (A.rope_cos != nullptr && proj < 2) {
+            const float yp = partner + (bias ? load_f<DT>(bias, r ^ 1) : 0.f);
+            const int d = orig % A.head_dim;
+            const float c = A.rope_cos[(long)b * A.head_dim + d];
+            const float s = A.rope_sin[(long)b * A.head_dim + d];
+            y = (d < (A.head_dim >> 1)) ? (y * c - yp * s) : (y * c + yp * s);
+        }
+        store_f<DT>(out, (long)b * n + orig, y);
+    }
+}
+
+// ---------------------------------------------------------------- scalar code access
+// Code j (0..31) of a chunk held in BITS registers (straddling codes of W3 are
+// joined with a 64-bit funnel shift).
+template <int BITS>
+__device__ __forceinline__ uint32_t chunk_code(const uint32_t (&w)[BITS], int j) {
+    const int pos = j * BITS, wi = pos >> 5, off = pos & 31;
+    uint32_t v = w[wi] >> off;
+    if (off + BITS > 32) v |= w[wi + 1] << (32 - off);
+    return v & ((1u << BITS) - 1u);
+}
+
+// Random-access code k of one packed row (bitpack.cuh:10-18 semantics).
+__device__ __forceinline__ uint32_t row_code(const uint32_t* row, long k, int bits) {
+    const long pos = k * bits;
+    const long wi = pos >> 5;
+    const int off = (int)(pos & 31);
+    uint32_t v = row[wi] >> off;
+    if (off + bits > 32) v |= row[wi + 1] << (32 - off);
+    return v & ((1u << bits) - 1u);
+}
+
+}  // namespace cbk

@@ -1,0 +1,39 @@
+// cbk_kernels.hpp -- launchers exported by the kernel translation units to abi.cpp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include "cbk_device.hpp"
+
+namespace cbk {
+
+// gemv_mfma.hip: fp16, group size % 128 == 0.  Kernel address for the attribute
+// queries and the launch; max_batch <= 1 selects the single-row epilogue.
+const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);
+
+// gemv_generic.hip: any dtype / group size; 32 virtual rows x 1 batch row per job.
+constexpr int GENERIC_THREADS = 256;
+constexpr int GENERIC_ROWS = 32;
+hipError_t launch_gemv_generic(const GemvArgs& A, int dt, int mode, int grid, hipStream_t stream);
+const void* gemv_generic_kernel_for(int dt, int mode);
+
+// gemv_generic.hip: split-K combine + epilogue (P > 1).
+hipError_t launch_gemv_reduce(const GemvArgs& A, int dt, int mode, hipStream_t stream);
+
+struct GemmArgs {
+    const void* x;          // [M, K]
+    const uint32_t* w;      // packed [N, wpr]
+    const void* s;          // scales [N, G]
+    const void* z;          // zeros [N, G]
+    const void* b;          // bias [N] or nullptr
+    void* out;              // [M, N]
+    int M, N, K, C, G, gs, wpr, bits, act;
+};
+
+// gemm.hip
+hipError_t launch_gemm_mfma(const GemmArgs& A, int dt, hipStream_t stream);
+hipError_t launch_gemm_valu(const GemmArgs& A, int dt, hipStream_t stream);
+
+// unpack.hip
+hipError_t launch_unpack(const uint32_t* packed, int N, int K, int bits, int32_t* codes, hipStream_t stream);
+
+}  // namespace cbk

@@ -1,0 +1,124 @@
+"""numpy restatement of the reference quantizer / packer -- TEST INFRASTRUCTURE ONLY.
+
+Follows /root/reference/Crispybits/Kernel/crispybits_kernels/reference.py.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline use this.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+__all__ = ["quantize_affine", "dequantize", "pack_codes", "unpack_codes", "pack_linear_dict",
+           "dequantized_weight", "chunk_code", "code_to_float", "words_per_row"]
+
+
+def words_per_row(K: int, bits: int) -> int:
+    """ceil(K/32) * bits int32 words per row (reference.py:41,53; host_utils.h:63-64)."""
+    return math.ceil(K / 32) * bits
+
+
+def quantize_affine(w: np.ndarray, bits: int, group_size: int = 128):
+    """Group-wise asymmetric min/max quantization (reference.py:10-27).
+
+    All arithmetic in IEEE fp32, round-half-to-even (``np.rint`` == ``torch.round``).
+    K is padded up to a multiple of ``group_size`` by repeating the last column
+    (reference.py:18-19).  Returns (q int32 [N,K], scale fp32 [N,G], zero fp32 [N,G]).
+    """
+    assert bits in (2, 3, 4)
+    w = np.asarray(w, dtype=np.float32)
+    N, K = w.shape
+    G = math.ceil(K / group_size)
+    Kp = G * group_size
+    wf = np.zeros((N, Kp), dtype=np.float32)
+    wf[:, :K] = w
+    if Kp != K:
+        wf[:, K:] = wf[:, K - 1:K]
+    g = wf.reshape(N, G, group_size)
+    qmax = np.float32((1 << bits) - 1)
+    mn = g.min(-1)
+    mx = g.max(-1)
+    scale = np.maximum((mx - mn) / qmax, np.float32(1e-8)).astype(np.float32)
+    zero = np.clip(np.rint(-mn / scale), 0, qmax).astype(np.float32)
+    q = np.clip(np.rint(g / scale[..., None]) + zero[..., None], 0, qmax)
+    q = q.reshape(N, Kp)[:, :K].astype(np.int32)
+    return q, scale, zero
+
+
+def dequantize(q: np.ndarray, scales: np.ndarray, zeros: np.ndarray, group_size: int) -> np.ndarray:
+    """(q - z) * s in fp32 with the per-group metadata repeated along K (reference.py:30-34)."""
+    K = q.shape[1]
+    s = np.repeat(np.asarray(scales, dtype=np.float32), group_size, axis=1)[:, :K]
+    z = np.repeat(np.asarray(zeros, dtype=np.float32), group_size, axis=1)[:, :K]
+    return ((q.astype(np.float32) - z) * s).astype(np.float32)
+
+
+def pack_codes(q: np.ndarray, bits: int) -> np.ndarray:
+    """LSB-first bitstream per row, rows padded to 32-code chunks (reference.py:37-55).
+
+    Code k of a row occupies bits [k*bits, (k+1)*bits) of the row's bitstream; each
+    32-code chunk takes exactly ``bits`` words, so chunks start on word boundaries.
+    Returned as int32 (two's complement view of the uint32 words).
+    """
+    assert bits in (2, 3, 4)
+    q = np.asarray(q)
+    N, K = q.shape
+    C = math.ceil(K / 32)
+    qq = np.zeros((N, C * 32), dtype=np.uint64)
+    qq[:, :K] = q.astype(np.uint64) & np.uint64((1 << bits) - 1)
+    qq = qq.reshape(N, C, 32)
+    words = np.zeros((N, C, bits + 1), dtype=np.uint64)
+    for j in range(32):
+        pos = j * bits
+        wi, off = pos // 32, pos % 32
+        v = qq[:, :, j] << np.uint64(off)
+        words[:, :, wi] |= v & np.uint64(0xFFFFFFFF)
+        words[:, :, wi + 1] |= v >> np.uint64(32)
+    assert not words[:, :, bits].any()
+    w = words[:, :, :bits].reshape(N, C * bits).astype(np.uint32)
+    return w.view(np.int32).copy()
+
+
+def unpack_codes(packed: np.ndarray, bits: int, K: int) -> np.ndarray:
+    """Random-access inverse of pack_codes (reference.py:58-67): int32 [N, K]."""
+    w = np.asarray(packed).astype(np.int64) & 0xFFFFFFFF
+    k = np.arange(K)
+    pos = k * bits
+    wi, off = pos // 32, pos % 32
+    lo = w[:, wi] >> off
+    nxt = np.minimum(wi + 1, w.shape[1] - 1)
+    hi = np.where(off + bits > 32, w[:, nxt] << (32 - off), 0)
+    return ((lo | hi) & ((1 << bits) - 1)).astype(np.int32)
+
+
+def chunk_code(words, j: int, bits: int) -> int:
+    """Code j of one 32-code chunk held in ``bits`` words (bitpack.cuh:35-41 semantics)."""
+    pos = j * bits
+    wi, off = pos >> 5, pos & 31
+    v = (int(words[wi]) & 0xFFFFFFFF) >> off
+    if off + bits > 32:
+        v |= (int(words[wi + 1]) & 0xFFFFFFFF) << (32 - off)
+    return v & ((1 << bits) - 1)
+
+
+def code_to_float(q: int) -> float:
+    """u32 -> fp32 via the 2^23 magic constant (bitpack.cuh:44-46)."""
+    f = np.array([q | 0x4B000000], dtype=np.uint32).view(np.float32)[0]
+    return float(f - np.float32(8388608.0))
+
+
+def pack_linear_dict(weight: np.ndarray, bits: int, group_size: int = 128, bias=None,
+                     meta_dtype=np.float16) -> dict:
+    """Quantize + pack one linear, metadata cast to ``meta_dtype`` (reference.py:70-76)."""
+    q, s, z = quantize_affine(weight, bits, group_size)
+    return dict(packed=pack_codes(q, bits), scales=s.astype(meta_dtype), zeros=z.astype(meta_dtype),
+                bits=bits, group_size=group_size, in_features=weight.shape[1],
+                out_features=weight.shape[0],
+                bias=None if bias is None else np.asarray(bias).astype(meta_dtype))
+
+
+def dequantized_weight(d: dict) -> np.ndarray:
+    """fp32 W-hat of a packed dict (reference.py:79-82)."""
+    q = unpack_codes(d["packed"], d["bits"], d["in_features"])
+    return dequantize(q, np.asarray(d["scales"], np.float32), np.asarray(d["zeros"], np.float32),
+                      d["group_size"])

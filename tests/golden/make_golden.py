@@ -1,0 +1,79 @@
+"""Writes the small golden fixtures under tests/golden/ (run from the repo root:
+``python tests/golden/make_golden.py``).
+
+The expected values come from ``oracle.bruteforce`` -- pure-Python bitstream
+and scalar-fp32 restatements of the reference's closed forms
+(Kernel/crispybits_kernels/reference.py:10-67) -- so the vectorised numpy
+oracle and the HIP kernels are both checked against an independent derivation.
+Floats are stored as the hex of their IEEE fp32 bit pattern so the fixtures
+are exact.
+"""
+from __future__ import annotations
+
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from oracle import bruteforce  # noqa: E402
+
+
+def f32hex(v) -> str:
+    return "%08x" % int(np.array([v], dtype=np.float32).view(np.uint32)[0])
+
+
+def packing_cases():
+    rng = np.random.default_rng(1234)
+    cases = []
+    for bits in (2, 3, 4):
+        for K in (32, 45, 96, 200):
+            q = rng.integers(0, 1 << bits, size=(3, K))
+            cases.append(dict(bits=bits, K=K, codes=q.tolist(),
+                              words=[bruteforce.pack_row(r, bits) for r in q]))
+    # structured rows: all-max codes, a single straddling code, ascending codes
+    for bits in (2, 3, 4):
+        qmax = (1 << bits) - 1
+        rows = [[qmax] * 64, [0] * 64, [k % (qmax + 1) for k in range(64)]]
+        if bits == 3:
+            rows[1][10] = 0b101    # straddles words 0|1 of chunk 0
+            rows[1][21] = 0b110    # straddles words 1|2 of chunk 0
+            rows[1][42] = 0b011    # code 10 of chunk 1
+        cases.append(dict(bits=bits, K=64, codes=rows, words=[bruteforce.pack_row(r, bits) for r in rows]))
+    return cases
+
+
+def quant_cases():
+    rng = np.random.default_rng(99)
+    cases = []
+    for bits in (2, 3, 4):
+        for K, gs in ((64, 32), (96, 64), (200, 128), (256, 128)):
+            w = (rng.standard_normal((2, K)) * 0.02).astype(np.float32)
+            rows = []
+            for r in w:
+                q, s, z = bruteforce.quantize_row(r.tolist(), bits, gs)
+                rows.append(dict(q=q, scale=[f32hex(v) for v in s], zero=[f32hex(v) for v in z]))
+            cases.append(dict(bits=bits, K=K, group_size=gs, w=[[f32hex(v) for v in r] for r in w], rows=rows))
+    # constant group (scale clamps to 1e-8) and a group that does not span zero
+    for bits in (2, 3, 4):
+        w = np.stack([np.full(128, 0.37, np.float32), np.linspace(1.0, 2.0, 128, dtype=np.float32)])
+        rows = []
+        for r in w:
+            q, s, z = bruteforce.quantize_row(r.tolist(), bits, 128)
+            rows.append(dict(q=q, scale=[f32hex(v) for v in s], zero=[f32hex(v) for v in z]))
+        cases.append(dict(bits=bits, K=128, group_size=128, w=[[f32hex(v) for v in r] for r in w], rows=rows))
+    return cases
+
+
+def main():
+    with open(os.path.join(HERE, "packing.json"), "w") as f:
+        json.dump(packing_cases(), f, separators=(",", ":"))
+    with open(os.path.join(HERE, "quantize.json"), "w") as f:
+        json.dump(quant_cases(), f, separators=(",", ":"))
+
+
+if __name__ == "__main__":
+    main()

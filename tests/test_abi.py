@@ -1,0 +1,102 @@
+"""The C-ABI library loads and exports every entry point include/crispybits_hip.h
+declares, and rejects invalid arguments before touching a device (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "crispybits_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cbk_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared()
+    for n in ("cbk_packed_gemv", "cbk_packed_gemm", "cbk_fused_gate_up", "cbk_fused_qkv", "cbk_sm_count",
+              "cbk_tile_n", "cbk_max_rho", "cbk_unpack_codes"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from crispybits_kernels import _C
+    lib = ctypes.CDLL(_C.LIB_PATH)
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert set(_declared()) == set(_C.EXPORTS)
+    assert _C.ABI_VERSION == 1
+    assert _C.tile_n() == 16
+
+
+def _lib():
+    from crispybits_kernels import _C
+    return _C._lib
+
+
+def _err():
+    return _lib().cbk_last_error().decode()
+
+
+ALIGNED = 1 << 20          # a fake, 16-byte aligned "device" address: never dereferenced
+
+
+def _gemv(**kw):
+    a = dict(x=ALIGNED, dtype=0, M=1, K=256, packed=ALIGNED, scales=ALIGNED, zeros=ALIGNED, bias=None, N=64, bits=4,
+             gs=128, split_k=1, rho=1, act=0, ws=None, partial=None, out=ALIGNED, device=0, stream=None)
+    a.update(kw)
+    return _lib().cbk_packed_gemv(*a.values())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(bits=5), "bits must be 2/3/4"),
+    (dict(gs=48), "group_size must be a positive multiple of 32"),
+    (dict(gs=0), "group_size must be a positive multiple of 32"),
+    (dict(dtype=7), "x must be fp16/bf16/fp32"),
+    (dict(split_k=0), "split_k must be >= 1"),
+    (dict(act=3), "act must be 0 (none), 1 (relu) or 2 (silu)"),
+    (dict(packed=ALIGNED + 4), "16-byte aligned"),
+    (dict(bits=2, packed=ALIGNED + 4), "8-byte aligned"),
+    (dict(K=0), "in_features"),
+    (dict(out=None), "out must be non-null"),
+    (dict(scales=None), "non-null"),
+])
+def test_gemv_argument_errors(kw, msg):
+    assert _gemv(**kw) == 1
+    assert msg in _err()
+
+
+def test_w3_only_needs_word_alignment_and_empty_batch_is_a_no_op():
+    assert _gemv(bits=3, packed=ALIGNED + 4, M=0) == 0       # validated, nothing launched
+
+
+def test_gemm_and_unpack_argument_errors():
+    lib = _lib()
+    assert lib.cbk_packed_gemm(ALIGNED, 0, 4, 256, ALIGNED, ALIGNED, ALIGNED, None, 64, 4, 100, 0, 1, ALIGNED, 0,
+                               None) == 1
+    assert "group_size" in _err()
+    assert lib.cbk_unpack_codes(ALIGNED, 4, 64, 1, ALIGNED, 0, None) == 1
+    assert "bits" in _err()
+
+
+def test_fused_qkv_rope_checks():
+    lib = _lib()
+    args = [ALIGNED, 0, 1, 256] + [ALIGNED, ALIGNED, ALIGNED, None, 256] * 3
+    # RoPE tables without pair-interleaved Q/K
+    rc = lib.cbk_fused_qkv(*args, ALIGNED, ALIGNED, 128, 0, 4, 128, 1, 1, None, None, ALIGNED, ALIGNED, ALIGNED,
+                           0, None)
+    assert rc == 1 and "pair-interleaved" in _err()
+    rc = lib.cbk_fused_qkv(*args, None, None, 0, 6, 4, 128, 1, 1, None, None, ALIGNED, ALIGNED, ALIGNED, 0, None)
+    assert rc == 1 and "multiples of head_dim" in _err()
+
+
+def test_partial_query():
+    lib = _lib()
+    assert lib.cbk_gemv_partial_floats(0, 1, 4096, 4096, 128, 1) == 0
+    assert lib.cbk_gemv_partial_floats(0, 2, 4096, 4096, 128, 4) == 4 * 2 * 4096
+    # fp16 batch 16 x K 16384 needs more LDS than one workgroup holds -> forced split
+    assert lib.cbk_gemv_partial_floats(0, 16, 64, 16384, 128, 1) > 0

@@ -1,0 +1,234 @@
+"""Host logic of crispybits_kernels (ops / io / autotune / integration) on the CPU,
+with the oracle injected as the backend (the ``emu`` fixture).  Mirrors the
+reference's emulator-parametrised tests (Kernel/tests/test_correctness.py,
+test_integration.py); the GPU parity tests run the same API on the HIP kernels."""
+import copy
+
+import pytest
+import torch
+
+from crispybits_kernels import (apply_rope_reference, candidate_split_k, fused_gate_up, fused_qkv, new_workspace,
+                                packed_linear, permute_for_rope, sm_count, tile_n, ops)
+from crispybits_kernels.io import from_packed_dict
+from crispybits_kernels.reference import dequantized_weight, pack_linear_dict
+
+TOL = {torch.float16: 3e-3, torch.bfloat16: 2e-2, torch.float32: 1e-4}
+
+
+def make(n, k, bits, dtype, device, bias=False, seed=0, gs=128):
+    g = torch.Generator().manual_seed(seed)
+    W = torch.randn(n, k, generator=g) * 0.05
+    b = torch.randn(n, generator=g) * 0.1 if bias else None
+    d = pack_linear_dict(W, bits, gs, b, dtype)
+    return from_packed_dict(d, device, dtype), dequantized_weight(d).to(device), (
+        None if b is None else d["bias"].float().to(device))
+
+
+def ref_linear(x, Wd, bd, act=None):
+    y = x.float() @ Wd.T
+    if bd is not None:
+        y = y + bd
+    if act == "relu":
+        y = torch.relu(y)
+    elif act == "silu":
+        y = torch.nn.functional.silu(y)
+    return y
+
+
+def close(y, ref, dtype):
+    err = (y.float() - ref).abs().max().item()
+    scale = ref.abs().max().item() + 1e-6
+    assert err / scale < TOL[dtype], f"rel err {err / scale:.2e}"
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 20])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_packed_linear_routes_and_reshapes(emu, M, bits):
+    w, Wd, bd = make(48, 200, bits, torch.float32, emu, bias=True)
+    x = torch.randn(M, 200)
+    y = packed_linear(x, w, act="relu")
+    close(y, ref_linear(x, Wd, bd, "relu"), torch.float32)
+    x3 = torch.randn(2, M, 200)
+    assert packed_linear(x3, w).shape == (2, M, 48)
+
+
+def test_decode_threshold_boundary(emu, monkeypatch):
+    w, Wd, _ = make(32, 128, 4, torch.float32, emu)
+    calls = []
+    for name in ("packed_gemv", "packed_gemm"):
+        fn = getattr(ops._C, name)
+        monkeypatch.setattr(ops._C, name, lambda *a, _fn=fn, _n=name: (calls.append(_n), _fn(*a))[1])
+    packed_linear(torch.randn(ops.DECODE_THRESHOLD, 128), w)
+    packed_linear(torch.randn(ops.DECODE_THRESHOLD + 1, 128), w)
+    assert calls == ["packed_gemv", "packed_gemm"]
+
+
+def test_fused_gate_up_decode_and_prefill(emu):
+    g, Gd, _ = make(96, 256, 3, torch.float32, emu, seed=1)
+    u, Ud, _ = make(96, 256, 3, torch.float32, emu, seed=2)
+    for M in (1, 12):
+        x = torch.randn(M, 256)
+        ref = torch.nn.functional.silu(x @ Gd.T) * (x @ Ud.T)
+        close(fused_gate_up(x, g, u, 2, 1), ref, torch.float32)
+    g2, _, _ = make(96, 256, 2, torch.float32, emu)
+    with pytest.raises(ValueError):
+        fused_gate_up(torch.randn(1, 256), g2, u)
+
+
+def _rope_tables(M, head_dim, device):
+    pos = torch.randint(0, 2048, (M,)).float()
+    inv = 1.0 / (10000 ** (torch.arange(0, head_dim, 2).float() / head_dim))
+    f = pos[:, None] * inv[None]
+    emb = torch.cat([f, f], -1)
+    return emb.cos().to(device), emb.sin().to(device)
+
+
+@pytest.mark.parametrize("M", [1, 3, 12])
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("bits", [(3, 3, 3), (4, 2, 3)])
+def test_fused_qkv_gqa(emu, M, rope, bits):
+    K, nq, nkv, hd = 256, 4, 2, 64
+    q, Qd, qb = make(nq * hd, K, bits[0], torch.float32, emu, True, 1)
+    k, Kd, kb = make(nkv * hd, K, bits[1], torch.float32, emu, True, 2)
+    v, Vd, vb = make(nkv * hd, K, bits[2], torch.float32, emu, False, 3)
+    q, k = permute_for_rope(q, hd), permute_for_rope(k, hd)
+    x = torch.randn(M, K)
+    rq, rk, rv = ref_linear(x, Qd, qb), ref_linear(x, Kd, kb), ref_linear(x, Vd, vb)
+    r = None
+    if rope:
+        cos, sin = _rope_tables(M, hd, emu)
+        rq, rk = apply_rope_reference(rq, cos, sin, hd), apply_rope_reference(rk, cos, sin, hd)
+        r = (cos, sin, hd)
+    oq, ok, ov = fused_qkv(x, q, k, v, 2, 1, rope=r)
+    close(oq, rq, torch.float32); close(ok, rk, torch.float32); close(ov, rv, torch.float32)
+
+
+def test_rope_requires_permuted_weights(emu):
+    q, _, _ = make(256, 256, 3, torch.float32, emu)
+    x = torch.randn(1, 256)
+    cos, sin = _rope_tables(1, 128, emu)
+    with pytest.raises(ValueError):
+        fused_qkv(x, q, q, q, rope=(cos, sin, 128))
+    with pytest.raises(ValueError):
+        packed_linear(x, permute_for_rope(q, 128))
+    with pytest.raises(ValueError):
+        permute_for_rope(permute_for_rope(q, 128), 64)
+
+
+def test_policy_rule(emu):
+    S, bn = sm_count(), tile_n()
+    assert candidate_split_k(1, bn * 4, bn, S, 1) == max(1, -(-S // 4))
+    assert candidate_split_k(64, 4096, bn, S, 1) == 1
+    assert candidate_split_k(1, 10 ** 6, bn, S, 1) == 1
+    assert candidate_split_k(1, bn, bn, S, 2, max_split=8) == 8
+    # _resolve clamps to the chunk count and counts batch tiles of 16 rows
+    dev = torch.device("cpu")
+    assert ops._resolve(None, 1, 1, 64, 64, dev) == 2           # rule wants 64, K has 2 chunks
+    assert ops._resolve(5, 1, 1, 64, 4096, dev) == 5
+    assert ops._resolve(None, 1, 16, 4096, 4096, dev) == ops._resolve(None, 1, 1, 4096, 4096, dev)
+
+
+def test_workspace_contract(emu):
+    w, Wd, _ = make(512, 256, 3, torch.float32, emu)
+    ws = new_workspace(emu)
+    x = torch.randn(1, 256)
+    for pk, rho in [(1, 1), (4, 2), (1, 0), (7, 1)]:
+        close(packed_linear(x, w, pk, rho, workspace=ws), ref_linear(x, Wd, None), torch.float32)
+    assert ws.tolist() == [0, 0]
+    ws[0] = 3
+    with pytest.raises(AssertionError):
+        packed_linear(x, w, 1, 1, workspace=ws)
+
+
+def test_set_backend_names():
+    with pytest.raises(ValueError):
+        ops.set_backend("nonsense")
+    with pytest.raises(RuntimeError):
+        ops.set_backend("emulator")
+
+
+def test_autotune_report_on_emulator(emu):
+    from crispybits_kernels import tune_gemv
+    w, _, _ = make(64, 256, 4, torch.float32, emu)
+    rep = tune_gemv(torch.randn(1, 256), w, warmup=0, iters=1, exhaustive=True)
+    assert rep.best in rep.results and rep.oracle in rep.results
+    assert rep.regret >= 0
+    assert all(1 <= r.split_k <= 8 for r in rep.results)
+
+
+# ---------------------------------------------------------------- HF integration (tiny models)
+
+transformers = pytest.importorskip("transformers")
+
+from crispybits_kernels import FusedLlamaMLP, FusedQKV, install_bitmap, tune_model  # noqa: E402
+from crispybits_kernels.integration import _blocks  # noqa: E402
+from crispybits_kernels.reference import write_packed_dir  # noqa: E402
+
+
+def _dequantize_model_(model, bitmap):
+    for block, bits in zip(_blocks(model), bitmap):
+        for _, m in block.named_modules():
+            if isinstance(m, torch.nn.Linear):
+                d = pack_linear_dict(m.weight.detach().float().cpu(), bits, 128, None, torch.float16)
+                m.weight.data.copy_(dequantized_weight(d).to(m.weight))
+
+
+def _tiny(kind):
+    if kind == "llama":
+        cfg = transformers.LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=3,
+                                       num_attention_heads=4, num_key_value_heads=2, vocab_size=512)
+        m = transformers.LlamaForCausalLM(cfg)
+        with torch.no_grad():
+            for blk in _blocks(m):
+                blk.self_attn.q_proj.weight.mul_(8.0)
+                blk.self_attn.k_proj.weight.mul_(8.0)
+        return m
+    cfg = transformers.OPTConfig(hidden_size=256, ffn_dim=512, num_hidden_layers=3, num_attention_heads=4,
+                                 vocab_size=512, word_embed_proj_dim=256)
+    return transformers.OPTForCausalLM(cfg)
+
+
+@pytest.mark.parametrize("kind,fuse,fuse_rope", [("llama", False, False), ("llama", True, False),
+                                                 ("llama", True, True), ("opt", True, True)])
+def test_model_matches_dequantized(emu, tmp_path, kind, fuse, fuse_rope):
+    torch.manual_seed(0)
+    dtype = torch.float32
+    base = _tiny(kind).to(dtype).eval()
+    bitmap = [4, 2, 3]
+    write_packed_dir(base, tmp_path, bits_options=(2, 3, 4), dtype=dtype)
+    ref = copy.deepcopy(base)
+    _dequantize_model_(ref, bitmap)
+    model = install_bitmap(copy.deepcopy(base), tmp_path, bitmap, device="cpu", dtype=dtype, fuse=fuse,
+                           fuse_rope=fuse_rope)
+    if fuse and kind == "llama":
+        owners = [m for m in model.modules() if isinstance(m, FusedQKV)]
+        assert owners and any(isinstance(m, FusedLlamaMLP) for m in model.modules())
+        assert all(bool(o.rope_head_dim) == fuse_rope for o in owners)
+    if fuse:
+        tune_model(model, iters=1, warmup=0, dtype=dtype)
+    ids = torch.randint(0, 512, (1, 12))
+    with torch.no_grad():
+        a, b = ref(ids, use_cache=True), model(ids, use_cache=True)
+        la, lb = a.logits[:, -1], b.logits[:, -1]
+        assert (la - lb).abs().max() / la.abs().max() < 2e-2
+        pa, pb = a.past_key_values, b.past_key_values
+        for _ in range(2):
+            nxt = la.argmax(-1, keepdim=True)
+            a = ref(nxt, past_key_values=pa, use_cache=True)
+            b = model(nxt, past_key_values=pb, use_cache=True)
+            la, lb, pa, pb = a.logits[:, -1], b.logits[:, -1], a.past_key_values, b.past_key_values
+            assert (la - lb).abs().max() / la.abs().max() < 2e-2
+
+
+def test_proxy_mismatch_raises(emu):
+    from crispybits_kernels.ops import PackedLinear
+    from crispybits_kernels.integration import _QKVProxy
+    ws = [PackedLinear(from_packed_dict(pack_linear_dict(torch.randn(128, 128) * .05, 3, 128, None, torch.float32),
+                                        "cpu", torch.float32)) for _ in range(3)]
+    ws[0].permute_for_rope_(64)
+    ws[1].permute_for_rope_(64)
+    owner = FusedQKV(*ws, rope_head_dim=64)
+    x = torch.randn(1, 128)
+    owner.prime(x, torch.ones(1, 64), torch.zeros(1, 64))
+    with pytest.raises(RuntimeError):
+        _QKVProxy(owner, 0)(x.clone())
