@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+"""MI355X benchmark of the packed W2/W3/W4 linear kernels (one GPU).
+
+Timed workload (the metric's W3 decode GEMV): one step
+is one token (M = 1, fp16 activations) through the W3 decode GEMV of the three
+Llama-2-7B-like shapes (K, N) = (4096, 4096), (4096, 11008), (11008, 4096),
+group size 128, for 32 layers with distinct weight copies (1.29 GB of packed
+weights, so the 256 MB Infinity Cache cannot serve repeats).  The 96 launches of
+a step are captured once in a HIP graph; `value` is the whole-step throughput in
+algorithmic GB/s (wall clock over K replays, inputs resident in HBM).
+
+Also reported (outside the timed region): per-launch kernel durations from the
+library's dispatch-recorded event timer for the full decode matrix (W2/W3/W4 x
+M in {1,4,8} x the three shapes), the fused QKV / gate-up decode, the M=1024 and
+M=2048 prefill GEMM, the roofline of the dominant kernel, and the CPU oracle
+(dequant + matmul) on a bounded sample on the host cores.
+
+Algorithmic bytes of one decode launch:
+    N*ceil(K/32)*bits*4 (packed) + N*ceil(K/128)*2*2 (fp16 scales+zeros) + M*K*2 + M*N*2
+Algorithmic FLOPs of one prefill launch: 2*M*N*K.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "llm_quantization-kernel_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+MFMA_F16_PEAK_TFS = 2500.0     # MI355X dense fp16 MFMA, published
+METRIC = "W3/W4 GEMV µs & HBM GB/s (% peak); M=1024 prefill GEMM TFLOP/s (% peak)"
+SHAPES = [(4096, 4096), (4096, 11008), (11008, 4096)]          # (K, N)
+LAYERS = 32
+GS = 128
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(M, K, N, bits, gs=GS):
+    return N * math.ceil(K / 32) * bits * 4 + N * math.ceil(K / gs) * 4 + M * K * 2 + M * N * 2
+
+
+def make_weight(torch, N, K, bits, seed, device):
+    """BASELINE inputs: W = randn(N, K, seed) * 0.02, group-affine quantized and packed."""
+    from crispybits_kernels.ops import PackedLinearWeight
+    from crispybits_kernels.reference import pack_codes, quantize_affine
+    g = torch.Generator().manual_seed(seed)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(device)
+    q, s, z = quantize_affine(W, bits, GS)
+    return PackedLinearWeight(pack_codes(q, bits), s.half(), z.half(), bits, GS, K, N)
+
+
+def clone_weight(w):
+    from dataclasses import replace
+    return replace(w, packed=w.packed.clone(), scales=w.scales.clone(), zeros=w.zeros.clone())
+
+
+def randx(torch, M, K, seed, device):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(M, K, generator=g).half().to(device)
+
+
+def timed_kernels(C, fn, n_launch):
+    """Run fn() (which makes n_launch library launches) with the dispatch timer armed."""
+    C.timer_start(n_launch + 8)
+    try:
+        fn()
+    finally:
+        total, durs = C.timer_stop()
+    return total, durs
+
+
+def best_config(torch, C, ops, x, ws, candidates):
+    """Pick (split_k, rho) with the smallest summed kernel time over the layer copies."""
+    best = None
+    for sk, rho in candidates:
+        def run():
+            for w in ws:
+                ops.packed_linear(x, w, sk, rho)
+        run()
+        total, _ = timed_kernels(C, run, len(ws) * 2)
+        if best is None or total < best[0]:
+            best = (total, sk, rho)
+    return best[1], best[2]
+
+
+def cpu_baseline(torch, weights, xs):
+    """Oracle (numpy dequant + matmul, reference.py:30-34 + test_correctness.py:23-31) on the host."""
+    import numpy as np
+    from oracle import reference as R
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    host = [(w.packed.cpu().numpy(), w.scales.float().cpu().numpy(), w.zeros.float().cpu().numpy(), w.bits,
+             w.in_features, x.float().cpu().numpy()) for w, x in zip(weights, xs)]
+
+    def one_pass():
+        for packed, s, z, bits, K, x in host:
+            Wd = R.dequantize(R.unpack_codes(packed, bits, K), s, z, GS)
+            _ = x @ Wd.T
+
+    for _ in range(2):
+        one_pass()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        one_pass()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    nbytes = sum(gemv_bytes(1, w.in_features, w.out_features, w.bits) for w in weights)
+    return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
+            "ms_per_layer_set": round(t * 1e3, 2),
+            "sample": "one layer-set of the timed step (the 3 W3 GEMVs at M=1) through oracle.reference "
+                      "unpack+dequantize (numpy, 1 thread) + fp32 matmul (BLAS threads = cores); "
+                      "2 warm-up passes, median of 3"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="timed step + roofline only (no sweeps)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build targets one MI355X; --gpus {args.gpus} is not supported "
+              "(the decode path would shard by output rows, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from crispybits_kernels import ops
+    if ops._CUDA is None:
+        raise SystemExit(f"HIP library not built: {ops._IMPORT_ERROR}")
+    C = ops._CUDA
+    ops.set_backend("cuda")
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"device {torch.cuda.get_device_name(dev)}  CUs={C.sm_count()}")
+
+    # ---------------------------------------------------------------- timed workload
+    bits = 3
+    base = [make_weight(torch, N, K, bits, 0, dev) for K, N in SHAPES]
+    layers = [[clone_weight(w) for w in base] for _ in range(LAYERS)]
+    xs = [randx(torch, 1, K, 1, dev) for K, _ in SHAPES]
+    torch.cuda.synchronize()
+    pool_gb = sum(w.packed.numel() * 4 + w.scales.numel() * 4 for lw in layers for w in lw) / 1e9
+    log(f"weights: {LAYERS} layers x 3 shapes, {pool_gb:.2f} GB packed")
+
+    cand = [(1, 0), (1, 1), (1, 2), (2, 0), (None, 1)]
+    cfg = [best_config(torch, C, ops, xs[s], [lw[s] for lw in layers], cand) for s in range(3)]
+    log(f"per-shape (split_k, rho): {cfg}")
+
+    def step_eager():
+        for lw in layers:
+            for s in range(3):
+                ops.packed_linear(xs[s], lw[s], cfg[s][0], cfg[s][1])
+
+    step_eager()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step_eager()
+    torch.cuda.synchronize()
+
+    step_bytes = LAYERS * sum(gemv_bytes(1, K, N, bits) for K, N in SHAPES)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    value = step_bytes / (wall / args.steps) / 1e9
+    log(f"timed: {args.steps} steps, {ms_per_step:.4f} ms/step, {value:.1f} GB/s")
+
+    # ---------------------------------------------------------------- roofline of the dominant kernel
+    total_ms, durs = timed_kernels(C, step_eager, 3 * LAYERS)
+    per_shape = []
+    for s, (K, N) in enumerate(SHAPES):
+        d = durs[s::3]
+        us = statistics.mean(d) * 1e3
+        per_shape.append({"K": K, "N": N, "bits": bits, "M": 1, "us": round(us, 3),
+                          "GBps": round(gemv_bytes(1, K, N, bits) / (us * 1e-6) / 1e9, 1),
+                          "split_k": cfg[s][0], "rho": cfg[s][1]})
+    achieved = step_bytes / (total_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gemv_mfma_kernel<3,GEMV,1> (W3 decode GEMV, M=1)",
+                "bytes_per_launch_avg": round(step_bytes / (3 * LAYERS)),
+                "avg_launch_us": round(total_ms * 1e3 / (3 * LAYERS), 3), "per_shape": per_shape}
+    log(f"roofline: {achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of HBM peak; {per_shape}")
+
+    out = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+           "config": {"workload": "W3 decode GEMV, M=1, 32 layers x {4096x4096, 4096->11008, 11008->4096}, "
+                                  "g=128, one HIP graph per step", "bits": bits, "M": 1, "group_size": GS,
+                      "shapes_KN": SHAPES, "layers": LAYERS, "weight_pool_GB": round(pool_gb, 3)},
+           "roofline": roofline}
+
+    del graph
+    if not args.quick:
+        out["gemv_sweep"] = gemv_sweep(torch, C, ops, dev)
+        out["fused"] = fused_sweep(torch, C, ops, dev)
+        out["gemm"] = gemm_sweep(torch, C, ops, dev)
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(torch, base, xs)
+    print(json.dumps(out), flush=True)
+
+
+def gemv_sweep(torch, C, ops, dev):
+    """W2/W3/W4 x M in {1,4,8} x shapes: mean kernel us over 32 weight copies."""
+    rows = []
+    for bits in (4, 3, 2):
+        base = [make_weight(torch, N, K, bits, 0, dev) for K, N in SHAPES]
+        copies = [[clone_weight(w) for w in base] for _ in range(LAYERS)]
+        for M in (1, 4, 8):
+            for s, (K, N) in enumerate(SHAPES):
+                x = randx(torch, M, K, 1, dev)
+                ws = [c[s] for c in copies]
+                sk, rho = best_config(torch, C, ops, x, ws, [(1, 0), (1, 1), (2, 0), (None, 1)])
+                run = lambda: [ops.packed_linear(x, w, sk, rho) for w in ws]
+                run()
+                total, durs = timed_kernels(C, run, 2 * len(ws))
+                us = total * 1e3 / len(durs)
+                gbs = gemv_bytes(M, K, N, bits) / (us * 1e-6) / 1e9
+                rows.append({"bits": bits, "M": M, "K": K, "N": N, "us": round(us, 3), "GBps": round(gbs, 1),
+                             "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "split_k": sk, "rho": rho})
+                log(f"gemv W{bits} M={M} K={K} N={N}: {us:.2f} us {gbs:.0f} GB/s")
+        del copies
+        torch.cuda.empty_cache()
+    return rows
+
+
+def fused_sweep(torch, C, ops, dev):
+    import numpy as np
+    res = {}
+    qkv_bits = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 3)]
+    sets = [[make_weight(torch, 4096, 4096, b, s + 1, dev) for s, b in enumerate(qkv_bits)]]
+    sets += [[clone_weight(w) for w in sets[0]] for _ in range(15)]
+    x = randx(torch, 1, 4096, 1, dev)
+    run = lambda: [ops.fused_qkv(x, *ws) for ws in sets]
+    run()
+    total, durs = timed_kernels(C, run, 2 * len(sets))
+    us = total * 1e3 / len(durs)
+    nbytes = sum(gemv_bytes(1, 4096, 4096, b) for b in qkv_bits) - 2 * 4096 * 2
+    res["qkv"] = {"bits": qkv_bits, "K": 4096, "N": [4096] * 3, "us": round(us, 3),
+                  "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    g0 = make_weight(torch, 11008, 4096, 3, 4, dev)
+    u0 = make_weight(torch, 11008, 4096, 3, 5, dev)
+    pairs = [(g0, u0)] + [(clone_weight(g0), clone_weight(u0)) for _ in range(11)]
+    run = lambda: [ops.fused_gate_up(x, g, u) for g, u in pairs]
+    run()
+    total, durs = timed_kernels(C, run, 2 * len(pairs))
+    us = total * 1e3 / len(durs)
+    nbytes = 2 * gemv_bytes(1, 4096, 11008, 3) - 4096 * 2 - 11008 * 2
+    res["gate_up"] = {"bits": 3, "K": 4096, "N": [11008, 11008], "us": round(us, 3),
+                      "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    log(f"fused: {res}")
+    return res
+
+
+def gemm_sweep(torch, C, ops, dev):
+    rows = []
+    for M in (1024, 2048):
+        for K, N in SHAPES:
+            x = randx(torch, M, K, 1, dev)
+            for bits in (4, 3, 2):
+                ws = [make_weight(torch, N, K, bits, 0, dev)]
+                ws += [clone_weight(ws[0]) for _ in range(2)]
+                run = lambda: [ops.packed_linear(x, w) for w in ws * 2]
+                run()
+                total, durs = timed_kernels(C, run, len(ws) * 2)
+                us = total * 1e3 / len(durs)
+                tfs = 2.0 * M * N * K / (us * 1e-6) / 1e12
+                rows.append({"M": M, "K": K, "N": N, "bits": bits, "us": round(us, 2), "TFLOPs": round(tfs, 1),
+                             "pct_peak": round(100 * tfs / MFMA_F16_PEAK_TFS, 1)})
+                log(f"gemm M={M} K={K} N={N} W{bits}: {us:.1f} us {tfs:.1f} TFLOP/s")
+    return rows
+
+
+if __name__ == "__main__":
+    main()

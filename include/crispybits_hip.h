@@ -117,6 +117,16 @@ int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K,
 int cbk_unpack_codes(const int32_t* packed, int64_t N, int64_t K, int bits, int32_t* codes,
                      int device, void* stream);
 
+/* Additive measurement hook (no counterpart in the reference, which times with CUDA
+ * events around whole calls, autotune.py:37-52).  cbk_timer_start arms a per-process
+ * timer for up to `capacity` kernel launches: each launch made by this library
+ * records start/stop events inside its own dispatch (hipExtLaunchKernel), so the
+ * measured durations are kernel execution only.  cbk_timer_stop waits for those
+ * launches, writes their summed milliseconds, their count, and optionally each
+ * launch's duration, and disarms the timer.  Not for use under graph capture. */
+int cbk_timer_start(int capacity);
+int cbk_timer_stop(double* total_ms, int* launches, double* durations_ms, int max_durations);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,8 @@ _SIGS = {
                                  _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "cbk_packed_gemm": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P, _I, _P]),
     "cbk_unpack_codes": (_I, [_P, _L, _L, _I, _P, _I, _P]),
+    "cbk_timer_start": (_I, [_I]),
+    "cbk_timer_stop": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -260,3 +262,17 @@ def max_rho(bits, kind="gemv") -> int:
     v = _I()
     _raise(_lib.cbk_max_rho(_device_index(), int(bits), _KIND[kind], ctypes.byref(v)))
     return v.value
+
+
+def timer_start(capacity: int = 4096):
+    """Arm the library's per-launch kernel timer (measurement hook, see cbk_timer_start)."""
+    _raise(_lib.cbk_timer_start(int(capacity)))
+
+
+def timer_stop():
+    """Disarm the timer; returns (total_ms, per-launch durations in ms)."""
+    total, n = ctypes.c_double(), _I()
+    cap = 1 << 16
+    buf = (ctypes.c_double * cap)()
+    _raise(_lib.cbk_timer_stop(ctypes.byref(total), ctypes.byref(n), buf, cap))
+    return total.value, list(buf[:min(n.value, cap)])

@@ -5,6 +5,7 @@
 // module exports of bindings.cpp:32-40.  Every check runs before the first HIP
 // call, so invalid arguments are reported without touching a device.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <algorithm>
 #include <cstdarg>
@@ -12,11 +13,44 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/crispybits_hip.h"
 #include "cbk_kernels.hpp"
 
 using namespace cbk;
+
+namespace {
+
+// Measurement timer: while armed, each launch gets its own start/stop event pair
+// recorded by the dispatch itself (hipExtLaunchKernel), so the durations exclude
+// host overhead and the gaps between launches.
+struct Timer {
+    std::mutex mu;
+    bool armed = false;
+    int used = 0;
+    std::vector<hipEvent_t> ev;    // 2 per launch slot
+} g_timer;
+
+}  // namespace
+
+namespace cbk {
+
+hipError_t launch(const void* f, dim3 grid, dim3 block, void** args, size_t lds, hipStream_t stream) {
+    hipEvent_t start = nullptr, stop = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_timer.mu);
+        if (g_timer.armed && 2 * (g_timer.used + 1) <= (int)g_timer.ev.size()) {
+            start = g_timer.ev[2 * g_timer.used];
+            stop = g_timer.ev[2 * g_timer.used + 1];
+            ++g_timer.used;
+        }
+    }
+    if (start) return hipExtLaunchKernel(f, grid, block, args, lds, stream, start, stop, 0);
+    return hipLaunchKernel(f, grid, block, args, lds, stream);
+}
+
+}  // namespace cbk
 
 namespace {
 
@@ -183,7 +217,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
         e = ensure_lds(f, pl.lds);
         if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
         void* args[] = {&A};
-        e = hipLaunchKernel(f, dim3(pl.grid), dim3(64 * pl.nw), args, (size_t)pl.lds, s);
+        e = launch(f, dim3(pl.grid), dim3(64 * pl.nw), args, (size_t)pl.lds, s);
     } else {
         e = launch_gemv_generic(A, dtype, mode, pl.grid, s);
     }
@@ -417,6 +451,40 @@ int cbk_unpack_codes(const int32_t* packed, int64_t N, int64_t K, int bits, int3
     const hipError_t e = launch_unpack(reinterpret_cast<const uint32_t*>(packed), (int)N, (int)K, bits, codes,
                                        reinterpret_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "unpack_codes: launch");
+    return CBK_OK;
+}
+
+int cbk_timer_start(int capacity) {
+    if (capacity <= 0 || capacity > (1 << 20)) return fail(CBK_EINVAL, "timer capacity must be in [1, 2^20]");
+    std::lock_guard<std::mutex> lk(g_timer.mu);
+    if (g_timer.armed) return fail(CBK_EINVAL, "timer already armed");
+    while ((int)g_timer.ev.size() < 2 * capacity) {
+        hipEvent_t e;
+        const hipError_t err = hipEventCreate(&e);
+        if (err != hipSuccess) return hip_fail(err, "timer: event create");
+        g_timer.ev.push_back(e);
+    }
+    g_timer.used = 0;
+    g_timer.armed = true;
+    return CBK_OK;
+}
+
+int cbk_timer_stop(double* total_ms, int* launches, double* durations_ms, int max_durations) {
+    std::lock_guard<std::mutex> lk(g_timer.mu);
+    if (!g_timer.armed) return fail(CBK_EINVAL, "timer not armed");
+    g_timer.armed = false;
+    double total = 0.0;
+    for (int i = 0; i < g_timer.used; ++i) {
+        hipError_t err = hipEventSynchronize(g_timer.ev[2 * i + 1]);
+        if (err != hipSuccess) return hip_fail(err, "timer: synchronize");
+        float ms = 0.f;
+        err = hipEventElapsedTime(&ms, g_timer.ev[2 * i], g_timer.ev[2 * i + 1]);
+        if (err != hipSuccess) return hip_fail(err, "timer: elapsed");
+        total += ms;
+        if (durations_ms && i < max_durations) durations_ms[i] = ms;
+    }
+    if (total_ms) *total_ms = total;
+    if (launches) *launches = g_timer.used;
     return CBK_OK;
 }
 

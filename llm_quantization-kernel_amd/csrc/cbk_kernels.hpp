@@ -6,6 +6,11 @@
 
 namespace cbk {
 
+// abi.cpp: every kernel launch goes through here.  While the measurement timer is
+// armed (cbk_timer_start) the launch records start/stop events inside the dispatch
+// (hipExtLaunchKernel), so cbk_timer_stop reports pure kernel durations.
+hipError_t launch(const void* f, dim3 grid, dim3 block, void** args, size_t lds, hipStream_t stream);
+
 // gemv_mfma.hip: fp16, group size % 128 == 0.  Kernel address for the attribute
 // queries and the launch; max_batch <= 1 selects the single-row epilogue.
 const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);

@@ -235,14 +235,14 @@ const void* valu_for_bits(int bits) {
 hipError_t launch_gemm_mfma(const GemmArgs& A, int dt, hipStream_t stream) {
     const void* f = dt == DT_F16 ? mfma_for_bits<DT_F16>(A.bits) : mfma_for_bits<DT_BF16>(A.bits);
     void* args[] = {const_cast<GemmArgs*>(&A)};
-    return hipLaunchKernel(f, dim3((A.N + BN - 1) / BN, (A.M + BM - 1) / BM), dim3(THREADS), args, 0, stream);
+    return launch(f, dim3((A.N + BN - 1) / BN, (A.M + BM - 1) / BM), dim3(THREADS), args, 0, stream);
 }
 
 hipError_t launch_gemm_valu(const GemmArgs& A, int dt, hipStream_t stream) {
     const void* f = dt == DT_F16 ? valu_for_bits<DT_F16>(A.bits)
                   : dt == DT_BF16 ? valu_for_bits<DT_BF16>(A.bits) : valu_for_bits<DT_F32>(A.bits);
     void* args[] = {const_cast<GemmArgs*>(&A)};
-    return hipLaunchKernel(f, dim3((A.N + VT - 1) / VT, (A.M + VT - 1) / VT), dim3(VT * VT), args, 0, stream);
+    return launch(f, dim3((A.N + VT - 1) / VT, (A.M + VT - 1) / VT), dim3(VT * VT), args, 0, stream);
 }
 
 }  // namespace cbk

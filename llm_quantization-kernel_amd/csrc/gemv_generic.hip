@@ -135,7 +135,7 @@ const void* gemv_generic_kernel_for(int dt, int mode) {
 
 hipError_t launch_gemv_generic(const GemvArgs& A, int dt, int mode, int grid, hipStream_t stream) {
     void* args[] = {const_cast<GemvArgs*>(&A)};
-    return hipLaunchKernel(gemv_generic_kernel_for(dt, mode), dim3(grid), dim3(GENERIC_THREADS), args, 0, stream);
+    return launch(gemv_generic_kernel_for(dt, mode), dim3(grid), dim3(GENERIC_THREADS), args, 0, stream);
 }
 
 hipError_t launch_gemv_reduce(const GemvArgs& A, int dt, int mode, hipStream_t stream) {
@@ -143,7 +143,7 @@ hipError_t launch_gemv_reduce(const GemvArgs& A, int dt, int mode, hipStream_t s
     const void* f = dt == DT_F16 ? reduce_for_mode<DT_F16>(mode)
                   : dt == DT_BF16 ? reduce_for_mode<DT_BF16>(mode) : reduce_for_mode<DT_F32>(mode);
     void* args[] = {const_cast<GemvArgs*>(&A)};
-    return hipLaunchKernel(f, dim3((unsigned)((total + 255) / 256)), dim3(256), args, 0, stream);
+    return launch(f, dim3((unsigned)((total + 255) / 256)), dim3(256), args, 0, stream);
 }
 
 }  // namespace cbk

@@ -38,10 +38,11 @@ hipError_t launch_unpack(const uint32_t* packed, int N, int K, int bits, int32_t
     const int C = (K + 31) / 32;
     const long total = (long)N * C;
     const dim3 grid((unsigned)((total + 255) / 256)), block(256);
-    if (bits == 2) hipLaunchKernelGGL(unpack_kernel<2>, grid, block, 0, stream, packed, N, K, C, codes);
-    else if (bits == 3) hipLaunchKernelGGL(unpack_kernel<3>, grid, block, 0, stream, packed, N, K, C, codes);
-    else hipLaunchKernelGGL(unpack_kernel<4>, grid, block, 0, stream, packed, N, K, C, codes);
-    return hipGetLastError();
+    const void* f = bits == 2 ? reinterpret_cast<const void*>(&unpack_kernel<2>)
+                  : bits == 3 ? reinterpret_cast<const void*>(&unpack_kernel<3>)
+                              : reinterpret_cast<const void*>(&unpack_kernel<4>);
+    void* args[] = {&packed, &N, &K, const_cast<int*>(&C), &codes};
+    return launch(f, grid, block, args, 0, stream);
 }
 
 }  // namespace cbk
