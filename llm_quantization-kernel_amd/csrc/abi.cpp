@@ -15,7 +15,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/crispybits_hip.h"
+#include "crispybits_hip.h"
 #include "cbk_kernels.hpp"
 
 using namespace cbk;
@@ -102,8 +102,10 @@ int cu_count(int device) {
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 constexpr int MFMA_TILE = 16;          // virtual rows per MFMA decode job
-constexpr int LDS_BUDGET = 96 * 1024;  // dynamic LDS per decode workgroup
+constexpr int LDS_BUDGET = 160 * 1024; // dynamic LDS per decode workgroup (gfx950: 160 KB per CU)
 constexpr int WAVES_PER_CU = 8;        // decode occupancy target
+constexpr int MFMA_STAGE_UNITS = Ring<4>::S;   // units per weight-ring stage (gemv_mfma.hip)
+constexpr int MFMA_MAX_WAVES = 8;      // waves per decode workgroup (launch bound 512 threads)
 
 bool valid_dtype(int dt) { return dt == CBK_F16 || dt == CBK_BF16 || dt == CBK_F32; }
 
@@ -134,39 +136,71 @@ int check_x(const void* x, int dtype, int64_t M, int64_t K) {
 struct Plan {
     bool mfma = false;
     int P = 1, ntiles = 0, mtiles = 0, jobs = 0, grid = 0;
-    int nw = 1, units = 0, xs_bytes = 0, red_off = 0, lds = 0;
+    int nw = 1, units = 0, xs_bytes = 0, meta_off = 0, ring_off = 0, wave_bytes = 0, red_off = 0, lds = 0;
 };
 
-int mfma_lds(int64_t units, int P, int mt, int nw, int* xs_bytes, int* red_off) {
+struct LdsLayout {
+    int xs_bytes = 0, meta_off = 0, ring_off = 0, wave_bytes = 0, red_off = 0, total = 0;
+};
+
+// LDS of one MFMA decode workgroup (gemv_mfma.hip): NW private wave regions (staged
+// activations, their unit sums, (scale, zero) pairs, a 2-slot weight ring) and the
+// cross-wave reduction area.
+LdsLayout mfma_lds(int64_t units, int P, int mt, int nw, int bits, int gs) {
+    LdsLayout L;
     const int64_t nu = ceil_div(units, P);
-    const int64_t xs = nu * 256 * mt;
-    const int64_t xsum = nu * 16 * 4;
-    const int64_t red = std::max<int64_t>(nu * 4 * mt * 4, (int64_t)std::max(nw - 1, 1) * 1024);
-    if (xs_bytes) *xs_bytes = (int)xs;
-    if (red_off) *red_off = (int)(xs + xsum);
-    return (int)(xs + xsum + red);
+    const int64_t nuw = ceil_div(nu, nw);                       // units of the busiest wave
+    const int64_t ngw = nuw / std::max(gs / 128, 1) + 2;         // groups it touches, upper bound
+    const int64_t xs = nuw * 256 * mt;
+    const int64_t meta_off = xs + nuw * 16 * 4;
+    const int64_t ring_off = (meta_off + 16 * ngw * 4 + 15) / 16 * 16;
+    const int64_t wave_bytes = ring_off + 2 * ring_slot_bytes(bits);
+    L.xs_bytes = (int)xs;
+    L.meta_off = (int)meta_off;
+    L.ring_off = (int)ring_off;
+    L.wave_bytes = (int)wave_bytes;
+    L.red_off = (int)(nw * wave_bytes);
+    L.total = (int)(nw * wave_bytes + (int64_t)std::max(nw - 1, 1) * 1024);
+    return L;
 }
 
-Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int split_k, int rho, int cus, bool mfma_ok) {
+Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int split_k, int rho, int cus,
+               bool mfma_ok) {
     Plan pl;
     const int64_t C = ceil_div(K, 32);
-    pl.mfma = mfma_ok && dtype == CBK_F16 && gs % 128 == 0;
+    // MFMA path: fp16, whole 128-code units per group, rows a multiple of 16 bytes
+    pl.mfma = mfma_ok && dtype == CBK_F16 && gs % 128 == 0 && (C * bits) % 4 == 0;
     const int64_t sm = std::max(cus, 1);
     if (pl.mfma) {
         pl.units = (int)ceil_div(C, 4);
         const int mt = (int)std::min<int64_t>(16, std::max<int64_t>(M, 1));
-        pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, pl.units));
-        while (pl.P < pl.units && mfma_lds(pl.units, pl.P, mt, 8, nullptr, nullptr) > LDS_BUDGET) ++pl.P;
         pl.ntiles = (int)ceil_div(V, MFMA_TILE);
         pl.mtiles = (int)ceil_div(std::max<int64_t>(M, 1), 16);
-        const int64_t jobs = (int64_t)pl.mtiles * pl.ntiles * pl.P;
-        pl.jobs = (int)jobs;
-        pl.grid = (int)(rho > 0 ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm)) : jobs);
-        const int64_t min_units = pl.units / pl.P;
-        int64_t nw = ceil_div((int64_t)WAVES_PER_CU * sm, pl.grid);
-        nw = std::max<int64_t>(1, std::min<int64_t>({nw, 8, std::max<int64_t>(min_units, 1)}));
-        pl.nw = (int)nw;
-        pl.lds = mfma_lds(pl.units, pl.P, mt, pl.nw, &pl.xs_bytes, &pl.red_off);
+        const int S = MFMA_STAGE_UNITS;
+        for (pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, pl.units));; ++pl.P) {
+            const int64_t jobs = (int64_t)pl.mtiles * pl.ntiles * pl.P;
+            pl.jobs = (int)jobs;
+            pl.grid = (int)(rho > 0 ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm)) : jobs);
+            // waves per job: about two ring stages of units each, and ~WAVES_PER_CU in total
+            const int64_t units_job = std::max<int64_t>(pl.units / pl.P, 1);
+            int64_t nw = ceil_div(units_job, 2 * S);
+            if ((int64_t)pl.grid * nw < (int64_t)WAVES_PER_CU * sm)
+                nw = std::min<int64_t>(ceil_div((int64_t)WAVES_PER_CU * sm, pl.grid), ceil_div(units_job, S));
+            nw = std::max<int64_t>(1, std::min<int64_t>(nw, MFMA_MAX_WAVES));
+            // fewer waves before more splits when the LDS does not fit
+            while (nw > 1 && mfma_lds(pl.units, pl.P, mt, (int)nw, bits, gs).total > LDS_BUDGET) --nw;
+            const LdsLayout L = mfma_lds(pl.units, pl.P, mt, (int)nw, bits, gs);
+            if (L.total <= LDS_BUDGET || pl.P >= pl.units) {
+                pl.nw = (int)nw;
+                pl.xs_bytes = L.xs_bytes;
+                pl.meta_off = L.meta_off;
+                pl.ring_off = L.ring_off;
+                pl.wave_bytes = L.wave_bytes;
+                pl.red_off = L.red_off;
+                pl.lds = L.total;
+                break;
+            }
+        }
     } else {
         pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, C));
         pl.ntiles = (int)ceil_div(V, GENERIC_ROWS);
@@ -186,6 +220,8 @@ hipError_t ensure_lds(const void* f, int bytes) {
     return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
+int max_bits(const GemvArgs& A) { return std::max({A.p[0].bits, A.p[1].bits, A.p[2].bits}); }
+
 // Common body of the three decode entry points.
 int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rho, float* partial, int device,
                void* stream) {
@@ -193,8 +229,11 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
     const int cus = cu_count(device);
     if (cus <= 0) return fail(CBK_EHIP, "cannot query the compute-unit count of device %d", device);
-    const bool mfma_ok = !mixed || (A.p[0].n % MFMA_TILE == 0 && A.p[1].n % MFMA_TILE == 0);
-    const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, split_k, rho, cus, mfma_ok);
+    bool mfma_ok = !mixed || (A.p[0].n % MFMA_TILE == 0 && A.p[1].n % MFMA_TILE == 0);
+    // direct-to-LDS dwordx4 streaming needs 16-byte aligned rows
+    for (int i = 0; i < 3; ++i)
+        mfma_ok = mfma_ok && (reinterpret_cast<uintptr_t>(A.p[i].w) % 16 == 0) && ((int64_t)A.C * A.p[i].bits) % 4 == 0;
+    const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, max_bits(A), split_k, rho, cus, mfma_ok);
     A.P = pl.P;
     A.ntiles = pl.ntiles;
     A.mtiles = pl.mtiles;
@@ -202,6 +241,9 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     A.nw = pl.nw;
     A.units = pl.units;
     A.xs_bytes = pl.xs_bytes;
+    A.meta_off = pl.meta_off;
+    A.ring_off = pl.ring_off;
+    A.wave_bytes = pl.wave_bytes;
     A.red_off = pl.red_off;
     A.lds_bytes = pl.lds;
     if (A.P > 1) {
@@ -323,7 +365,7 @@ int cbk_max_rho(int device, int bits, int mode, int* out) {
     if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
     // fp16 decode of a 4096-wide row at batch 1 with 4 waves per workgroup
     const void* f = gemv_mfma_kernel_for(mode, bits, false, 1);
-    const int lds = mfma_lds(32, 1, 1, 4, nullptr, nullptr);
+    const int lds = mfma_lds(32, 1, 1, 4, bits, 128).total;
     int blocks = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, 256, (size_t)lds);
     if (e != hipSuccess) return hip_fail(e, "max_rho: occupancy query");
@@ -335,8 +377,10 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
     if (M <= 0 || V <= 0 || K <= 0 || group_size <= 0 || split_k < 1) return 0;
     int P = 1;
     for (bool mf : {true, false}) {
-        const Plan pl = plan_gemv(dtype, M, V, K, group_size, split_k, 0, 256, mf);
-        P = std::max(P, pl.P);
+        for (int bits : {2, 3, 4}) {
+            const Plan pl = plan_gemv(dtype, M, V, K, group_size, bits, split_k, 0, 256, mf);
+            P = std::max(P, pl.P);
+        }
     }
     return P > 1 ? (int64_t)P * M * V : 0;
 }

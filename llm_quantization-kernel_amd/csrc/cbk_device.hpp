@@ -95,10 +95,31 @@ struct GemvArgs {
     int ntiles, mtiles, jobs;
     int nw;                // waves per workgroup (MFMA kernel)
     int units;             // 128-code units per row (MFMA kernel)
-    int xs_bytes;          // LDS bytes of the staged activation (MFMA kernel)
-    int red_off;           // LDS offset of the chunk-sum / cross-wave reduction area
+    int xs_bytes;          // per-wave LDS: bytes of the staged activations (unit sums follow)
+    int meta_off;          // per-wave LDS: offset of the (scale, zero) pairs
+    int ring_off;          // per-wave LDS: offset of the weight ring
+    int wave_bytes;        // per-wave LDS region size
+    int red_off;           // workgroup LDS: offset of the cross-wave reduction area
     int lds_bytes;         // dynamic LDS bytes per workgroup
 };
+
+// Per-wave weight ring of the MFMA decode kernel (host and device).  A stage is
+// S consecutive 128-code units of the 16 rows of a job tile, copied HBM -> LDS
+// with direct-to-LDS dwordx4 loads: 16-byte piece p of a stage lands at byte 16p,
+// row r of the tile owns pieces [r*PITCH, r*PITCH + PPR) and one pad piece that
+// staggers the rows across LDS banks.  R stages are in flight per wave.
+template <int BITS> struct Ring {
+    static constexpr int S = 4;                       // units per stage
+    static constexpr int R = 2;                       // stages in flight
+    static constexpr int PPR = S * BITS;              // 16-byte pieces of one row per stage
+    static constexpr int PITCH = PPR + 1;             // LDS row pitch in pieces
+    static constexpr int NDMA = (16 * PITCH + 63) / 64;   // dwordx4 LDS-DMA instructions per stage
+    static constexpr int SLOT = NDMA * 64 * 16;       // LDS bytes of one stage
+};
+
+__host__ __device__ constexpr int ring_slot_bytes(int bits) {
+    return bits == 2 ? Ring<2>::SLOT : (bits == 3 ? Ring<3>::SLOT : Ring<4>::SLOT);
+}
 
 // Projection field select without dynamic indexing of the kernel-argument struct.
 #define CBK_SEL(A, proj, field) \
