@@ -135,37 +135,61 @@ int check_x(const void* x, int dtype, int64_t M, int64_t K) {
 // ----------------------------------------------------------------------------- decode plan
 struct Plan {
     bool mfma = false;
+    bool unit_rows = false;            // batch-1 MFMA layout (units as MFMA rows, LDS-DMA staging)
     int P = 1, ntiles = 0, mtiles = 0, jobs = 0, grid = 0;
     int nw = 1, units = 0, xs_bytes = 0, meta_off = 0, ring_off = 0, wave_bytes = 0, red_off = 0, lds = 0;
+    int ring = 1;
 };
 
 struct LdsLayout {
     int xs_bytes = 0, meta_off = 0, ring_off = 0, wave_bytes = 0, red_off = 0, total = 0;
 };
 
-// LDS of one MFMA decode workgroup (gemv_mfma.hip): NW private wave regions (staged
-// activations, their unit sums, (scale, zero) pairs, a 2-slot weight ring) and the
-// cross-wave reduction area.
-LdsLayout mfma_lds(int64_t units, int P, int mt, int nw, int bits, int gs) {
+// Stages of the busiest wave of a job.
+int64_t mfma_wave_stages(int64_t units, int P, int nw) {
+    return ceil_div(ceil_div(ceil_div(units, P), nw), MFMA_STAGE_UNITS);
+}
+
+// LDS of one MFMA decode workgroup (gemv_mfma.hip): NW private wave regions, each
+// holding the staged activation operands, the scales and a ring of `ring` weight
+// stages.  Batch 1 (unit_rows): operands and masked fp32 scales for the
+// stage-padded unit count (the raw pairs and unit sums pass through the scale
+// area, the cross-wave slots reuse the operand area).  Otherwise: operands per
+// batch row, [unit][2][16] float sums, packed (scale, zero) halves [row][unit],
+// and a separate cross-wave reduction area.
+LdsLayout mfma_lds(int64_t units, int P, int mt, int nw, int bits, int gs, int ring, bool unit_rows) {
     LdsLayout L;
+    (void)gs;
     const int64_t nu = ceil_div(units, P);
     const int64_t nuw = ceil_div(nu, nw);                       // units of the busiest wave
-    const int64_t ngw = nuw / std::max(gs / 128, 1) + 2;         // groups it touches, upper bound
-    const int64_t xs = nuw * 256 * mt;
-    const int64_t meta_off = xs + nuw * 16 * 4;
-    const int64_t ring_off = (meta_off + 16 * ngw * 4 + 15) / 16 * 16;
-    const int64_t wave_bytes = ring_off + 2 * ring_slot_bytes(bits);
+    int64_t xs, meta_off, ring_off;
+    if (unit_rows) {
+        const int64_t npad = ceil_div(nuw, MFMA_STAGE_UNITS) * MFMA_STAGE_UNITS;
+        xs = npad * 256;
+        meta_off = xs;
+        ring_off = xs + npad * 256;
+    } else {
+        xs = nuw * 256 * mt;
+        meta_off = xs + nuw * 32 * 4;
+        ring_off = (meta_off + 16 * nuw * 4 + 15) / 16 * 16;
+    }
+    const int64_t wave_bytes = ring_off + (int64_t)ring * ring_slot_bytes(bits);
     L.xs_bytes = (int)xs;
     L.meta_off = (int)meta_off;
     L.ring_off = (int)ring_off;
     L.wave_bytes = (int)wave_bytes;
     L.red_off = (int)(nw * wave_bytes);
-    L.total = (int)(nw * wave_bytes + (int64_t)std::max(nw - 1, 1) * 1024);
+    L.total = (int)(nw * wave_bytes + (unit_rows ? 0 : (int64_t)std::max(nw - 1, 1) * 1024));
     return L;
 }
 
+// Decode launch plan.  MFMA path: jobs of 16 rows x one K split, NW waves per job
+// (about two stages of units each, raised towards WAVES_PER_CU per CU), and a ring
+// deep enough to request every stage of a wave at once; when the LDS is short the
+// ring shrinks to 2 slots, then the workgroup loses waves, then the ring drops to
+// 1 slot, and only then K is split further.
 Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int split_k, int rho, int cus,
-               bool mfma_ok) {
+               bool mfma_ok, bool xvec) {
     Plan pl;
     const int64_t C = ceil_div(K, 32);
     // MFMA path: fp16, whole 128-code units per group, rows a multiple of 16 bytes
@@ -174,24 +198,39 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
     if (pl.mfma) {
         pl.units = (int)ceil_div(C, 4);
         const int mt = (int)std::min<int64_t>(16, std::max<int64_t>(M, 1));
+        // batch 1 with 16-byte x pieces: activations and scales staged by LDS-DMA
+        pl.unit_rows = M <= 1 && xvec;
         pl.ntiles = (int)ceil_div(V, MFMA_TILE);
         pl.mtiles = (int)ceil_div(std::max<int64_t>(M, 1), 16);
         const int S = MFMA_STAGE_UNITS;
+        const int RMAX = Ring<4>::RMAX;
         for (pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, pl.units));; ++pl.P) {
             const int64_t jobs = (int64_t)pl.mtiles * pl.ntiles * pl.P;
             pl.jobs = (int)jobs;
             pl.grid = (int)(rho > 0 ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm)) : jobs);
-            // waves per job: about two ring stages of units each, and ~WAVES_PER_CU in total
-            const int64_t units_job = std::max<int64_t>(pl.units / pl.P, 1);
+            const int64_t units_job = std::max<int64_t>(ceil_div(pl.units, pl.P), 1);
             int64_t nw = ceil_div(units_job, 2 * S);
             if ((int64_t)pl.grid * nw < (int64_t)WAVES_PER_CU * sm)
                 nw = std::min<int64_t>(ceil_div((int64_t)WAVES_PER_CU * sm, pl.grid), ceil_div(units_job, S));
             nw = std::max<int64_t>(1, std::min<int64_t>(nw, MFMA_MAX_WAVES));
-            // fewer waves before more splits when the LDS does not fit
-            while (nw > 1 && mfma_lds(pl.units, pl.P, mt, (int)nw, bits, gs).total > LDS_BUDGET) --nw;
-            const LdsLayout L = mfma_lds(pl.units, pl.P, mt, (int)nw, bits, gs);
-            if (L.total <= LDS_BUDGET || pl.P >= pl.units) {
-                pl.nw = (int)nw;
+            auto fits = [&](int w, int r) {
+                return mfma_lds(pl.units, pl.P, mt, w, bits, gs, r, pl.unit_rows).total <= LDS_BUDGET;
+            };
+            int w = (int)nw;
+            int r = (int)std::min<int64_t>(mfma_wave_stages(pl.units, pl.P, w), RMAX);
+            while (r > 2 && !fits(w, r)) --r;
+            while (w > 1 && !fits(w, r)) {
+                --w;
+                r = (int)std::min<int64_t>({mfma_wave_stages(pl.units, pl.P, w), RMAX, (int64_t)std::max(r, 2)});
+                while (r > 2 && !fits(w, r)) --r;
+            }
+            if (!fits(w, r)) r = 1;
+            // the batch-1 staging covers at most 16 units per wave in one pass
+            const bool ok = fits(w, r) && (!pl.unit_rows || ceil_div(units_job, w) <= 16);
+            if (ok || pl.P >= pl.units) {
+                const LdsLayout L = mfma_lds(pl.units, pl.P, mt, w, bits, gs, r, pl.unit_rows);
+                pl.nw = w;
+                pl.ring = r;
                 pl.xs_bytes = L.xs_bytes;
                 pl.meta_off = L.meta_off;
                 pl.ring_off = L.ring_off;
@@ -233,7 +272,8 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     // direct-to-LDS dwordx4 streaming needs 16-byte aligned rows
     for (int i = 0; i < 3; ++i)
         mfma_ok = mfma_ok && (reinterpret_cast<uintptr_t>(A.p[i].w) % 16 == 0) && ((int64_t)A.C * A.p[i].bits) % 4 == 0;
-    const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, max_bits(A), split_k, rho, cus, mfma_ok);
+    const bool xvec = (A.K % 8 == 0) && (reinterpret_cast<uintptr_t>(A.x) % 16 == 0);
+    const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, max_bits(A), split_k, rho, cus, mfma_ok, xvec);
     A.P = pl.P;
     A.ntiles = pl.ntiles;
     A.mtiles = pl.mtiles;
@@ -246,6 +286,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     A.wave_bytes = pl.wave_bytes;
     A.red_off = pl.red_off;
     A.lds_bytes = pl.lds;
+    A.ring = pl.ring;
     if (A.P > 1) {
         if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
         A.partial = partial;
@@ -255,7 +296,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t e;
     if (pl.mfma) {
-        const void* f = gemv_mfma_kernel_for(mode, A.p[0].bits, mixed, A.M);
+        const void* f = gemv_mfma_kernel_for(mode, A.p[0].bits, mixed, pl.unit_rows ? 1 : 16);
         e = ensure_lds(f, pl.lds);
         if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
         void* args[] = {&A};
@@ -365,7 +406,7 @@ int cbk_max_rho(int device, int bits, int mode, int* out) {
     if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
     // fp16 decode of a 4096-wide row at batch 1 with 4 waves per workgroup
     const void* f = gemv_mfma_kernel_for(mode, bits, false, 1);
-    const int lds = mfma_lds(32, 1, 1, 4, bits, 128).total;
+    const int lds = mfma_lds(32, 1, 1, 4, bits, 128, 2, true).total;
     int blocks = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, 256, (size_t)lds);
     if (e != hipSuccess) return hip_fail(e, "max_rho: occupancy query");
@@ -378,8 +419,10 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
     int P = 1;
     for (bool mf : {true, false}) {
         for (int bits : {2, 3, 4}) {
-            const Plan pl = plan_gemv(dtype, M, V, K, group_size, bits, split_k, 0, 256, mf);
-            P = std::max(P, pl.P);
+            for (bool xv : {true, false}) {
+                const Plan pl = plan_gemv(dtype, M, V, K, group_size, bits, split_k, 0, 256, mf, xv);
+                P = std::max(P, pl.P);
+            }
         }
     }
     return P > 1 ? (int64_t)P * M * V : 0;

@@ -101,16 +101,19 @@ struct GemvArgs {
     int wave_bytes;        // per-wave LDS region size
     int red_off;           // workgroup LDS: offset of the cross-wave reduction area
     int lds_bytes;         // dynamic LDS bytes per workgroup
+    int ring;              // weight-ring slots per wave (MFMA kernel), 1 .. Ring<>::RMAX
+    int pad_;
 };
 
 // Per-wave weight ring of the MFMA decode kernel (host and device).  A stage is
 // S consecutive 128-code units of the 16 rows of a job tile, copied HBM -> LDS
 // with direct-to-LDS dwordx4 loads: 16-byte piece p of a stage lands at byte 16p,
 // row r of the tile owns pieces [r*PITCH, r*PITCH + PPR) and one pad piece that
-// staggers the rows across LDS banks.  R stages are in flight per wave.
+// staggers the rows across LDS banks.  Up to RMAX stages are in flight per wave
+// (RMAX * NDMA stays well inside the 6-bit vmcnt counter).
 template <int BITS> struct Ring {
     static constexpr int S = 4;                       // units per stage
-    static constexpr int R = 2;                       // stages in flight
+    static constexpr int RMAX = 8;                    // ring slots per wave, at most
     static constexpr int PPR = S * BITS;              // 16-byte pieces of one row per stage
     static constexpr int PITCH = PPR + 1;             // LDS row pitch in pieces
     static constexpr int NDMA = (16 * PITCH + 63) / 64;   // dwordx4 LDS-DMA instructions per stage
@@ -121,9 +124,18 @@ __host__ __device__ constexpr int ring_slot_bytes(int bits) {
     return bits == 2 ? Ring<2>::SLOT : (bits == 3 ? Ring<3>::SLOT : Ring<4>::SLOT);
 }
 
-// Projection field select without dynamic indexing of the kernel-argument struct.
-#define CBK_SEL(A, proj, field) \
-    ((proj) == 0 ? (A).p[0].field : ((proj) == 1 ? (A).p[1].field : (A).p[2].field))
+// Projection field select between values of the kernel-argument struct.  The
+// empty asm pins each loaded field as an SGPR value, so LLVM cannot fold the
+// choice into a load from a chosen field address -- an address select into the
+// kernarg struct would force a copy of the whole struct to scratch.
+template <typename T>
+__device__ __forceinline__ T kernarg_value(T v) {
+    asm("" : "+s"(v));
+    return v;
+}
+#define CBK_SEL(A, proj, field)                                                                      \
+    ((proj) == 0 ? kernarg_value((A).p[0].field)                                                     \
+                 : ((proj) == 1 ? kernarg_value((A).p[1].field) : kernarg_value((A).p[2].field)))
 
 // Virtual row v -> (projection, local row): QKV concatenates [q; k; v], gate-up
 // interleaves gate row n -> 2n and up row n -> 2n+1 (packed_gemv.cu:33-42).

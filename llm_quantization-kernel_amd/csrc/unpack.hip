@@ -22,13 +22,13 @@ __global__ void __launch_bounds__(256) unpack_kernel(const uint32_t* __restrict_
 #pragma unroll
     for (int i = 0; i < BITS; ++i) w[i] = p[i];
     uint32_t h[16];
-    Decode<BITS>::run(w, h);
+    Decode<BITS>::run(w, h, MAGIC2);
 #pragma unroll
     for (int q = 0; q < 32; ++q) {
         const int k = c * 32 + Decode<BITS>::kappa(q);
         const uint32_t half = (q & 1) ? (h[q >> 1] >> 16) : (h[q >> 1] & 0xFFFFu);
-        // half = fp16 bits of 1024 + code: the code is the low mantissa field
-        if (k < K) codes[(long)n * K + k] = (int32_t)(half - 0x6400u);
+        // half = fp16 bits of 1024 + 2^e * code; anything else reads back as -1
+        if (k < K) codes[(long)n * K + k] = code_of_half<BITS>(half, q);
     }
 }
 
