@@ -287,6 +287,12 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     A.red_off = pl.red_off;
     A.lds_bytes = pl.lds;
     A.ring = pl.ring;
+    if ((int64_t)A.units * A.P >= (1ll << 31) || (int64_t)A.jobs * 16 >= (1ll << 31))
+        return fail(CBK_EINVAL, "packed_gemv: problem too large for 32-bit job indexing");
+    A.divP = make_fastdiv((uint32_t)A.P);
+    A.divT = make_fastdiv((uint32_t)std::max(A.ntiles, 1));
+    A.divW = make_fastdiv((uint32_t)std::max(A.nw, 1));
+    A.divG = make_fastdiv((uint32_t)std::max(A.gs >> 7, 1));
     if (A.P > 1) {
         if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
         A.partial = partial;

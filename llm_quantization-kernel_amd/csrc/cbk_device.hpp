@@ -69,6 +69,36 @@ __device__ __forceinline__ int rope_unperm(int r, int hd) {
     return head * hd + ((p & 1) ? (p >> 1) + (hd >> 1) : (p >> 1));
 }
 
+// ---------------------------------------------------------------- invariant division
+// n / d for 32-bit unsigned n and a divisor fixed per launch, as one multiply-high
+// and three shifts/adds (Granlund & Montgomery, "Division by Invariant Integers
+// using Multiplication", PLDI 1994, fig. 4.1): with l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1, t = mulhi(m, n), q = (t + ((n - t) >> 1)) >> (l - 1)
+// (shifts 0 and 0 for d = 1).  Job and unit indices are divided this way instead
+// of by the generic 32/64-bit division sequences, which cost hundreds of scalar
+// instructions per wave.
+struct FastDiv {
+    uint32_t m;
+    uint32_t s1, s2;
+    uint32_t d;
+};
+
+__host__ inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f;
+    uint32_t l = 0;
+    while (l < 32 && (1ull << l) < d) ++l;
+    f.m = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    f.s1 = l < 1 ? l : 1;
+    f.s2 = l > 1 ? l - 1 : 0;
+    f.d = d;
+    return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+    const uint32_t t = __umulhi(n, f.m);
+    return (t + ((n - t) >> f.s1)) >> f.s2;
+}
+
 // ---------------------------------------------------------------- decode-call arguments
 struct Proj {
     const uint32_t* w;   // packed [n, wpr]
@@ -103,6 +133,7 @@ struct GemvArgs {
     int lds_bytes;         // dynamic LDS bytes per workgroup
     int ring;              // weight-ring slots per wave (MFMA kernel), 1 .. Ring<>::RMAX
     int pad_;
+    FastDiv divP, divT, divW, divG;   // by P, ntiles, nw and gs / 128 (MFMA kernel)
 };
 
 // Per-wave weight ring of the MFMA decode kernel (host and device).  A stage is

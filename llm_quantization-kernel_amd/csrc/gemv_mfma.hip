@@ -105,7 +105,7 @@ __device__ __forceinline__ void load_x(const GemvArgs& A, int b0, int ua, int nc
                                        XTask& t) {
     t.real = task < ntask;
     const int tk = t.real ? task : 0;
-    t.i = tk / nch;
+    t.i = (int)(((float)tk + 0.5f) / (float)nch);   // exact: tk < 2^12, nch <= 64
     t.c = tk - t.i * nch;
     const _Float16* xr = reinterpret_cast<const _Float16*>(A.x) + (long)(b0 + t.i) * A.K;
     const int k0 = (ua * 4 + t.c) * 32;
@@ -189,7 +189,7 @@ struct MetaRegs {
 };
 
 template <int MODE>
-__device__ __forceinline__ void load_meta(const GemvArgs& A, int tile, int ua, int my, int gdiv, int e0, int lane,
+__device__ __forceinline__ void load_meta(const GemvArgs& A, int tile, int ua, int my, int e0, int lane,
                                           MetaRegs& m) {
     const uint32_t* w;
     const _Float16 *s, *z;
@@ -198,7 +198,7 @@ __device__ __forceinline__ void load_meta(const GemvArgs& A, int tile, int ua, i
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         if (e < ne) {
-            const int g = (ua + min(e0 + (lane >> 4) + 4 * e, my - 1)) / gdiv;
+            const int g = (int)fdiv((uint32_t)(ua + min(e0 + (lane >> 4) + 4 * e, my - 1)), A.divG);
             m.s[e] = s[g];
             m.z[e] = z[g];
         }
@@ -264,16 +264,19 @@ __device__ __forceinline__ int dma_x1(const GemvArgs& A, int ua, int npad, int l
 // writes one dword per lane); lanes past 16 my re-read the last entry into the
 // padding.  Returns the number of DMA instructions issued.
 template <int MODE>
-__device__ __forceinline__ int dma_meta1(const GemvArgs& A, int tile, int ua, int my, int gdiv, int lane, char* sraw,
+__device__ __forceinline__ int dma_meta1(const GemvArgs& A, int tile, int ua, int my, int lane, char* sraw,
                                          char* zraw) {
     const int n = 16 * my, ni = (n + 63) >> 6;
+    const float rmy = 1.f / (float)my;
     for (int t = 0; t < ni; ++t) {
         const int e = min(64 * t + lane, n - 1);
-        const int j = e / my, ul = e - j * my;
+        // e / my for e < 1024, my <= 16: the float quotient of (e + 0.5) is at least
+        // 1 / 32 away from an integer, far beyond its rounding error
+        const int j = (int)(((float)e + 0.5f) * rmy), ul = e - j * my;
         const uint32_t* w;
         const _Float16 *s, *z;
         tile_row<MODE>(A, tile * 16 + j, w, s, z);
-        const int g = (ua + ul) / gdiv;
+        const int g = (int)fdiv((uint32_t)(ua + ul), A.divG);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(s + g), (lds_void*)(sraw + t * 256), 2, 0, 0);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(z + g), (lds_void*)(zraw + t * 256), 2, 0, 0);
     }
@@ -456,22 +459,22 @@ __device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int NW = A.nw;
-    const int p = job % A.P;
-    const int rest = job / A.P;
-    const int tile = rest % A.ntiles;
-    const int mtile = rest / A.ntiles;
+    // job = (mtile * ntiles + tile) * P + p; every division is by a launch invariant
+    const int rest = (int)fdiv((uint32_t)job, A.divP);
+    const int p = job - rest * A.P;
+    const int mtile = (int)fdiv((uint32_t)rest, A.divT);
+    const int tile = rest - mtile * A.ntiles;
     const int b0 = mtile * 16;
     const int mt = MB == 1 ? 1 : min(16, A.M - b0);
-    const int u0 = (int)(((long)A.units * p) / A.P);
-    const int u1 = (int)(((long)A.units * (p + 1)) / A.P);
+    const int u0 = (int)fdiv((uint32_t)(A.units * p), A.divP);
+    const int u1 = (int)fdiv((uint32_t)(A.units * (p + 1)), A.divP);
     const int nu = u1 - u0;
-    const int gdiv = A.gs >> 7;                                  // units per quantization group
     const int rowbytes = A.C * BITS * 4;
     const int j = lane & 15, kq = lane >> 4;
 
     // this wave's contiguous unit range, in stages of S units, and its LDS region
-    const int ua = u0 + (int)(((long)nu * wave) / NW);
-    const int ub = u0 + (int)(((long)nu * (wave + 1)) / NW);
+    const int ua = u0 + (int)fdiv((uint32_t)(nu * wave), A.divW);
+    const int ub = u0 + (int)fdiv((uint32_t)(nu * (wave + 1)), A.divW);
     const int my = ub - ua;
     const int nst = (my + RG::S - 1) / RG::S;
     const int R = A.ring;
@@ -502,7 +505,7 @@ __device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
             // 1) ring stage 0, the activations, the pairs, ring stages 1 .. R-1
             dma_stage<BITS>(dl, ua, rowbytes, ring);
             dma_x1(A, ua, npad, lane, xw);
-            dma_meta1<MODE>(A, tile, ua, my, gdiv, lane, sraw, zraw);
+            dma_meta1<MODE>(A, tile, ua, my, lane, sraw, zraw);
 #pragma unroll
             for (int r = 1; r < RG::RMAX; ++r)
                 if (r < R) dma_stage<BITS>(dl, ua + r * RG::S, rowbytes, ring + r * RG::SLOT);
@@ -558,7 +561,7 @@ __device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
             XTask xt;
             load_x(A, b0, ua, nch, ntask, lane, vec, xt);
             MetaRegs mr;
-            load_meta<MODE>(A, tile, ua, my, gdiv, 0, lane, mr);
+            load_meta<MODE>(A, tile, ua, my, 0, lane, mr);
             dma_stage<BITS>(dl, ua, rowbytes, ring);
 #pragma unroll
             for (int r = 1; r < RG::RMAX; ++r)
@@ -574,7 +577,7 @@ __device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
             uint32_t* mp = reinterpret_cast<uint32_t*>(meta);
             store_meta(A, mr, tile, my, 0, lane, mp);
             for (int e0 = 16; e0 < my; e0 += 16) {
-                load_meta<MODE>(A, tile, ua, my, gdiv, e0, lane, mr);
+                load_meta<MODE>(A, tile, ua, my, e0, lane, mr);
                 store_meta(A, mr, tile, my, e0, lane, mp);
             }
 
@@ -632,7 +635,8 @@ template <int MB>
 __global__ void __launch_bounds__(512) gemv_mfma_qkv_mixed_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     for (int job = blockIdx.x; job < A.jobs; job += gridDim.x) {
-        const int v0 = ((job / A.P) % A.ntiles) * 16;
+        const int rest = (int)fdiv((uint32_t)job, A.divP);
+        const int v0 = (rest - (int)fdiv((uint32_t)rest, A.divT) * A.ntiles) * 16;
         const int proj = v0 < A.p[0].n ? 0 : (v0 < A.p[0].n + A.p[1].n ? 1 : 2);
         const int bits = CBK_SEL(A, proj, bits);
         if (bits == 2) run_job<2, MODE_QKV, MB>(A, job, lds);
