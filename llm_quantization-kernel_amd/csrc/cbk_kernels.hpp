@@ -32,11 +32,17 @@ struct GemmArgs {
     const void* b;          // bias [N] or nullptr
     void* out;              // [M, N]
     int M, N, K, C, G, gs, wpr, bits, act;
+    int pad_;
+    FastDiv divG;           // by the group size (gemm_f16.hip)
 };
 
 // gemm.hip
 hipError_t launch_gemm_mfma(const GemmArgs& A, int dt, hipStream_t stream);
 hipError_t launch_gemm_valu(const GemmArgs& A, int dt, hipStream_t stream);
+
+// gemm_f16.hip: fp16, K % 8 == 0, 16-byte aligned x.
+bool gemm_f16_supported(const GemmArgs& A);
+hipError_t launch_gemm_f16(const GemmArgs& A, hipStream_t stream);
 
 // unpack.hip
 hipError_t launch_unpack(const uint32_t* packed, int N, int K, int bits, int32_t* codes, hipStream_t stream);
