@@ -19,7 +19,13 @@ Algorithmic bytes of one decode launch:
     N*ceil(K/32)*bits*4 (packed) + N*ceil(K/128)*2*2 (fp16 scales+zeros) + M*K*2 + M*N*2
 Algorithmic FLOPs of one prefill launch: 2*M*N*K.
 
+`roofline.traffic` (HBM bytes per launch of the dominant kernel) is read from
+profiles/gemv_w3_m1_traffic.txt, written from two rocprofv3 --pmc passes
+(FETCH_SIZE, WRITE_SIZE) over `bench.py --pmc-workload` scaled by the same
+counters' reading for a copy of known size; null if that file is absent.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+       python bench.py --pmc-workload     (fixed launches for counter collection)
 Prints one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -38,6 +44,8 @@ for _p in (ROOT, os.path.join(ROOT, "llm_quantization-kernel_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_w3_m1_traffic.txt")
+PMC_COPY_BYTES = 256 << 20     # calibration copy of the counter passes
 MFMA_F16_PEAK_TFS = 2500.0     # MI355X dense fp16 MFMA, published
 METRIC = "W3/W4 GEMV µs & HBM GB/s (% peak); M=1024 prefill GEMM TFLOP/s (% peak)"
 SHAPES = [(4096, 4096), (4096, 11008), (11008, 4096)]          # (K, N)
@@ -137,6 +145,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="timed step + roofline only (no sweeps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run the fixed launch sequence of the counter passes and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one MI355X; --gpus {args.gpus} is not supported "
@@ -152,6 +162,9 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}  CUs={C.sm_count()}")
+    if args.pmc_workload:
+        pmc_workload(torch, ops, dev)
+        return
 
     # ---------------------------------------------------------------- timed workload
     bits = 3
@@ -202,7 +215,7 @@ def main():
                           "split_k": cfg[s][0], "rho": cfg[s][1]})
     achieved = step_bytes / (total_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                 "kernel": "gemv_mfma_kernel<3,GEMV,1> (W3 decode GEMV, M=1)",
                 "bytes_per_launch_avg": round(step_bytes / (3 * LAYERS)),
                 "avg_launch_us": round(total_ms * 1e3 / (3 * LAYERS), 3), "per_shape": per_shape}
@@ -225,6 +238,40 @@ def main():
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch, base, xs)
     print(json.dumps(out), flush=True)
+
+
+def read_traffic():
+    """HBM bytes per launch of the timed W3 GEMV, averaged over the step's shapes, from
+    the committed counter summary (a `traffic_bytes_per_launch: <int>` line)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def pmc_workload(torch, ops, dev):
+    """Launch sequence of the counter passes: the calibration copy (PMC_COPY_BYTES read and
+    written by one device-to-device copy), then 8 copies of each W3 decode shape at M=1 with
+    the timed step's defaults.  Dispatch order: copy, 8 x (4096,4096), 8 x (4096,11008),
+    8 x (11008,4096)."""
+    src = torch.empty(PMC_COPY_BYTES // 2, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    for K, N in SHAPES:
+        base = make_weight(torch, N, K, 3, 0, dev)
+        ws = [base] + [clone_weight(base) for _ in range(7)]
+        x = randx(torch, 1, K, 1, dev)
+        torch.cuda.synchronize()
+        for w in ws:
+            ops.packed_linear(x, w, 1, 1)
+        torch.cuda.synchronize()
+    log("pmc workload done")
 
 
 def gemv_sweep(torch, C, ops, dev):
