@@ -133,61 +133,82 @@ int check_x(const void* x, int dtype, int64_t M, int64_t K) {
 }
 
 // ----------------------------------------------------------------------------- decode plan
-struct Plan {
-    bool mfma = false;
-    bool unit_rows = false;            // batch-1 MFMA layout (units as MFMA rows, LDS-DMA staging)
-    int P = 1, ntiles = 0, mtiles = 0, jobs = 0, grid = 0;
-    int nw = 1, units = 0, xs_bytes = 0, meta_off = 0, ring_off = 0, wave_bytes = 0, red_off = 0, lds = 0;
-    int ring = 1;
-};
-
 struct LdsLayout {
     int xs_bytes = 0, meta_off = 0, ring_off = 0, wave_bytes = 0, red_off = 0, total = 0;
+    int sum_off = 0, tab_off = 0, raw_off = 0, raw_np = 0;
 };
 
-// Stages of the busiest wave of a job.
+struct Plan {
+    bool mfma = false;
+    bool unit_rows = false;            // batch-1 MFMA layout (units as MFMA rows, shared staging)
+    int P = 1, ntiles = 0, mtiles = 0, jobs = 0, grid = 0;
+    int nw = 1, units = 0, lds = 0;
+    int ring = 1;
+    LdsLayout L;
+};
+
+// Ring stages of the busiest wave of a job (batch rows).
 int64_t mfma_wave_stages(int64_t units, int P, int nw) {
     return ceil_div(ceil_div(ceil_div(units, P), nw), MFMA_STAGE_UNITS);
 }
 
-// LDS of one MFMA decode workgroup (gemv_mfma.hip): NW private wave regions, each
-// holding the staged activation operands, the scales and a ring of `ring` weight
-// stages.  Batch 1 (unit_rows): operands and masked fp32 scales for the
-// stage-padded unit count (the raw pairs and unit sums pass through the scale
-// area, the cross-wave slots reuse the operand area).  Otherwise: operands per
-// batch row, [unit][2][16] float sums, packed (scale, zero) halves [row][unit],
-// and a separate cross-wave reduction area.
+// LDS of one MFMA decode workgroup (gemv_mfma.hip).
+// Batch 1 (unit_rows), for the stg stages of the largest K split: shared
+// activation operands of ceil(4 stg / 16) groups of 16 units (4 KB each), their
+// unit sums, the masked scale table (1 KB per stage), the raw (scale, zero) row
+// spans (32 spans of np 16-byte pieces, in whole 1 KB DMA instructions), 16 row
+// sums per wave, then the packed tile: 16 rows of nb 1 KB blocks at pitch
+// RP = 1024 nb + 16 (returned as wave_bytes).
+// Batch rows: NW private regions (operands per batch row, [unit][2][16] float
+// sums, packed (scale, zero) halves [row][unit], the ring) and the cross-wave
+// reduction area.
 LdsLayout mfma_lds(int64_t units, int P, int mt, int nw, int bits, int gs, int ring, bool unit_rows) {
     LdsLayout L;
-    (void)gs;
     const int64_t nu = ceil_div(units, P);
-    const int64_t nuw = ceil_div(nu, nw);                       // units of the busiest wave
-    int64_t xs, meta_off, ring_off;
+    const int64_t slot = ring_slot_bytes(bits);
     if (unit_rows) {
-        const int64_t npad = ceil_div(nuw, MFMA_STAGE_UNITS) * MFMA_STAGE_UNITS;
-        xs = npad * 256;
-        meta_off = xs;
-        ring_off = xs + npad * 256;
-    } else {
-        xs = nuw * 256 * mt;
-        meta_off = xs + nuw * 32 * 4;
-        ring_off = (meta_off + 16 * nuw * 4 + 15) / 16 * 16;
+        const int64_t stg = ceil_div(nu, MFMA_STAGE_UNITS);
+        const int64_t ngrp = ceil_div(MFMA_STAGE_UNITS * stg, 16);
+        const int64_t groups = ceil_div(nu, std::max(gs / 128, 1)) + 1;   // groups a split touches, at most
+        const int64_t np = ceil_div(2 * groups + 14, 16);                  // 16-byte pieces per row span
+        const int64_t sum_off = ngrp * 4096;
+        const int64_t tab_off = sum_off + ngrp * 16 * 8;
+        const int64_t raw_off = tab_off + stg * 1024;
+        const int64_t red_off = raw_off + ceil_div(32 * np, 64) * 1024;
+        const int64_t ring_off = red_off + MFMA_MAX_WAVES * 16 * 4;
+        const int64_t rp = ceil_div(nu * 16 * bits, 1024) * 1024 + 16;
+        const int64_t total = ring_off + 16 * rp;
+        L.sum_off = (int)sum_off;
+        L.tab_off = (int)tab_off;
+        L.raw_off = (int)raw_off;
+        L.red_off = (int)red_off;
+        L.ring_off = (int)ring_off;
+        L.raw_np = (int)np;
+        L.wave_bytes = (int)std::min<int64_t>(rp, INT32_MAX);
+        L.total = (int)std::min<int64_t>(total, INT32_MAX);
+        return L;
     }
-    const int64_t wave_bytes = ring_off + (int64_t)ring * ring_slot_bytes(bits);
+    const int64_t nuw = ceil_div(nu, nw);                       // units of the busiest wave
+    const int64_t xs = nuw * 256 * mt;
+    const int64_t meta_off = xs + nuw * 32 * 4;
+    const int64_t ring_off = (meta_off + 16 * nuw * 4 + 15) / 16 * 16;
+    const int64_t wave_bytes = ring_off + (int64_t)ring * slot;
     L.xs_bytes = (int)xs;
     L.meta_off = (int)meta_off;
     L.ring_off = (int)ring_off;
     L.wave_bytes = (int)wave_bytes;
     L.red_off = (int)(nw * wave_bytes);
-    L.total = (int)(nw * wave_bytes + (unit_rows ? 0 : (int64_t)std::max(nw - 1, 1) * 1024));
+    L.total = (int)std::min<int64_t>(nw * wave_bytes + (int64_t)std::max(nw - 1, 1) * 1024, INT32_MAX);
     return L;
 }
 
 // Decode launch plan.  MFMA path: jobs of 16 rows x one K split, NW waves per job
-// (about two stages of units each, raised towards WAVES_PER_CU per CU), and a ring
-// deep enough to request every stage of a wave at once; when the LDS is short the
-// ring shrinks to 2 slots, then the workgroup loses waves, then the ring drops to
-// 1 slot, and only then K is split further.
+// (about two stages of units each, raised towards WAVES_PER_CU per CU).  Batch 1
+// holds the split's whole tile in LDS, so K is split further when it does not
+// fit.  Batch rows use a per-wave ring deep enough to request every stage of a
+// wave at once; when the LDS is short the ring shrinks to 2 slots, then the
+// workgroup loses waves, then the ring drops to 1 slot, and only then K is split
+// further.
 Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int split_k, int rho, int cus,
                bool mfma_ok, bool xvec) {
     Plan pl;
@@ -216,27 +237,21 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
             auto fits = [&](int w, int r) {
                 return mfma_lds(pl.units, pl.P, mt, w, bits, gs, r, pl.unit_rows).total <= LDS_BUDGET;
             };
+            auto stages = [&](int w) { return mfma_wave_stages(pl.units, pl.P, w); };
             int w = (int)nw;
-            int r = (int)std::min<int64_t>(mfma_wave_stages(pl.units, pl.P, w), RMAX);
+            int r = (int)std::min<int64_t>(stages(w), RMAX);
             while (r > 2 && !fits(w, r)) --r;
             while (w > 1 && !fits(w, r)) {
                 --w;
-                r = (int)std::min<int64_t>({mfma_wave_stages(pl.units, pl.P, w), RMAX, (int64_t)std::max(r, 2)});
+                r = (int)std::min<int64_t>({stages(w), RMAX, (int64_t)std::max(r, 2)});
                 while (r > 2 && !fits(w, r)) --r;
             }
             if (!fits(w, r)) r = 1;
-            // the batch-1 staging covers at most 16 units per wave in one pass
-            const bool ok = fits(w, r) && (!pl.unit_rows || ceil_div(units_job, w) <= 16);
-            if (ok || pl.P >= pl.units) {
-                const LdsLayout L = mfma_lds(pl.units, pl.P, mt, w, bits, gs, r, pl.unit_rows);
+            if (fits(w, r) || pl.P >= pl.units) {
+                pl.L = mfma_lds(pl.units, pl.P, mt, w, bits, gs, r, pl.unit_rows);
                 pl.nw = w;
                 pl.ring = r;
-                pl.xs_bytes = L.xs_bytes;
-                pl.meta_off = L.meta_off;
-                pl.ring_off = L.ring_off;
-                pl.wave_bytes = L.wave_bytes;
-                pl.red_off = L.red_off;
-                pl.lds = L.total;
+                pl.lds = pl.L.total;
                 break;
             }
         }
@@ -272,7 +287,11 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     // direct-to-LDS dwordx4 streaming needs 16-byte aligned rows
     for (int i = 0; i < 3; ++i)
         mfma_ok = mfma_ok && (reinterpret_cast<uintptr_t>(A.p[i].w) % 16 == 0) && ((int64_t)A.C * A.p[i].bits) % 4 == 0;
-    const bool xvec = (A.K % 8 == 0) && (reinterpret_cast<uintptr_t>(A.x) % 16 == 0);
+    // batch 1 stages x through 16-byte pieces and fetches (scale, zero) spans as
+    // 16-byte-aligned pieces
+    bool xvec = (A.K % 8 == 0) && (reinterpret_cast<uintptr_t>(A.x) % 16 == 0);
+    for (int i = 0; i < 3; ++i)
+        xvec = xvec && reinterpret_cast<uintptr_t>(A.p[i].s) % 16 == 0 && reinterpret_cast<uintptr_t>(A.p[i].z) % 16 == 0;
     const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, max_bits(A), split_k, rho, cus, mfma_ok, xvec);
     A.P = pl.P;
     A.ntiles = pl.ntiles;
@@ -280,11 +299,15 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     A.jobs = pl.jobs;
     A.nw = pl.nw;
     A.units = pl.units;
-    A.xs_bytes = pl.xs_bytes;
-    A.meta_off = pl.meta_off;
-    A.ring_off = pl.ring_off;
-    A.wave_bytes = pl.wave_bytes;
-    A.red_off = pl.red_off;
+    A.xs_bytes = pl.L.xs_bytes;
+    A.meta_off = pl.L.meta_off;
+    A.ring_off = pl.L.ring_off;
+    A.wave_bytes = pl.L.wave_bytes;
+    A.red_off = pl.L.red_off;
+    A.sum_off = pl.L.sum_off;
+    A.tab_off = pl.L.tab_off;
+    A.raw_off = pl.L.raw_off;
+    A.raw_np = pl.L.raw_np;
     A.lds_bytes = pl.lds;
     A.ring = pl.ring;
     if ((int64_t)A.units * A.P >= (1ll << 31) || (int64_t)A.jobs * 16 >= (1ll << 31))
@@ -293,6 +316,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     A.divT = make_fastdiv((uint32_t)std::max(A.ntiles, 1));
     A.divW = make_fastdiv((uint32_t)std::max(A.nw, 1));
     A.divG = make_fastdiv((uint32_t)std::max(A.gs >> 7, 1));
+    A.divNP = make_fastdiv((uint32_t)std::max(A.raw_np, 1));
     if (A.P > 1) {
         if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
         A.partial = partial;

@@ -132,8 +132,14 @@ struct GemvArgs {
     int red_off;           // workgroup LDS: offset of the cross-wave reduction area
     int lds_bytes;         // dynamic LDS bytes per workgroup
     int ring;              // weight-ring slots per wave (MFMA kernel), 1 .. Ring<>::RMAX
+    // batch-1 MFMA layout: workgroup-shared staging areas (offsets into the LDS)
+    int sum_off;           // unit sums [unit][2] fp32
+    int tab_off;           // masked scales [unit][tile row][kq] fp32
+    int raw_off;           // raw (scale, zero) row spans [tensor][tile row][piece] x 16 B
+    int raw_np;            // 16-byte pieces per row span
     int pad_;
     FastDiv divP, divT, divW, divG;   // by P, ntiles, nw and gs / 128 (MFMA kernel)
+    FastDiv divNP;                    // by raw_np
 };
 
 // Per-wave weight ring of the MFMA decode kernel (host and device).  A stage is
@@ -145,6 +151,7 @@ struct GemvArgs {
 template <int BITS> struct Ring {
     static constexpr int S = 4;                       // units per stage
     static constexpr int RMAX = 8;                    // ring slots per wave, at most
+    static constexpr int RMAX1 = 4;                   // ... at batch 1 (units as MFMA rows)
     static constexpr int PPR = S * BITS;              // 16-byte pieces of one row per stage
     static constexpr int PITCH = PPR + 1;             // LDS row pitch in pieces
     static constexpr int NDMA = (16 * PITCH + 63) / 64;   // dwordx4 LDS-DMA instructions per stage

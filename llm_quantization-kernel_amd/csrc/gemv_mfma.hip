@@ -58,7 +58,7 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xF
 // flight.  n is wave-uniform, so the switch is scalar branches.
 template <int NDMA>
 __device__ __forceinline__ void wait_stages(int n) {
-    static_assert(NDMA * (Ring<4>::RMAX - 1) < 64, "vmcnt range");
+    static_assert(NDMA * Ring<4>::RMAX < 64, "vmcnt range");
     switch (n) {
         case 0: wait_vmcnt<0>(); break;
         case 1: wait_vmcnt<NDMA>(); break;
@@ -67,28 +67,19 @@ __device__ __forceinline__ void wait_stages(int n) {
         case 4: wait_vmcnt<4 * NDMA>(); break;
         case 5: wait_vmcnt<5 * NDMA>(); break;
         case 6: wait_vmcnt<6 * NDMA>(); break;
-        default: wait_vmcnt<7 * NDMA>(); break;
+        case 7: wait_vmcnt<7 * NDMA>(); break;
+        default: wait_vmcnt<8 * NDMA>(); break;
     }
 }
 
-// ------------------------------------------------------------------ per-wave staging
+// ------------------------------------------------------------------ batch rows: per-wave staging
+// With batch rows (M > 1) MFMA row i = batch row i and column j = tile row j.
 // Each wave stages only what its own units need, in its private LDS region, so no
-// workgroup barrier stands between the loads and the first MFMA.  Two layouts:
-//
-// batch rows (MB = 16, M > 1): MFMA row i = batch row i, row j = tile row j
+// workgroup barrier stands between the loads and the first MFMA:
 //   x   : [unit][operand m][chunk kq][batch row i] x 16 B
 //   X   : [unit][2][16] activation sums: plain, and weighted by the slot offsets
 //   meta: [tile row j][unit] (scale, zero) halves
-// units as rows (MB = 1): MFMA row i = unit g0 + i of a group of 16 units, so the
-//   activation operand is loaded once per 16 units and each unit keeps only its
-//   own output row: lane (j, kq) scales D[4kq + r][j] by the scale of unit
-//   g0 + 4kq + r and by zero in every other unit's step.
-//   x   : [unit][chunk kq][operand m] x 16 B
-//   X   : [unit][2] activation sums, plain and slot-offset weighted (staging only)
-//   meta: [unit][tile row j][kq] fp32 scale, zero unless kq is the unit's
-//         row block; units past the wave's range are all zero
-//   The offset term sum_u s_u (XB_u + z_u X_u) of each tile row is formed at
-//   staging and subtracted once after the main loop.
+// (Batch 1 uses units as MFMA rows and workgroup-shared staging, further down.)
 //
 // The loads are issued before the weight DMA and consumed after it.  One x task
 // = 32 activations (one chunk) of one batch row; tasks are chunk-fastest, so the
@@ -121,7 +112,7 @@ __device__ __forceinline__ void load_x(const GemvArgs& A, int b0, int ua, int nc
 // Stage one x task: its chunk sums X = sum x and XB = sum x B(p) and its four MFMA
 // operands, the activations in decode order scaled by 2^-expo (exact) to meet the
 // in-place decoded fields (the MFMA then sums x (B(p) + q)).
-template <int BITS, int MB>
+template <int BITS>
 __device__ __forceinline__ void store_x(const XTask& t, int ua, int K, int mt, char* xw, float* Xw) {
     u4* xs = reinterpret_cast<u4*>(xw);
     const int k0 = (ua * 4 + t.c) * 32;
@@ -146,13 +137,8 @@ __device__ __forceinline__ void store_x(const XTask& t, int ua, int K, int mt, c
     const int ul = t.c >> 2, kq = t.c & 3;
     if (!t.real) return;
     if (kq == 0) {
-        if constexpr (MB == 1) {
-            Xw[ul * 2] = sum;
-            Xw[ul * 2 + 1] = sumb;
-        } else {
-            Xw[ul * 32 + t.i] = sum;
-            Xw[ul * 32 + 16 + t.i] = sumb;
-        }
+        Xw[ul * 32 + t.i] = sum;
+        Xw[ul * 32 + 16 + t.i] = sumb;
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -162,8 +148,7 @@ __device__ __forceinline__ void store_x(const XTask& t, int ua, int K, int mt, c
             constexpr float kScale[6] = {1.f, 0.5f, 0.25f, 0.125f, 0.0625f, 0.03125f};
             op[p] = xv[Decode<BITS>::kappa(8 * m + p)] * (_Float16)kScale[Decode<BITS>::expo(8 * m + p)];
         }
-        if constexpr (MB == 1) xs[(ul * 4 + kq) * 4 + m] = *reinterpret_cast<u4*>(&op);
-        else xs[((ul * 4 + m) * 4 + kq) * mt + t.i] = *reinterpret_cast<u4*>(&op);
+        xs[((ul * 4 + m) * 4 + kq) * mt + t.i] = *reinterpret_cast<u4*>(&op);
     }
 }
 
@@ -217,96 +202,135 @@ __device__ __forceinline__ void store_meta(const GemvArgs& A, const MetaRegs& m,
     }
 }
 
-// unit-row layout: the masked fp32 scales of units up to npad (zero past my), and
-// this lane's share of its tile row's zero-point term
-__device__ __forceinline__ float store_meta_units(const GemvArgs& A, const MetaRegs& m, int tile, int my, int npad,
-                                                  int e0, int lane, const float* Xw, float* meta) {
-    const bool row_ok = tile * 16 + (lane & 15) < A.V;
-    float corr = 0.f;
+// ------------------------------------------------------------------ batch 1: workgroup-shared staging
+// At batch 1 the waves of a job share the staged activations and scales (LDS
+// offsets in GemvArgs, sizes per unit of the job's K split):
+//   x    groups of 16 units (one MFMA activation operand), 4 KB each, fetched and
+//        converted by wave g mod NW, one chunk per lane; within a group operand m
+//        of chunk kq of unit u sits at slot (kq * 4 + m) * 16 + ((u + 4 kq) & 15)
+//        (16 B slots), so the 16 units a lane group reads or writes together fill
+//        16 distinct bank groups
+//   sums [unit][2] fp32: sum x and sum x B(p) of each unit
+//   tab  [unit][tile row j][kq] fp32 masked scales: the scale of (unit, row) in
+//        slot kq = (unit >> 2) & 3, zero in the other slots, for units past the
+//        split and for rows past V
+//   raw  each tile row's span of (scale, zero) halves for the split's groups,
+//        [tensor][tile row][piece] x 16 B, fetched as 16-byte pieces aligned to
+//        16 bytes (the host checks the scale and zero tensors are 16-byte
+//        aligned, so a piece never crosses a page and its first byte is inside
+//        the tensor)
+// Raw activations and spans arrive by direct-to-LDS loads issued before the
+// weight ring, so the staging runs while the weights stream.
+
+// Workgroup barrier after this wave's LDS traffic (no vmcnt wait: the weight ring
+// stays in flight).
+__device__ __forceinline__ void barrier_lds() {
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+}
+
+// Raw activations of unit group g (16 units, 4 KB) -> x + 4096 g.  The buffer
+// descriptor spans x[0, K), so pieces past K arrive as zeros.
+__device__ __forceinline__ void dma_x_group(__amdgpu_buffer_rsrc_t xr, int u0, int g, int lane, char* xo) {
+    const int voff = (u0 + 16 * g) * 256 + 16 * lane;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int ul = e0 + (lane >> 4) + 4 * e;
-        if (ul < npad) {
-            float sv = 0.f;
-            if (ul < my && row_ok) {
-                sv = (float)m.s[e];
-                corr = fmaf(sv, fmaf((float)m.z[e], Xw[ul * 2], Xw[ul * 2 + 1]), corr);
-            }
-            const int blk = (ul >> 2) & 3;
-            const f4 v = {blk == 0 ? sv : 0.f, blk == 1 ? sv : 0.f, blk == 2 ? sv : 0.f, blk == 3 ? sv : 0.f};
-            *reinterpret_cast<f4*>(meta + (ul * 16 + (lane & 15)) * 4) = v;
+    for (int t = 0; t < 4; ++t)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(xo + g * 4096 + t * 1024), 16, voff, t * 1024, 0, 0);
+}
+
+// Convert group g in place: lane c holds chunk c (unit c >> 2, chunk c & 3) and
+// writes its four operands to their slots, and lane 4u the sums of unit u.  Every
+// lane's raw reads precede every write (one wave, in-order LDS).
+template <int BITS>
+__device__ __forceinline__ void stage_x_group(char* xo, float* sums, int g, int lane) {
+    u4* grp = reinterpret_cast<u4*>(xo + g * 4096);
+    const u4* blk = grp + lane * 4;
+    _Float16 xv[32];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const h8 v = *reinterpret_cast<const h8*>(blk + q);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[8 * q + e] = v[e];
+    }
+    const h2 one2 = {(_Float16)1.f, (_Float16)1.f};
+    float sum = 0.f, sumb = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; e += 2) {
+        const h2 pr = {xv[e], xv[e + 1]};
+        sum = __builtin_amdgcn_fdot2(pr, one2, sum, false);
+        const h2 ps = {xv[Decode<BITS>::kappa(e)], xv[Decode<BITS>::kappa(e + 1)]};
+        const h2 bs = {(_Float16)slot_offset(Decode<BITS>::expo(e)), (_Float16)slot_offset(Decode<BITS>::expo(e + 1))};
+        sumb = __builtin_amdgcn_fdot2(ps, bs, sumb, false);
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sumb += __shfl_xor(sumb, 1, 64);
+    sumb += __shfl_xor(sumb, 2, 64);
+    if ((lane & 3) == 0) {
+        sums[(16 * g + (lane >> 2)) * 2] = sum;
+        sums[(16 * g + (lane >> 2)) * 2 + 1] = sumb;
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        h8 op;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            constexpr float kScale[6] = {1.f, 0.5f, 0.25f, 0.125f, 0.0625f, 0.03125f};
+            op[p] = xv[Decode<BITS>::kappa(8 * m + p)] * (_Float16)kScale[Decode<BITS>::expo(8 * m + p)];
         }
+        const int u = lane >> 2, kq = lane & 3;
+        grp[(kq * 4 + m) * 16 + ((u + 4 * kq) & 15)] = *reinterpret_cast<u4*>(&op);
     }
-    return corr;
 }
 
-// ------------------------------------------------------------------ batch 1: staging by LDS-DMA
-// At batch 1 the activations and the (scale, zero) pairs travel HBM -> LDS by
-// direct-to-LDS loads like the weights, so no register load stands between the
-// kernel start and the weight stream and the first stage's math waits only for
-// its own data (an exact vmcnt; the compiler would wait for the whole ring).
-//
-// x: piece p (unit p >> 4, 16-byte piece p & 15 of the unit) -> xs + 16 p, read from
-// a clamped, valid address; a task converts its own 64 bytes in place.
-__device__ __forceinline__ int dma_x1(const GemvArgs& A, int ua, int npad, int lane, char* xs) {
-    const char* xb = reinterpret_cast<const char*>(A.x);
-    const int last = A.K * 2 - 16;
-    const int n = npad >> 2;                  // 64 pieces = 4 units per instruction
-    for (int t = 0; t < n; ++t) {
-        const char* src = xb + min(ua * 256 + 1024 * t + 16 * lane, last);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), (lds_void*)(xs + t * 1024), 16, 0, 0);
-    }
-    return n;
-}
-
-// meta: entry e = j * my + ul (tile row j, unit ul): its scale and zero land
-// zero-extended in the dwords at sraw + 4e and zraw + 4e (the 2-byte LDS-DMA
-// writes one dword per lane); lanes past 16 my re-read the last entry into the
-// padding.  Returns the number of DMA instructions issued.
+// The raw spans: lane L of the job's 32 * np lanes fetches piece L % np of the
+// span of tensor (L / np) >> 4 (0 scales, 1 zeros), tile row (L / np) & 15, to
+// raw + 16 L; pieces past the span re-read its last piece.  Instruction i is
+// issued by wave i mod NW.
 template <int MODE>
-__device__ __forceinline__ int dma_meta1(const GemvArgs& A, int tile, int ua, int my, int lane, char* sraw,
-                                         char* zraw) {
-    const int n = 16 * my, ni = (n + 63) >> 6;
-    const float rmy = 1.f / (float)my;
-    for (int t = 0; t < ni; ++t) {
-        const int e = min(64 * t + lane, n - 1);
-        // e / my for e < 1024, my <= 16: the float quotient of (e + 0.5) is at least
-        // 1 / 32 away from an integer, far beyond its rounding error
-        const int j = (int)(((float)e + 0.5f) * rmy), ul = e - j * my;
+__device__ __forceinline__ void dma_spans(const GemvArgs& A, int tile, int g0, int g1, int wave, int lane,
+                                          char* raw) {
+    const int np = A.raw_np, nl = 32 * np;
+    for (int i = wave; i * 64 < nl; i += A.nw) {
+        const int L = min(i * 64 + lane, nl - 1);
+        const int tr = (int)fdiv((uint32_t)L, A.divNP);
+        const int k = L - tr * np;
         const uint32_t* w;
         const _Float16 *s, *z;
-        tile_row<MODE>(A, tile * 16 + j, w, s, z);
-        const int g = (int)fdiv((uint32_t)(ua + ul), A.divG);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(s + g), (lds_void*)(sraw + t * 256), 2, 0, 0);
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(z + g), (lds_void*)(zraw + t * 256), 2, 0, 0);
+        tile_row<MODE>(A, tile * 16 + (tr & 15), w, s, z);
+        const uintptr_t row = reinterpret_cast<uintptr_t>(tr >> 4 ? z : s);
+        const uintptr_t first = (row + 2 * g0) & ~(uintptr_t)15, last = (row + 2 * g1) & ~(uintptr_t)15;
+        const uintptr_t piece = min(first + 16 * (uintptr_t)k, last);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(piece), (lds_void*)(raw + i * 1024), 16, 0, 0);
     }
-    return 2 * ni;
 }
 
-// Masked fp32 scales from the staged raw pairs, and this lane's share of its tile
-// row's offset term.  All reads come before the first write: the raw pairs and
-// sums sit inside the scale area being written (one pass, my <= 16).
-__device__ __forceinline__ float stage_meta1(const GemvArgs& A, int tile, int my, int npad, int lane,
-                                             const uint32_t* sraw, const uint32_t* zraw, const float* Xw,
-                                             float* meta) {
+// Masked scales of this wave's table entries (passes e0 = 64 (wave + NW i) over
+// the 64 * nstg entries of the job; lane l takes entry e0 + l, tile row l & 15),
+// and this lane's share of its tile row's offset term sum_u s (z X_u + XB_u).
+template <int MODE>
+__device__ __forceinline__ float stage_tab(const GemvArgs& A, int tile, int u0, int u1, int g0, int nstg, int wave,
+                                           int lane, const char* raw, const float* sums, float* tab) {
     const int j = lane & 15;
     const bool row_ok = tile * 16 + j < A.V;
-    float sv[4], corr = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int ul = (lane >> 4) + 4 * e;
-        const int uc = min(ul, my - 1);
-        const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)sraw[j * my + uc]);
-        const float zc = (float)__builtin_bit_cast(_Float16, (uint16_t)zraw[j * my + uc]);
-        sv[e] = (ul < my && row_ok) ? sc : 0.f;
-        corr = fmaf(sv[e], fmaf(zc, Xw[uc * 2], Xw[uc * 2 + 1]), corr);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int ul = (lane >> 4) + 4 * e;
-        const int blk = (ul >> 2) & 3;
-        const f4 v = {blk == 0 ? sv[e] : 0.f, blk == 1 ? sv[e] : 0.f, blk == 2 ? sv[e] : 0.f, blk == 3 ? sv[e] : 0.f};
-        if (ul < npad) *reinterpret_cast<f4*>(meta + (ul * 16 + j) * 4) = v;
+    const uint32_t* w;
+    const _Float16 *s, *z;
+    tile_row<MODE>(A, tile * 16 + j, w, s, z);
+    // byte offset of group g0 within the row's first fetched piece
+    const int sa = (int)((reinterpret_cast<uintptr_t>(s) + 2 * g0) & 15);
+    const int za = (int)((reinterpret_cast<uintptr_t>(z) + 2 * g0) & 15);
+    const _Float16* sr = reinterpret_cast<const _Float16*>(raw + j * A.raw_np * 16 + sa);
+    const _Float16* zr = reinterpret_cast<const _Float16*>(raw + (16 + j) * A.raw_np * 16 + za);
+    float corr = 0.f;
+    for (int e0 = 64 * wave; e0 < 64 * nstg; e0 += 64 * A.nw) {
+        const int e = e0 + lane, u = e >> 4;
+        const int gi = (int)fdiv((uint32_t)min(u0 + u, u1 - 1), A.divG) - g0;
+        const float sc = (u0 + u < u1 && row_ok) ? (float)sr[gi] : 0.f;
+        const float zc = (float)zr[gi];
+        corr = fmaf(sc, fmaf(zc, sums[2 * u], sums[2 * u + 1]), corr);
+        const int blk = (u >> 2) & 3;
+        const f4 v = {blk == 0 ? sc : 0.f, blk == 1 ? sc : 0.f, blk == 2 ? sc : 0.f, blk == 3 ? sc : 0.f};
+        *reinterpret_cast<f4*>(tab + 4 * e) = v;
     }
     return corr;
 }
@@ -430,10 +454,11 @@ __device__ __forceinline__ void stage_math(const char* lp, const uint32_t* meta,
 }
 
 // ------------------------------------------------------------------ unit arithmetic, units as rows
-// Stage s holds units 4s .. 4s+3 of the wave: unit 4s + t is MFMA row 4 (s & 3) + t
-// of the current activation operand, so its result is register t of the lanes with
-// kq = s & 3 (the masked scales zero the other lanes).  lp / mp: the lane's ring
-// and scale addresses for the stage.
+// A stage holds units lu .. lu+3 of the split (lu a multiple of 4): unit lu + t is
+// MFMA row (lu & 15) + t of the activation operand of its group of 16 units, so its
+// result is register t of the lanes with kq = (lu >> 2) & 3 (the masked scales
+// zero the other lanes).  lp / mp: the lane's ring and scale addresses for the
+// stage.
 template <int BITS>
 __device__ __forceinline__ void stage_math_units(const char* lp, const float* mp, const u4 (&a)[4], uint32_t g,
                                                  float (&acc)[4]) {
@@ -453,8 +478,151 @@ __device__ __forceinline__ void stage_math_units(const char* lp, const float* mp
     }
 }
 
-template <int BITS, int MODE, int MB>
-__device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
+// Waits until at most n vector-memory instructions of this wave are in flight,
+// n rounded down to a multiple of 4 (waiting longer is always safe).
+__device__ __forceinline__ void wait_vm_atmost(int n) {
+    switch (min(n, 60) >> 2) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<4>(); break;
+        case 2: wait_vmcnt<8>(); break;
+        case 3: wait_vmcnt<12>(); break;
+        case 4: wait_vmcnt<16>(); break;
+        case 5: wait_vmcnt<20>(); break;
+        case 6: wait_vmcnt<24>(); break;
+        case 7: wait_vmcnt<28>(); break;
+        case 8: wait_vmcnt<32>(); break;
+        case 9: wait_vmcnt<36>(); break;
+        case 10: wait_vmcnt<40>(); break;
+        case 11: wait_vmcnt<44>(); break;
+        case 12: wait_vmcnt<48>(); break;
+        case 13: wait_vmcnt<52>(); break;
+        case 14: wait_vmcnt<56>(); break;
+        default: wait_vmcnt<60>(); break;
+    }
+}
+
+// Batch 1: job = (tile of 16 rows, K split p).  The packed bytes of the split's
+// units, kbytes per row, travel to a workgroup-shared tile in LDS as row-aligned
+// 1 KB blocks (16 * nb direct-to-LDS instructions, dealt round-robin to the
+// waves): each block is 64 consecutive 16-byte pieces of one row, so the row
+// pointer is scalar, the requests are contiguous, and pieces past the split
+// re-read its last piece.  Row j of the tile sits at j * RP with RP = 1024 nb +
+// 16, which staggers the rows over the LDS banks.
+//
+// Order: raw (scale, zero) spans and raw activations, then the tile; the shared
+// staging runs while the tile streams; one wait and barrier; then wave w takes
+// stages [nstg w / NW, nstg (w + 1) / NW) of S units from the tile and the
+// waves' row sums meet in fixed order on wave 0.
+template <int BITS, int MODE>
+__device__ __forceinline__ void run_job_units(const GemvArgs& A, int job, char* lds) {
+    constexpr int S = Ring<BITS>::S;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int NW = A.nw;
+    const int tile = (int)fdiv((uint32_t)job, A.divP);   // one batch tile at batch 1
+    const int p = job - tile * A.P;
+    const int u0 = (int)fdiv((uint32_t)(A.units * p), A.divP);
+    const int u1 = (int)fdiv((uint32_t)(A.units * (p + 1)), A.divP);
+    const int nstg = (u1 - u0 + S - 1) / S;
+    const int s0 = (int)fdiv((uint32_t)(nstg * wave), A.divW);
+    const int ns = (int)fdiv((uint32_t)(nstg * (wave + 1)), A.divW) - s0;
+    const int ngrp = (S * nstg + 15) >> 4;
+    const int rowbytes = A.C * BITS * 4;
+    const int kb0 = u0 * 16 * BITS;
+    const int kbytes = min(u1 * 16 * BITS, rowbytes) - kb0;
+    const int nb = (kbytes + 1023) >> 10;
+    const int RP = A.wave_bytes;
+    const int j = lane & 15, kq = lane >> 4;
+
+    char* xo = lds;
+    float* sums = reinterpret_cast<float*>(lds + A.sum_off);
+    float* tab = reinterpret_cast<float*>(lds + A.tab_off);
+    char* raw = lds + A.raw_off;
+    float* red = reinterpret_cast<float*>(lds + A.red_off);
+    char* tl = lds + A.ring_off;
+    const int g0 = (int)fdiv((uint32_t)u0, A.divG), g1 = (int)fdiv((uint32_t)(u1 - 1), A.divG);
+
+    // 1) raw spans, raw activations, then this wave's blocks of the tile
+    dma_spans<MODE>(A, tile, g0, g1, wave, lane, raw);
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.K * 2, 0x00020000);
+    for (int g = wave; g < ngrp; g += NW) dma_x_group(xr, u0, g, lane, xo);
+    int nt = 0;
+    {
+        int r = 0, b = wave;                              // block i = r * nb + b, i = wave mod NW
+        while (b >= nb) { b -= nb; ++r; }
+        while (r < 16) {
+            const uint32_t* w;
+            const _Float16 *sp, *zp;
+            tile_row<MODE>(A, tile * 16 + r, w, sp, zp);
+            const char* src = reinterpret_cast<const char*>(w) + kb0 + min(b * 1024 + 16 * lane, kbytes - 16);
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src), (lds_void*)(tl + r * RP + b * 1024),
+                                             16, 0, 0);
+            ++nt;
+            b += NW;
+            while (b >= nb) { b -= nb; ++r; }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2) shared staging while the tile streams
+    wait_vm_atmost(nt);
+    for (int g = wave; g < ngrp; g += NW) stage_x_group<BITS>(xo, sums, g, lane);
+    barrier_lds();
+    float corr = stage_tab<MODE>(A, tile, u0, u1, g0, nstg, wave, lane, raw, sums, tab);
+    wait_vmcnt<0>();
+    barrier_lds();
+
+    // 3) this wave's stages from the tile; the activation operand (units 16 gc ..
+    //    16 gc + 15 of the split) is reloaded when the group changes
+    float ac[4] = {0.f, 0.f, 0.f, 0.f};
+    if (ns > 0) {
+        const uint32_t g2 = magic_vreg();
+        const char* lrow = tl + j * RP + kq * 4 * BITS;
+        const float* mlane = tab + j * 4 + kq;
+        u4 a[4];
+        int gc = -1;
+        for (int k = 0; k < ns; ++k) {
+            const int lu = S * (s0 + k);                  // first unit of the stage, split-relative
+            if ((lu >> 4) != gc) {
+                gc = lu >> 4;
+                const u4* xs = reinterpret_cast<const u4*>(xo + gc * 4096) + kq * 64 + ((j + 4 * kq) & 15);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) a[m] = xs[m * 16];
+            }
+            stage_math_units<BITS>(lrow + lu * 16 * BITS, mlane + lu * 64, a, g2, ac);
+        }
+    }
+
+    // 4) per tile row: this wave's sum less its share of the offset term, then the
+    //    workgroup sum in fixed order on wave 0
+    float tot = (ac[0] + ac[1]) + (ac[2] + ac[3]);
+    tot += __shfl_xor(tot, 16, 64);
+    tot += __shfl_xor(tot, 32, 64);
+    corr += __shfl_xor(corr, 16, 64);
+    corr += __shfl_xor(corr, 32, 64);
+    if (lane < 16) red[wave * 16 + lane] = tot - corr;
+    barrier_lds();
+    if (wave == 0) {
+        const int h = lane >> 4;
+        float v = (h < NW ? red[h * 16 + j] : 0.f) + (h + 4 < NW ? red[(h + 4) * 16 + j] : 0.f);
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        const float partner = __shfl_xor(v, 1, 64);
+        const int row = tile * 16 + j;
+        if (kq == 0 && row < A.V) {
+            if (A.P == 1) epilogue<DT_F16, MODE>(A, 0, row, v, partner);
+            else A.partial[(long)p * A.V + row] = v;
+        }
+    }
+    if (job + (int)gridDim.x < A.jobs) barrier_lds();   // the LDS is reused by the next job
+}
+
+// Batch rows (M = 2..16 per batch tile): job = (batch tile, tile of 16 rows, K
+// split p); wave w owns a contiguous unit range of the split, its staged
+// activations, scales and ring in a private LDS region.
+template <int BITS, int MODE>
+__device__ __forceinline__ void run_job_rows(const GemvArgs& A, int job, char* lds) {
     using RG = Ring<BITS>;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -465,7 +633,7 @@ __device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
     const int mtile = (int)fdiv((uint32_t)rest, A.divT);
     const int tile = rest - mtile * A.ntiles;
     const int b0 = mtile * 16;
-    const int mt = MB == 1 ? 1 : min(16, A.M - b0);
+    const int mt = min(16, A.M - b0);
     const int u0 = (int)fdiv((uint32_t)(A.units * p), A.divP);
     const int u1 = (int)fdiv((uint32_t)(A.units * (p + 1)), A.divP);
     const int nu = u1 - u0;
@@ -492,121 +660,54 @@ __device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
         const int issued = max(R, nst);             // ring stages issued in all (extra slots re-read)
         const char* lring = ring + j * RG::PITCH * 16 + kq * 4 * BITS;
         int slot = 0;
-        if constexpr (MB == 1) {
-            // LDS region: xs = activation operands (raw x first), meta = masked scales,
-            // whose first half holds the raw (scale, zero) pairs and then the unit
-            // sums until the scales are written
-            const int npad = nst * RG::S;
-            float* ms = reinterpret_cast<float*>(meta);
-            char* sraw = meta;
-            char* zraw = meta + npad * 64;
-            float* Xs = reinterpret_cast<float*>(meta + npad * 128);
-
-            // 1) ring stage 0, the activations, the pairs, ring stages 1 .. R-1
-            dma_stage<BITS>(dl, ua, rowbytes, ring);
-            dma_x1(A, ua, npad, lane, xw);
-            dma_meta1<MODE>(A, tile, ua, my, lane, sraw, zraw);
+        // 1) the first activation and metadata loads into registers, then the
+        //    first R weight stages (loads before the DMA, consumed after it)
+        const int nch = 4 * my, ntask = nch * mt;
+        const bool vec = ((A.K & 7) == 0) && ((reinterpret_cast<uintptr_t>(A.x) & 15) == 0);
+        XTask xt;
+        load_x(A, b0, ua, nch, ntask, lane, vec, xt);
+        MetaRegs mr;
+        load_meta<MODE>(A, tile, ua, my, 0, lane, mr);
+        dma_stage<BITS>(dl, ua, rowbytes, ring);
 #pragma unroll
-            for (int r = 1; r < RG::RMAX; ++r)
-                if (r < R) dma_stage<BITS>(dl, ua + r * RG::S, rowbytes, ring + r * RG::SLOT);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int r = 1; r < RG::RMAX; ++r)
+            if (r < R) dma_stage<BITS>(dl, ua + r * RG::S, rowbytes, ring + r * RG::SLOT);
+        __builtin_amdgcn_sched_barrier(0);
 
-            // 2) staging once stage 0, x and the pairs have landed
-            wait_stages<RG::NDMA>(R - 1);
-            {
-                XTask xt;
-                const int task = min(lane, 4 * my - 1);
-                const h8* blk = reinterpret_cast<const h8*>(xw + task * 64);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) xt.v[q] = blk[q];
-                xt.i = 0;
-                xt.c = task;
-                xt.real = lane < 4 * my;
-                store_x<BITS, 1>(xt, ua, A.K, 1, xw, Xs);
-            }
-            float corr = stage_meta1(A, tile, my, npad, lane, reinterpret_cast<const uint32_t*>(sraw),
-                                     reinterpret_cast<const uint32_t*>(zraw), Xs, ms);
-            corr += __shfl_xor(corr, 16, 64);
-            corr += __shfl_xor(corr, 32, 64);
+        // 2) staging; passes past the first wait for the whole ring
+        store_x<BITS>(xt, ua, A.K, mt, xw, Xw);
+        for (int t0 = 64; t0 < ntask; t0 += 64) {
+            load_x(A, b0, ua, nch, ntask, t0 + lane, vec, xt);
+            store_x<BITS>(xt, ua, A.K, mt, xw, Xw);
+        }
+        uint32_t* mp = reinterpret_cast<uint32_t*>(meta);
+        store_meta(A, mr, tile, my, 0, lane, mp);
+        for (int e0 = 16; e0 < my; e0 += 16) {
+            load_meta<MODE>(A, tile, ua, my, e0, lane, mr);
+            store_meta(A, mr, tile, my, e0, lane, mp);
+        }
 
-            // 3) the ring: stage s sits in slot s % R
-            float ac[4] = {0.f, 0.f, 0.f, 0.f};
-            u4 a[4];
-            const u4* xs = reinterpret_cast<const u4*>(xw);
-            const float* mlane = ms + j * 4 + kq;
-            for (int s = 0; s < nst; ++s) {
-                if ((s & 3) == 0) {          // activation operand of units 4s .. 4s+15
-                    const int unit = min(4 * s + j, my - 1);
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) a[m] = xs[(unit * 4 + kq) * 4 + m];
-                }
-                wait_stages<RG::NDMA>(min(R - 1, issued - 1 - s));
-                char* sp = ring + slot * RG::SLOT;
-                stage_math_units<BITS>(lring + slot * RG::SLOT, mlane + s * RG::S * 64, a, g, ac);
-                if (s + R < nst) {
-                    wait_lgkmcnt0();                // every read of this slot has returned
-                    dma_stage<BITS>(dl, ua + (s + R) * RG::S, rowbytes, sp);
-                }
-                slot = slot + 1 == R ? 0 : slot + 1;
+        // 3) the ring
+        for (int s = 0; s < nst; ++s) {
+            wait_stages<RG::NDMA>(min(R - 1, issued - 1 - s));
+            char* sp = ring + slot * RG::SLOT;
+            stage_math<BITS>(lring + slot * RG::SLOT, mp, my, xw, Xw, ua, ua + s * RG::S, ub, mt, lane, g, acc);
+            if (s + R < nst) {
+                wait_lgkmcnt0();
+                dma_stage<BITS>(dl, ua + (s + R) * RG::S, rowbytes, sp);
             }
-            float tot = (ac[0] + ac[1]) + (ac[2] + ac[3]);
-            tot += __shfl_xor(tot, 16, 64);
-            tot += __shfl_xor(tot, 32, 64);
-            acc[0] = kq == 0 ? tot - corr : 0.f;
-        } else {
-            // 1) the first activation and metadata loads into registers, then the
-            //    first R weight stages (loads before the DMA, consumed after it)
-            const int nch = 4 * my, ntask = nch * mt;
-            const bool vec = ((A.K & 7) == 0) && ((reinterpret_cast<uintptr_t>(A.x) & 15) == 0);
-            XTask xt;
-            load_x(A, b0, ua, nch, ntask, lane, vec, xt);
-            MetaRegs mr;
-            load_meta<MODE>(A, tile, ua, my, 0, lane, mr);
-            dma_stage<BITS>(dl, ua, rowbytes, ring);
-#pragma unroll
-            for (int r = 1; r < RG::RMAX; ++r)
-                if (r < R) dma_stage<BITS>(dl, ua + r * RG::S, rowbytes, ring + r * RG::SLOT);
-            __builtin_amdgcn_sched_barrier(0);
-
-            // 2) staging; passes past the first wait for the whole ring
-            store_x<BITS, MB>(xt, ua, A.K, mt, xw, Xw);
-            for (int t0 = 64; t0 < ntask; t0 += 64) {
-                load_x(A, b0, ua, nch, ntask, t0 + lane, vec, xt);
-                store_x<BITS, MB>(xt, ua, A.K, mt, xw, Xw);
-            }
-            uint32_t* mp = reinterpret_cast<uint32_t*>(meta);
-            store_meta(A, mr, tile, my, 0, lane, mp);
-            for (int e0 = 16; e0 < my; e0 += 16) {
-                load_meta<MODE>(A, tile, ua, my, e0, lane, mr);
-                store_meta(A, mr, tile, my, e0, lane, mp);
-            }
-
-            // 3) the ring
-            for (int s = 0; s < nst; ++s) {
-                wait_stages<RG::NDMA>(min(R - 1, issued - 1 - s));
-                char* sp = ring + slot * RG::SLOT;
-                stage_math<BITS>(lring + slot * RG::SLOT, mp, my, xw, Xw, ua, ua + s * RG::S, ub, mt, lane, g, acc);
-                if (s + R < nst) {
-                    wait_lgkmcnt0();
-                    dma_stage<BITS>(dl, ua + (s + R) * RG::S, rowbytes, sp);
-                }
-                slot = slot + 1 == R ? 0 : slot + 1;
-            }
+            slot = slot + 1 == R ? 0 : slot + 1;
         }
     }
 
     // cross-wave sum in fixed wave order, then the epilogue on wave 0; lane (j, kq)
     // register r holds batch row 4kq + r of tile row j
-    // (at batch 1 a wave's slot is the start of its own activation area, dead by now)
-    auto red = [&](int w) -> f4* {
-        return MB == 1 ? reinterpret_cast<f4*>(lds + w * A.wave_bytes)
-                       : reinterpret_cast<f4*>(lds + A.red_off) + (w - 1) * 64;
-    };
-    if (wave > 0) red(wave)[lane] = acc;
+    f4* red = reinterpret_cast<f4*>(lds + A.red_off);
+    if (wave > 0) red[(wave - 1) * 64 + lane] = acc;
     __syncthreads();
     if (wave == 0) {
         for (int w = 1; w < NW; ++w) {
-            const f4 o = red(w)[lane];
+            const f4 o = red[(w - 1) * 64 + lane];
             acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
         }
         const int v = tile * 16 + j;
@@ -621,6 +722,12 @@ __device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
         }
     }
     if (job + (int)gridDim.x < A.jobs) __syncthreads();   // the LDS is reused by the next job
+}
+
+template <int BITS, int MODE, int MB>
+__device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
+    if constexpr (MB == 1) run_job_units<BITS, MODE>(A, job, lds);
+    else run_job_rows<BITS, MODE>(A, job, lds);
 }
 
 template <int BITS, int MODE, int MB>
