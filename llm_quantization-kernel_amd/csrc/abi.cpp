@@ -105,7 +105,8 @@ constexpr int MFMA_TILE = 16;          // virtual rows per MFMA decode job
 constexpr int LDS_BUDGET = 160 * 1024; // dynamic LDS per decode workgroup (gfx950: 160 KB per CU)
 constexpr int WAVES_PER_CU = 8;        // decode occupancy target
 constexpr int MFMA_STAGE_UNITS = Ring<4>::S;   // units per weight-ring stage (gemv_mfma.hip)
-constexpr int MFMA_MAX_WAVES = 8;      // waves per decode workgroup (launch bound 512 threads)
+constexpr int MFMA_MAX_WAVES = 8;      // waves per decode workgroup, batch rows (launch bound 512 threads)
+constexpr int MFMA_MAX_WAVES_B1 = 16;  // ... at batch 1 (launch bound 1024 threads)
 
 bool valid_dtype(int dt) { return dt == CBK_F16 || dt == CBK_BF16 || dt == CBK_F32; }
 
@@ -175,7 +176,7 @@ LdsLayout mfma_lds(int64_t units, int P, int mt, int nw, int bits, int gs, int r
         const int64_t tab_off = sum_off + ngrp * 16 * 8;
         const int64_t raw_off = tab_off + stg * 1024;
         const int64_t red_off = raw_off + ceil_div(32 * np, 64) * 1024;
-        const int64_t ring_off = red_off + MFMA_MAX_WAVES * 16 * 4;
+        const int64_t ring_off = red_off + MFMA_MAX_WAVES_B1 * 16 * 4;
         const int64_t rp = ceil_div(nu * 16 * bits, 1024) * 1024 + 16;
         const int64_t total = ring_off + 16 * rp;
         L.sum_off = (int)sum_off;
@@ -233,7 +234,7 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
             int64_t nw = ceil_div(units_job, 2 * S);
             if ((int64_t)pl.grid * nw < (int64_t)WAVES_PER_CU * sm)
                 nw = std::min<int64_t>(ceil_div((int64_t)WAVES_PER_CU * sm, pl.grid), ceil_div(units_job, S));
-            nw = std::max<int64_t>(1, std::min<int64_t>(nw, MFMA_MAX_WAVES));
+            nw = std::max<int64_t>(1, std::min<int64_t>(nw, pl.unit_rows ? MFMA_MAX_WAVES_B1 : MFMA_MAX_WAVES));
             auto fits = [&](int w, int r) {
                 return mfma_lds(pl.units, pl.P, mt, w, bits, gs, r, pl.unit_rows).total <= LDS_BUDGET;
             };

@@ -605,7 +605,8 @@ __device__ __forceinline__ void run_job_units(const GemvArgs& A, int job, char* 
     barrier_lds();
     if (wave == 0) {
         const int h = lane >> 4;
-        float v = (h < NW ? red[h * 16 + j] : 0.f) + (h + 4 < NW ? red[(h + 4) * 16 + j] : 0.f);
+        float v = 0.f;
+        for (int w = h; w < NW; w += 4) v += red[w * 16 + j];
         v += __shfl_xor(v, 16, 64);
         v += __shfl_xor(v, 32, 64);
         const float partner = __shfl_xor(v, 1, 64);
@@ -731,7 +732,7 @@ __device__ __forceinline__ void run_job(const GemvArgs& A, int job, char* lds) {
 }
 
 template <int BITS, int MODE, int MB>
-__global__ void __launch_bounds__(512) gemv_mfma_kernel(const GemvArgs A) {
+__global__ void __launch_bounds__(MB == 1 ? 1024 : 512) gemv_mfma_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     for (int job = blockIdx.x; job < A.jobs; job += gridDim.x) run_job<BITS, MODE, MB>(A, job, lds);
 }
@@ -739,7 +740,7 @@ __global__ void __launch_bounds__(512) gemv_mfma_kernel(const GemvArgs A) {
 // Mixed-width fused QKV: every 16-row tile lies inside one projection (the host
 // checks nq and nk are multiples of 16), so the width is uniform per job.
 template <int MB>
-__global__ void __launch_bounds__(512) gemv_mfma_qkv_mixed_kernel(const GemvArgs A) {
+__global__ void __launch_bounds__(MB == 1 ? 1024 : 512) gemv_mfma_qkv_mixed_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     for (int job = blockIdx.x; job < A.jobs; job += gridDim.x) {
         const int rest = (int)fdiv((uint32_t)job, A.divP);
