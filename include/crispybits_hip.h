@@ -17,7 +17,9 @@
  *   - bias: [N] or NULL ("no bias" is an empty tensor in the reference, host_utils.h:80-81).
  *   - act: CBK_ACT_NONE / CBK_ACT_RELU / CBK_ACT_SILU (ops.py:24, common.cuh:10).
  *   - rho <= 0: one workgroup per job; rho > 0: min(jobs, rho * CUs) persistent
- *     workgroups (host_utils.h:90-93).
+ *     workgroups (host_utils.h:90-93).  The fp16 batch-1 decode path always runs one
+ *     workgroup per job (its workgroups gain nothing from persistence); rho is a
+ *     launch-shape hint and never changes results.
  *   - workspace: the caller's int32[2] job-queue word pair (host_utils.h:38-47).  Jobs are
  *     distributed statically here, so the workspace is accepted, never written, and its
  *     [0,0] contract holds trivially.  May be NULL.

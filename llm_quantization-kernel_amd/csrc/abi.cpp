@@ -229,7 +229,10 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
         for (pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, pl.units));; ++pl.P) {
             const int64_t jobs = (int64_t)pl.mtiles * pl.ntiles * pl.P;
             pl.jobs = (int)jobs;
-            pl.grid = (int)(rho > 0 ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm)) : jobs);
+            // batch 1 runs one workgroup per job whatever rho asks: its workgroup does
+            // not overlap consecutive jobs, so persistence only serialises them
+            pl.grid = (int)(rho > 0 && !pl.unit_rows ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm))
+                                                     : jobs);
             const int64_t units_job = std::max<int64_t>(ceil_div(pl.units, pl.P), 1);
             int64_t nw = ceil_div(units_job, 2 * S);
             if ((int64_t)pl.grid * nw < (int64_t)WAVES_PER_CU * sm)
