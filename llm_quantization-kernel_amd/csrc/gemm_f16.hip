@@ -4,37 +4,40 @@
 // activations, with the reference's weight rounding W-hat = RN_fp16((q - z) * s)
 // (packed_gemm.cu:56,60).
 //
-// Tile: 128 x 128 outputs per workgroup of eight waves in two roles, one of each
-// per SIMD:
-//   consumers (waves 0-3): stream the activation tile HBM -> LDS with
-//     direct-to-LDS loads AHEAD stages ahead (explicit vmcnt waits), and run a
-//     2 x 2 grid of 64 x 64 wave tiles, each 2 x 2 blocks of
-//     v_mfma_f32_32x32x16_f16 with fp32 accumulation -- the 32x32 instruction
-//     keeps the matrix core busy from a single wave, where 16x16 ones stall on
-//     issue;
-//   producers (waves 4-7): load the packed words and (scale, zero) of a
-//     (column, chunk) per thread into a 3-stage register ring (plain vector
-//     loads: these waves issue no direct-to-LDS loads, so the compiler's waits
-//     stay exact) and dequantize stage s+2 into LDS while the consumers multiply
-//     stage s.
-// K runs in stages of 64 codes (two 32-code chunks); one barrier per stage.  The
-// consumers multiply stage s from registers while they read stage s+1's operands
-// from LDS, so the LDS latency hides behind the matrix core.
+// Tile: 128 x 128 outputs per workgroup of six waves.  All global traffic is
+// direct-to-LDS loads issued by two loader waves; the four compute waves read LDS
+// only, so their waits are LDS counts the compiler tracks exactly.
+//   activation loader (wave 4): the activation tile, 128 rows x 64 codes per stage,
+//     into a ring of NSTAGE stages (16 instructions of 1 KB per stage, XOR-swizzled
+//     16-byte pieces: piece p of row r at slot r * 8 + (p ^ ((r >> 1) & 7))),
+//     NSTAGE - 1 stages ahead; one workgroup barrier publishes each stage.
+//   weight loader (wave 5): the packed tile in blocks of WBLK stages (256 codes =
+//     8 chunks of each of the 128 rows), double-buffered one block ahead.  A row's
+//     block is fetched as the 16-byte-aligned pieces that cover it (its start has
+//     phase (row address & 15) within the first), with an odd piece count per row
+//     as the LDS pitch, so the compute lanes' reads of 32 rows are free of bank
+//     conflicts.  Scales and zeros likewise: per row and tensor a 32-byte aligned
+//     span holding the 8 groups of a window (gs / 32 blocks), double-buffered.
+//     Aligned pieces never straddle a page, so a piece holding any valid byte is
+//     readable; pieces wholly past a tensor's end re-read its last piece.
+//   compute (waves 0-3, a 2 x 2 grid of 64 x 64 wave tiles): each wave reads its
+//     activation operands and its columns' packed chunks from LDS and dequantizes
+//     the chunks straight into the B operands of v_mfma_f32_32x32x16_f16; the
+//     dequantized tile never touches LDS.
 //
-// Activation stage: 128 rows x 64 codes, 16-byte pieces into an XOR-swizzled tile
-// (piece p of row r at slot r*8 + (p ^ ((r >> 1) & 7))), so the MFMA operand reads
-// of 16 consecutive rows hit 16 distinct groups of 4 banks.  The dequantized B
-// tile uses the same layout, in natural k order:
-//   fast path (integer zero point, as the reference quantizer produces): the
-//   codes of a pair are OR-ed into 0x6400 (1024 + q, exact), then
-//   (h - (1024 + z)) * s in packed fp16 -- the difference is an exact integer and
-//   the product rounds once, exactly RN_fp16((q - z) * s);
-//   other zero points: (q - z) * s in fp32, rounded to fp16 (the reference's
-//   fp32 arithmetic).
-// Codes at k >= K dequantize to zero, so the clamped activation reads past K
-// contribute nothing.
+// Weight rounding: the codes of a pair are OR-ed into 0x6400 (1024 + q, exact),
+// then (h - (1024 + z)) * s in packed fp16 when every zero point of the tile is an
+// integer below 1024 in magnitude (the reference quantizer's; the weight loader
+// scans the tile's zeros once): the difference is an exact integer and the product
+// rounds once, exactly RN_fp16((q - z) * s).  Other zero points take the fp32
+// product.  Codes at k >= K dequantize to zero, so the clamped activation reads and
+// the tail of the last weight block contribute nothing.
 //
-// LDS: 4 activation stages (64 KB) + 3 B tiles (48 KB).
+// MFMA operand lane map (32x32x16): lane (r = lane & 31, h = lane >> 5) holds
+// row / column r and 8 k-values of the step.  The k order within a stage is free
+// as long as both operands use it: step ks of a stage gives lane half h the codes
+// 32 h + 8 ks .. +7 (octet ks of chunk 2 s + h), so each compute lane needs one
+// packed chunk and one (scale, zero) pair per column per stage.
 #include "cbk_decode.hpp"
 #include "cbk_device.hpp"
 #include "cbk_kernels.hpp"
@@ -43,24 +46,37 @@ namespace cbk {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f16x __attribute__((ext_vector_type(16)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16x __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int NSTAGE = 4;                    // activation buffers: stages s .. s+3 live
-constexpr int AHEAD = 3;                     // activation stages issued ahead of the one computed
-constexpr int THREADS = 512;                 // 4 consumer + 4 producer waves
-constexpr int TILE = BM * BK * 2;            // bytes of an activation stage or a B tile (16 KB)
-constexpr int NB = 3;                        // B tiles: stage s (in registers), s+1 (read), s+2 (written)
-constexpr int A_OFF = 0;
-constexpr int B_OFF = NSTAGE * TILE;
-constexpr int LDS_BYTES = B_OFF + NB * TILE;
-constexpr int A_ISSUE = 4;                   // activation loads per consumer wave per stage
+constexpr int NSTAGE = 6;                    // activation stages in LDS
+constexpr int THREADS = 448;                 // 4 compute waves + 2 activation loaders + 1 weight loader
+constexpr int TILE = BM * BK * 2;            // bytes of an activation stage (16 KB)
+constexpr int A_INSTR = TILE / 1024 / 2;     // instructions per activation loader per stage
+constexpr int WBLK = 4;                      // stages per weight block
+constexpr int SZG = 8;                       // groups per scale / zero window
+constexpr int SZ_INSTR = 2 * BN * 2 / 64;    // window: [tensor][row] x two 16-byte pieces
+constexpr int SZ_BUF = 2 * BN * 32;
 
-// 16-byte slot of piece p (0..7) of tile row r: r * 8 + (p ^ swz(r))
+// Weight block geometry: a row's block is 32 * BITS bytes at phase 0 (W4), 0 / 8
+// (W2) or 0 / 4 / 8 / 12 (W3) within its first aligned piece.
+template <int BITS> struct WGeo {
+    static constexpr int PPR = BITS == 4 ? 9 : (BITS == 3 ? 7 : 5);   // pieces per row, odd
+    static constexpr int PITCH = 16 * PPR;
+    static constexpr int BUF = BN * PITCH;
+    static constexpr int INSTR = BN * PPR / 64;
+};
+
+constexpr int A_OFF = 0;
+constexpr int W_OFF = NSTAGE * TILE;
+template <int BITS> constexpr int SZ_OFF = W_OFF + 2 * WGeo<BITS>::BUF;
+template <int BITS> constexpr int FLAG_OFF = SZ_OFF<BITS> + 2 * SZ_BUF;   // tile zeros allow the fp16 form
+template <int BITS> constexpr int LDS_BYTES = FLAG_OFF<BITS> + 16;
+
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
 template <int N>
@@ -70,155 +86,368 @@ __device__ __forceinline__ void vmcnt() {
 }
 
 // Workgroup barrier without a memory fence: __syncthreads() would make the compiler
-// wait for every in-flight direct-to-LDS load (vmcnt(0)), draining the prefetch.
-// The stage waits are explicit (wait_groups); this only completes the wave's own
-// LDS writes (lgkmcnt(0)) before the barrier.
+// wait for every in-flight load of the wave (vmcnt(0)), draining the prefetch.
+// This only completes the wave's own LDS traffic (lgkmcnt(0)) before the barrier.
 __device__ __forceinline__ void barrier_lds() {
     __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));    // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
 }
 
+__device__ __forceinline__ void dma16(const void* g, char* lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+}
 
-// Activation sources of a consumer wave (cw = 0..3), fixed for the whole K loop:
-// slot q = 256 cw + 64 t + lane -> row q >> 3, logical piece (q & 7) ^ swz(row).
-struct ASrc {
-    const _Float16* a[A_ISSUE];   // activation row (clamped to M)
-    int ak[A_ISSUE];              // k of the piece within a stage
+// ------------------------------------------------------------------ activation loader
+// Loader wave h moves instructions t = 8 h .. 8 h + 7 of each stage; lane l of
+// instruction t moves slot q = 64 t + l: row q >> 3, logical piece (q & 7) ^ swz(row).
+// The loads go through a buffer descriptor over the activations: the lane's offset
+// (row clamped to M, piece) is fixed, the stage's column offset is a scalar, so a
+// stage costs no VALU.  Pieces past K read on into the next row (or, past the
+// tensor, zero), which meets zero weights -- except in the last stage, where they
+// re-read the row's own last piece so that no other row's values enter the sums.
+struct ALoader {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int voff[A_INSTR];
+    int rowoff[A_INSTR];          // byte offset of the lane's row
+    int pk[A_INSTR];              // k of the lane's piece within a stage
+    int t0;                       // first instruction of this loader
 };
 
-__device__ __forceinline__ void a_setup(const GemmArgs& A, int m0, int cw, int lane, ASrc& d) {
-    const _Float16* x = reinterpret_cast<const _Float16*>(A.x);
+__device__ __forceinline__ void a_setup(const GemmArgs& A, int m0, int half, int lane, ALoader& d) {
+    d.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * 2, 0x00020000);
+    d.t0 = A_INSTR * half;
 #pragma unroll
-    for (int t = 0; t < A_ISSUE; ++t) {
-        const int q = 256 * cw + 64 * t + lane;
+    for (int i = 0; i < A_INSTR; ++i) {
+        const int q = 64 * (d.t0 + i) + lane;
         const int r = q >> 3, p = (q & 7) ^ swz(r);
-        d.a[t] = x + (long)min(m0 + r, A.M - 1) * A.K;
-        d.ak[t] = 8 * p;
+        d.rowoff[i] = min(m0 + r, A.M - 1) * A.K * 2;
+        d.pk[i] = 8 * p;
+        d.voff[i] = d.rowoff[i] + 16 * p;
     }
 }
 
-// Issue activation stage s into slot `buf` (this wave's quarter).  Pieces past K
-// re-read a valid piece (their codes dequantize to zero); a stage past the last is
-// issued as the last one, into a slot whose stage is consumed, so every iteration
-// issues A_ISSUE loads and the waits are constants.
-__device__ __forceinline__ void issue_a(const GemmArgs& A, const ASrc& d, int s, int buf, char* lds, int cw, int nst) {
+// Stage s into slot s % NSTAGE; a stage past the last is issued as the last one,
+// so every iteration issues A_INSTR loads and the waits are constants.
+__device__ __forceinline__ void issue_a(const GemmArgs& A, const ALoader& d, int s, int nst, char* lds) {
+    char* dst = lds + A_OFF + (s % NSTAGE) * TILE + d.t0 * 1024;
     s = min(s, nst - 1);
-    char* abase = lds + A_OFF + buf * TILE + 256 * cw * 16;
+    if (s == nst - 1 && A.K % BK != 0) {
 #pragma unroll
-    for (int t = 0; t < A_ISSUE; ++t)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(d.a[t] + min(BK * s + d.ak[t], A.K - 8)),
-                                         (lds_void*)(abase + 64 * t * 16), 16, 0, 0);
-}
-
-// Packed words and (scale, zero) of one (column, chunk) of a stage, in registers.
-template <int BITS>
-struct WRegs {
-    uint32_t w[BITS];
-    _Float16 s, z;
-};
-
-template <int BITS>
-__device__ __forceinline__ void load_w(const GemmArgs& A, const uint32_t* wrow, const _Float16* srow,
-                                       const _Float16* zrow, int s, int c, WRegs<BITS>& r) {
-    const int chunk = min(2 * s + c, A.C - 1);
-    const uint32_t* p = wrow + chunk * BITS;
-#pragma unroll
-    for (int d = 0; d < BITS; ++d) r.w[d] = p[d];
-    const int g = (int)fdiv((uint32_t)(chunk * 32), A.divG);
-    r.s = srow[g];
-    r.z = zrow[g];
-}
-
-// ------------------------------------------------------------------ natural-order decode
-// h[i] = (1024 + code 2i, 1024 + code 2i+1) as packed fp16 bit patterns (g = 0x64006400
-// in a VGPR, so each pair is one v_and_or_b32 after its byte/bit placement).
-template <int BITS> struct NatDecode;
-
-template <> struct NatDecode<4> {
-    static __device__ __forceinline__ void run(const uint32_t (&w)[4], uint32_t (&h)[16], uint32_t g) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t v = w[t] >> 4;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                // byte b of w (code 8t+2b in its low nibble) and of w >> 4 (code 8t+2b+1)
-                const uint32_t sel = (uint32_t)b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
-                h[4 * t + b] = (__builtin_amdgcn_perm(v, w[t], sel) & 0x000F000Fu) | g;
-            }
-        }
-    }
-};
-
-template <> struct NatDecode<2> {
-    static __device__ __forceinline__ void run(const uint32_t (&w)[2], uint32_t (&h)[16], uint32_t g) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const uint32_t v0 = w[t], v2 = w[t] >> 2, v4 = w[t] >> 4, v6 = w[t] >> 6;
-#pragma unroll
-            for (int pr = 0; pr < 8; ++pr) {
-                // codes 2pr, 2pr+1 of the word sit at bits 4pr and 4pr + 2
-                const uint32_t b = (uint32_t)(pr >> 1);
-                const uint32_t sel = b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
-                const uint32_t lo = (pr & 1) ? v4 : v0, hi = (pr & 1) ? v6 : v2;
-                h[8 * t + pr] = (__builtin_amdgcn_perm(hi, lo, sel) & 0x00030003u) | g;
-            }
-        }
-    }
-};
-
-template <> struct NatDecode<3> {
-    static __device__ __forceinline__ void run(const uint32_t (&w)[3], uint32_t (&h)[16], uint32_t g) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            // codes 2i, 2i+1 at chunk bits 6i .. 6i+5
-            const int bit = 6 * i, wi = bit >> 5, off = bit & 31;
-            uint32_t a;
-            if (off == 0) a = w[wi];
-            else if (wi + 1 < 3) a = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], off);
-            else a = w[wi] >> off;
-            const uint32_t pair = (a & 0x0000FFFFu) | ((a << 13) & 0xFFFF0000u);   // v_bfi
-            h[i] = (pair & 0x00070007u) | g;
-        }
-    }
-};
-
-// Dequantize the (column n, chunk c) of stage s held in registers into B tile `bbuf`.
-template <int BITS>
-__device__ __forceinline__ void dequant(const GemmArgs& A, const WRegs<BITS>& r, int s, int n, int c, int bbuf,
-                                        char* lds) {
-    uint32_t h[16];
-    NatDecode<BITS>::run(r.w, h, magic_vreg());
-    uint32_t o[16];
-    const float zf = (float)r.z;
-    if (zf == __builtin_rintf(zf) && __builtin_fabsf(zf) < 1024.f) {
-        const _Float16 cz = (_Float16)(1024.f + zf);          // exact: an integer below 2048
-        const h2 c2 = {cz, cz}, s2 = {r.s, r.s};
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const h2 v = (__builtin_bit_cast(h2, h[i]) - c2) * s2;
-            o[i] = __builtin_bit_cast(uint32_t, v);
-        }
+        for (int i = 0; i < A_INSTR; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rsrc, (lds_void*)(dst + i * 1024), 16,
+                                                     d.rowoff[i] + 2 * min(BK * s + d.pk[i], A.K - 8), 0, 0, 0);
     } else {
-        const float sf = (float)r.s;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float lo = ((float)(h[i] & 0x3FFu) - zf) * sf;
-            const float hi = ((float)((h[i] >> 16) & 0x3FFu) - zf) * sf;
-            const h2 v = {(_Float16)lo, (_Float16)hi};
-            o[i] = __builtin_bit_cast(uint32_t, v);
+        for (int i = 0; i < A_INSTR; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rsrc, (lds_void*)(dst + i * 1024), 16, d.voff[i], BK * 2 * s,
+                                                     0, 0);
+    }
+}
+
+// ------------------------------------------------------------------ weight loader
+// Block j of the tile into buffer j & 1: lane l of instruction t moves piece
+// q = 64 t + l, row q / PPR, piece q % PPR of the row's aligned span.  Scale /
+// zero window w: instruction t < 4 the scales, else the zeros; lane l moves piece
+// q & 1 of tile row (q >> 1) & 127's span, the 16 halves from floor8(col * G) + 8 w
+// (floor8(col * G + 8 w), as 8 w is a multiple of 8).  Buffer descriptors over the
+// packed words, scales and zeros: the lane's offsets are fixed and the block /
+// window offset is a scalar; reads past a tensor return zero (they are never used).
+template <int BITS>
+struct WLoader {
+    __amdgpu_buffer_rsrc_t wr, sr, zr;
+    int woff[WGeo<BITS>::INSTR];
+    int szoff[SZ_INSTR];
+};
+
+template <int BITS>
+__device__ __forceinline__ void w_setup(const GemmArgs& A, int n0, int lane, WLoader<BITS>& d) {
+    using G = WGeo<BITS>;
+    d.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(A.w), (short)0, A.N * A.wpr * 4, 0x00020000);
+    d.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.s), (short)0, A.N * A.G * 2, 0x00020000);
+    d.zr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.z), (short)0, A.N * A.G * 2, 0x00020000);
+#pragma unroll
+    for (int t = 0; t < G::INSTR; ++t) {
+        const int q = 64 * t + lane;
+        const int r = q / G::PPR, p = q - r * G::PPR;
+        d.woff[t] = ((min(n0 + r, A.N - 1) * A.wpr * 4) & ~15) + 16 * p;
+    }
+#pragma unroll
+    for (int t = 0; t < SZ_INSTR; ++t) {
+        const int q = 64 * t + lane;
+        const int r = (q >> 1) & (BN - 1), p = q & 1;
+        d.szoff[t] = ((min(n0 + r, A.N - 1) * A.G) & ~7) * 2 + 16 * p;
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ void issue_w(const WLoader<BITS>& d, int j, char* lds) {
+    using G = WGeo<BITS>;
+    char* dst = lds + W_OFF + (j & 1) * G::BUF;
+#pragma unroll
+    for (int t = 0; t < G::INSTR; ++t)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.wr, (lds_void*)(dst + t * 1024), 16, d.woff[t], j * (32 * BITS), 0,
+                                                 0);
+}
+
+template <int BITS>
+__device__ __forceinline__ void issue_sz(const WLoader<BITS>& d, int w, char* lds) {
+    char* dst = lds + SZ_OFF<BITS> + (w & 1) * SZ_BUF;
+#pragma unroll
+    for (int t = 0; t < SZ_INSTR; ++t)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(t < SZ_INSTR / 2 ? d.sr : d.zr, (lds_void*)(dst + t * 1024), 16,
+                                                 d.szoff[t], 2 * SZG * w, 0, 0);
+}
+
+__device__ __forceinline__ _Float16 half_of(uint32_t v) {
+    return __builtin_bit_cast(_Float16, (uint16_t)v);
+}
+
+// An fp16 zero point allows the packed-fp16 form: an integer below 1024 in magnitude.
+__device__ __forceinline__ bool zero_is_small_int(uint32_t zbits) {
+    const float zf = (float)half_of(zbits);
+    return zf == __builtin_rintf(zf) && __builtin_fabsf(zf) < 1024.f;
+}
+
+// Whether every zero point of tile columns [n0, min(n0 + BN, N)) -- a contiguous
+// range of the zeros tensor, whose start is 16-byte aligned -- allows the
+// packed-fp16 form.
+__device__ __forceinline__ bool scan_zeros(const GemmArgs& A, int n0, int lane) {
+    const uint16_t* z = reinterpret_cast<const uint16_t*>(A.z);
+    const long beg = (long)n0 * A.G, end = (long)min(n0 + BN, A.N) * A.G;   // beg % 8 == 0
+    bool ok = true;
+    for (long i = beg + 8 * lane; i < end; i += 8 * 64) {
+        if (i + 8 <= end) {
+            const u4 v = *reinterpret_cast<const u4*>(z + i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                ok &= zero_is_small_int(v[j] & 0xFFFFu) & zero_is_small_int(v[j] >> 16);
+        } else {
+            for (long e = i; e < end; ++e) ok &= zero_is_small_int(z[e]);
         }
     }
-    const int k0 = BK * s + 32 * c;
-    if (__builtin_expect(k0 + 32 > A.K, 0)) {                  // K % 8 == 0: pairs never straddle K
+    return __builtin_amdgcn_ballot_w64(!ok) == 0;
+}
+
+// ------------------------------------------------------------------ compute
+// The lane's packed chunk of a stage (chunk 2 s + h), of both of its columns, and
+// their scales and zeros as raw fp16 bits.
+template <int BITS>
+struct WStage {
+    uint32_t w[2][BITS];
+};
+
+struct SZ {
+    uint32_t s[2], z[2];
+};
+
+// Octet o (codes 8o .. 8o+7) of a chunk as 4 packed pairs (1024 + q, exact;
+// g = 0x64006400 in a VGPR); o is a compile-time step index.
+template <int BITS> struct Octet;
+
+template <> struct Octet<4> {
+    // word o holds codes 8o .. 8o+7 as nibbles; pair i = the two nibbles of byte i
+    static __device__ __forceinline__ void run(const uint32_t (&w)[4], int o, uint32_t g, uint32_t (&h)[4]) {
+        const uint32_t v = w[o], v4 = v >> 4;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            if (k0 + 2 * i >= A.K) o[i] = 0u;
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t ps = (uint32_t)i | (0x0Cu << 8) | ((4u + i) << 16) | (0x0Cu << 24);
+            h[i] = (__builtin_amdgcn_perm(v4, v, ps) & 0x000F000Fu) | g;
+        }
     }
-    u4* bt = reinterpret_cast<u4*>(lds + B_OFF + bbuf * TILE);
+};
+
+template <> struct Octet<2> {
+    // word o >> 1 holds codes 16 (o >> 1) .. +15 at bits 2j; octet o is its half o & 1
+    static __device__ __forceinline__ void run(const uint32_t (&w)[2], int o, uint32_t g, uint32_t (&h)[4]) {
+        const uint32_t v0 = w[o >> 1] >> (16 * (o & 1));
+        const uint32_t v2 = v0 >> 2, v4 = v0 >> 4, v6 = v0 >> 6;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int p = 4 * c + j;
-        bt[n * 8 + (p ^ swz(n))] = u4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+        for (int i = 0; i < 4; ++i) {
+            // codes 2i, 2i+1 at bits 4i and 4i + 2
+            const uint32_t b = (uint32_t)(i >> 1);
+            const uint32_t ps = b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
+            const uint32_t lo = (i & 1) ? v4 : v0, hi = (i & 1) ? v6 : v2;
+            h[i] = (__builtin_amdgcn_perm(hi, lo, ps) & 0x00030003u) | g;
+        }
+    }
+};
+
+template <> struct Octet<3> {
+    // octet o = chunk bits 24o .. 24o+23 (octets 1 and 2 straddle words); pair i at
+    // bits 6i .. 6i+5 of it
+    static __device__ __forceinline__ void run(const uint32_t (&w)[3], int o, uint32_t g, uint32_t (&h)[4]) {
+        const uint32_t a = o == 0 ? w[0]
+                         : o == 1 ? __builtin_amdgcn_alignbit(w[1], w[0], 24)
+                         : o == 2 ? __builtin_amdgcn_alignbit(w[2], w[1], 16)
+                                  : (w[2] >> 8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t x = (a >> (6 * i)) & 0x3Fu;
+            h[i] = (((x << 13) | x) & 0x00070007u) | g;   // code 2i at bit 0, code 2i+1 at bit 16
+        }
+    }
+};
+
+// B operands of one stage: bw[ks][b] = codes 32 h + 8 ks .. +7 of column b.  FAST:
+// every zero point of the tile is an integer below 1024 in magnitude.  TAIL: the
+// stage may hold codes at k >= K (only the last one does), which become zero.
+template <int BITS, bool FAST, bool TAIL>
+__device__ __forceinline__ void dequant_stage(const WStage<BITS>& r, const SZ& q, int s, int K, int hk, uint32_t g,
+                                              u4 (&bw)[4][2]) {
+    const int k0 = BK * s + 32 * hk;             // first code of the lane's chunk
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const float zf = (float)half_of(q.z[b]);
+        const _Float16 cz = (_Float16)(1024.f + zf);      // exact when FAST: an integer below 2048
+        const _Float16 sh = half_of(q.s[b]);
+        const h2 c2 = {cz, cz}, s2 = {sh, sh};
+        const float sf = (float)sh;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            uint32_t h[4];
+            Octet<BITS>::run(r.w[b], ks, g, h);
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (FAST) {
+                    const h2 v = (__builtin_bit_cast(h2, h[i]) - c2) * s2;
+                    o[i] = __builtin_bit_cast(uint32_t, v);
+                } else {
+                    const float lo = ((float)(h[i] & 0x3FFu) - zf) * sf;
+                    const float hi = ((float)((h[i] >> 16) & 0x3FFu) - zf) * sf;
+                    const h2 v = {(_Float16)lo, (_Float16)hi};
+                    o[i] = __builtin_bit_cast(uint32_t, v);
+                }
+            }
+            if (TAIL && k0 + 8 * ks >= K) o[0] = o[1] = o[2] = o[3] = 0u;
+            bw[ks][b] = u4{o[0], o[1], o[2], o[3]};
+        }
+    }
+}
+
+// Activation operands of stage s: af[ks][a] = row 32 a + r32 of the wave tile,
+// codes 32 h + 8 ks .. +7 of the stage.
+__device__ __forceinline__ void read_a(const char* lds, int s, const int (&aoff)[2], int hk, int sw, u4 (&af)[4][2]) {
+    const u4* at = reinterpret_cast<const u4*>(lds + A_OFF + (s % NSTAGE) * TILE);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int p = (4 * hk + ks) ^ sw;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) af[ks][a] = at[aoff[a] + p];
+    }
+}
+
+// One stage of the 64 x 64 wave tile: 4 k-steps x 2 x 2 blocks of 32 x 32.
+__device__ __forceinline__ void mma_stage(const u4 (&af)[4][2], const u4 (&bw)[4][2], f16x (&acc)[2][2]) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(&af[ks][a]),
+                                                                   *reinterpret_cast<const h8*>(&bw[ks][b]),
+                                                                   acc[a][b], 0, 0, 0);
+}
+
+// Per-lane constants of a compute wave's two columns b (tile rows wn*64 + 32b + r32).
+struct ColInfo {
+    int woff[2];      // LDS byte of the row in a weight buffer (row * PITCH + phase)
+    int soff[2];      // LDS byte of the row's scale span in a window buffer
+    long cg[2];       // col * G
+};
+
+template <int BITS>
+__device__ __forceinline__ void read_w(const char* lds, const ColInfo& ci, int j, int c, WStage<BITS>& r) {
+    const char* wb = lds + W_OFF + (j & 1) * WGeo<BITS>::BUF + c * (4 * BITS);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const char* p = wb + ci.woff[b];
+        if constexpr (BITS == 4) {
+            const u4 v = *reinterpret_cast<const u4*>(p);
+            r.w[b][0] = v.x; r.w[b][1] = v.y; r.w[b][2] = v.z; r.w[b][3] = v.w;
+        } else if constexpr (BITS == 2) {
+            const u2 v = *reinterpret_cast<const u2*>(p);
+            r.w[b][0] = v.x; r.w[b][1] = v.y;
+        } else {
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
+            r.w[b][0] = w[0]; r.w[b][1] = w[1]; r.w[b][2] = w[2];
+        }
+    }
+}
+
+// Scale and zero of group gi (window w) of both columns.
+template <int BITS>
+__device__ __forceinline__ void read_sz(const GemmArgs& A, const char* lds, const ColInfo& ci, int w, int gi, SZ& q) {
+    const char* sb = lds + SZ_OFF<BITS> + (w & 1) * SZ_BUF;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const long span = (ci.cg[b] + SZG * w) & ~7L;
+        const int h = (int)(ci.cg[b] + gi - span);
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(sb + ci.soff[b]) + h;
+        q.s[b] = p[0];
+        q.z[b] = p[BN * 16];          // the zeros follow the scales' 128 rows x 32 bytes
+    }
+}
+
+// A compute wave's LDS operands of one stage.
+template <int BITS>
+struct StageRegs {
+    u4 af[4][2];
+    WStage<BITS> w;
+    SZ q;
+};
+
+// Issues the LDS reads of stage s: its activation slot, and the lane's chunk and
+// (scale, zero) of block s / WBLK (buffer and window as the weight loader filled them).
+template <int BITS>
+__device__ __forceinline__ void read_stage(const GemmArgs& A, const char* lds, int s, const ColInfo& ci, int hk,
+                                           int sw, const int (&aoff)[2], StageRegs<BITS>& r) {
+    const int j = s / WBLK;
+    read_a(lds, s, aoff, hk, sw, r.af);
+    read_w<BITS>(lds, ci, j, 2 * (s % WBLK) + hk, r.w);
+    const int w = (int)(fdiv((uint32_t)(j * 256), A.divG) >> 3);          // j / (gs / 32)
+    const int gi = (int)fdiv((uint32_t)((2 * s + hk) * 32), A.divG);
+    read_sz<BITS>(A, lds, ci, w, gi, r.q);
+}
+
+template <int BITS, bool FAST, bool TAIL>
+__device__ __forceinline__ void run_stage(const GemmArgs& A, const StageRegs<BITS>& r, int s, int hk, uint32_t g,
+                                          f16x (&acc)[2][2]) {
+    u4 bw[4][2];
+    dequant_stage<BITS, FAST, TAIL>(r.w, r.q, s, A.K, hk, g, bw);
+    mma_stage(r.af, bw, acc);
+}
+
+// The compute waves' stages, software-pipelined across the barrier: barrier s + 1
+// publishes stage s + 1, whose LDS reads are then issued before stage s is
+// dequantized and multiplied from registers.  Barrier s + 1 also tells the loaders
+// that stage s's LDS reads have completed (barrier_lds waits for them), so the
+// slot and block reuse rules are those of one stage per barrier.  Unrolled by two
+// so the two register sets alternate without copies.
+template <int BITS, bool FAST>
+__device__ __forceinline__ void compute_loop(const GemmArgs& A, const char* lds, int nst, const ColInfo& ci, int hk,
+                                             int sw, const int (&aoff)[2], uint32_t g, f16x (&acc)[2][2]) {
+    StageRegs<BITS> r0, r1;
+    barrier_lds();                                // stage 0 published
+    read_stage<BITS>(A, lds, 0, ci, hk, sw, aoff, r0);
+    int s = 0;
+    for (; s + 2 < nst; s += 2) {
+        barrier_lds();
+        read_stage<BITS>(A, lds, s + 1, ci, hk, sw, aoff, r1);
+        run_stage<BITS, FAST, false>(A, r0, s, hk, g, acc);
+        barrier_lds();
+        read_stage<BITS>(A, lds, s + 2, ci, hk, sw, aoff, r0);
+        run_stage<BITS, FAST, false>(A, r1, s + 1, hk, g, acc);
+    }
+    // the last one or two stages (only the last can hold codes at k >= K)
+    if (s + 1 < nst) {
+        barrier_lds();
+        read_stage<BITS>(A, lds, s + 1, ci, hk, sw, aoff, r1);
+        run_stage<BITS, FAST, false>(A, r0, s, hk, g, acc);
+        run_stage<BITS, FAST, true>(A, r1, s + 1, hk, g, acc);
+    } else {
+        run_stage<BITS, FAST, true>(A, r0, s, hk, g, acc);
     }
 }
 
@@ -227,45 +456,70 @@ __global__ void __launch_bounds__(THREADS) gemm_f16_kernel(const GemmArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool producer = wave >= 4;
     const int mtiles = (A.M + BM - 1) / BM;
     const int m0 = (blockIdx.x % mtiles) * BM, n0 = (blockIdx.x / mtiles) * BN;
     const int nst = (A.K + BK - 1) / BK;
 
-    if (producer) {
-        // thread (column n, chunk c) of every stage; a 3-stage register ring
-        const int ptid = tid - 256, n = ptid & 127, c = ptid >> 7;
-        const long col = (long)min(n0 + n, A.N - 1);
-        const uint32_t* wrow = A.w + col * A.wpr;
-        const _Float16* srow = reinterpret_cast<const _Float16*>(A.s) + col * A.G;
-        const _Float16* zrow = reinterpret_cast<const _Float16*>(A.z) + col * A.G;
-        // ring slot of stage t: t % 3; at iteration s stage s+2 is dequantized and
-        // stage s+5 loaded into the slot it leaves, three iterations ahead (the loop
-        // is unrolled by three so the slots are registers; every step issues its loads)
-        WRegs<BITS> rr[3];
-        load_w<BITS>(A, wrow, srow, zrow, 0, c, rr[0]);
-        load_w<BITS>(A, wrow, srow, zrow, 1, c, rr[1]);
-        load_w<BITS>(A, wrow, srow, zrow, 2, c, rr[2]);
-        dequant<BITS>(A, rr[0], 0, n, c, 0, lds);
-        load_w<BITS>(A, wrow, srow, zrow, 3, c, rr[0]);
-        dequant<BITS>(A, rr[1], 1, n, c, 1, lds);
-        load_w<BITS>(A, wrow, srow, zrow, 4, c, rr[1]);
-        for (int s0 = 0; s0 < nst; s0 += 3) {
-#pragma unroll
-            for (int u = 0; u < 3; ++u) {
-                const int s = s0 + u;
-                if (s < nst) {
-                    barrier_lds();                // B tiles s, s+1 ready; tile of s-1 free
-                    if (s + 2 < nst) dequant<BITS>(A, rr[(u + 2) % 3], s + 2, n, c, (s + 2) % NB, lds);
-                }
-                load_w<BITS>(A, wrow, srow, zrow, s + 5, c, rr[(u + 2) % 3]);
-            }
+    if (wave == 4 || wave == 5) {
+        // activation loaders: stages s+1 .. s+NSTAGE-2 stay in flight while stage s is
+        // published
+        ALoader da;
+        a_setup(A, m0, wave - 4, lane, da);
+        for (int j = 0; j < NSTAGE - 1; ++j) issue_a(A, da, j, nst, lds);
+        barrier_lds();                            // weight block 0 and the zero-point flag
+        for (int s = 0; s < nst; ++s) {
+            vmcnt<A_INSTR * (NSTAGE - 2)>();      // this loader's half of stage s landed
+            barrier_lds();                        // publish stage s; every wave is past stage s-1
+            issue_a(A, da, s + NSTAGE - 1, nst, lds);   // into the slot of stage s-1
         }
+        vmcnt<0>();                               // the surplus stages land before the wave ends
+        return;
+    }
+    if (wave == 6) {
+        // weight loader: block j + 1 (and the scale window it starts) is issued at
+        // the first barrier of block j and has landed before the first barrier of
+        // block j + 1
+        const int nblk = (nst + WBLK - 1) / WBLK, rp = A.gs >> 5;
+        WLoader<BITS> dw;
+        w_setup<BITS>(A, n0, lane, dw);
+        issue_w<BITS>(dw, 0, lds);
+        issue_sz<BITS>(dw, 0, lds);
+        const bool fast = scan_zeros(A, n0, lane);
+        if (lane == 0) *reinterpret_cast<int*>(lds + FLAG_OFF<BITS>) = fast;
+        vmcnt<0>();
+        barrier_lds();                            // weight block 0 and the zero-point flag
+        for (int s = 0; s < nst; ++s) {
+            barrier_lds();                        // every wave is past stage s-1
+            if (s % WBLK == 0) {
+                const int j = s / WBLK + 1;       // the next block: its buffer held block j - 2
+                if (j < nblk) {
+                    issue_w<BITS>(dw, j, lds);
+                    if (j % rp == 0) issue_sz<BITS>(dw, j / rp, lds);
+                }
+            }
+            if (s % WBLK == WBLK - 1) vmcnt<0>();     // landed before the next block's first barrier
+        }
+        vmcnt<0>();
         return;
     }
 
-    // consumer: 32x32 block (a, b) of the wave tile at rows wm*64 + 32a, columns wn*64 + 32b
+    // compute wave: 32 x 32 block (a, b) of the wave tile at rows wm*64 + 32a,
+    // columns wn*64 + 32b
     const int wm = wave >> 1, wn = wave & 1;
+    const int r32 = lane & 31;
+    const int hk = lane >> 5;
+    ColInfo ci;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int r = wn * 64 + 32 * b + r32;
+        const int col = min(n0 + r, A.N - 1);
+        const uintptr_t row = reinterpret_cast<uintptr_t>(A.w) + (uintptr_t)col * A.wpr * 4;
+        ci.woff[b] = r * WGeo<BITS>::PITCH + (int)(row & 15);
+        ci.soff[b] = r * 32;
+        ci.cg[b] = (long)col * A.G;
+    }
+    const uint32_t g = magic_vreg();
+
     f16x acc[2][2];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -274,61 +528,16 @@ __global__ void __launch_bounds__(THREADS) gemm_f16_kernel(const GemmArgs A) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
 
-    ASrc da;
-    a_setup(A, m0, wave, lane, da);
-    for (int j = 0; j < AHEAD; ++j) issue_a(A, da, j, j, lds, wave, nst);
-    // operand lane map of v_mfma_f32_32x32x16_f16: lane (r = lane & 31, h = lane >> 5)
-    // holds row / column r, k = 8h .. 8h+7 of the 16-code step
-    const int r32 = lane & 31, hk = lane >> 5;
-    int aoff[2], boff[2];
+    int aoff[2];
 #pragma unroll
     for (int a = 0; a < 2; ++a) aoff[a] = (wm * 64 + a * 32 + r32) * 8;
-#pragma unroll
-    for (int b = 0; b < 2; ++b) boff[b] = (wn * 64 + b * 32 + r32) * 8;
-    const int sw = swz(r32);                      // rows / columns are 32-aligned + r32
-    // operands of a stage: 4 steps of 16 codes x (2 A blocks, 2 B blocks)
-    auto read_ops = [&](int st, u4 (&af)[4][2], u4 (&bf)[4][2]) {
-        const u4* at = reinterpret_cast<const u4*>(lds + A_OFF + (st % NSTAGE) * TILE);
-        const u4* bt = reinterpret_cast<const u4*>(lds + B_OFF + (st % NB) * TILE);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int p = (2 * ks + hk) ^ sw;
-#pragma unroll
-            for (int a = 0; a < 2; ++a) af[ks][a] = at[aoff[a] + p];
-#pragma unroll
-            for (int b = 0; b < 2; ++b) bf[ks][b] = bt[boff[b] + p];
-        }
-    };
-    auto mfma_stage = [&](const u4 (&af)[4][2], const u4 (&bf)[4][2]) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(&af[ks][a]),
-                                                                       *reinterpret_cast<const h8*>(&bf[ks][b]),
-                                                                       acc[a][b], 0, 0, 0);
-    };
-    // stage s's operands are read during iteration s-1 (stage 0's after the first
-    // barrier); iteration s: barrier, read stage s+1, multiply stage s
-    u4 fa[2][4][2], fb[2][4][2];
-    vmcnt<(AHEAD - 1) * A_ISSUE>();              // activation stage 0 landed (this wave)
-    for (int s = 0; s < nst; s += 2) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int st = s + u;
-            if (st < nst) {
-                // this wave's activation stage st+1 landed (stage st+2 may still be in flight)
-                vmcnt<A_ISSUE>();
-                barrier_lds();                    // every wave's: activation st+1, B tiles st, st+1
-                if (st == 0) read_ops(0, fa[0], fb[0]);
-                issue_a(A, da, st + AHEAD, (st + AHEAD) % NSTAGE, lds, wave, nst);
-                if (st + 1 < nst) read_ops(st + 1, fa[(u + 1) & 1], fb[(u + 1) & 1]);
-                mfma_stage(fa[u], fb[u]);
-            }
-        }
-    }
+    const int sw = swz(r32);                      // rows are 32-aligned + r32
+
+    barrier_lds();                                // weight block 0 and the zero-point flag
+    if (__builtin_amdgcn_readfirstlane(*reinterpret_cast<const int*>(lds + FLAG_OFF<BITS>)))
+        compute_loop<BITS, true>(A, lds, nst, ci, hk, sw, aoff, g, acc);
+    else
+        compute_loop<BITS, false>(A, lds, nst, ci, hk, sw, aoff, g, acc);
 
     // D layout of the 32x32 block: lane (j = lane & 31, h = lane >> 5), register
     // 4g + r holds row 8g + 4h + r, column j
@@ -353,17 +562,27 @@ const void* kernel_for() {
     return reinterpret_cast<const void*>(&gemm_f16_kernel<BITS>);
 }
 
+template <int BITS>
+int lds_for() {
+    return LDS_BYTES<BITS>;
+}
+
 }  // namespace
 
 bool gemm_f16_supported(const GemmArgs& A) {
-    // 16-byte activation pieces, whole pairs before K, 4-byte scale/zero reads
-    return A.K % 8 == 0 && A.K >= 8 && (reinterpret_cast<uintptr_t>(A.x) & 15) == 0 &&
-           (reinterpret_cast<uintptr_t>(A.w) & 3) == 0;
+    // 16-byte activation pieces, whole octets before K, 16-byte aligned packed /
+    // scale / zero bases (the loaders' aligned pieces and the zero scan), windows of
+    // 8 groups spanning whole weight blocks (group size a multiple of 32), tensors
+    // within the 32-bit range of a buffer descriptor
+    const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const long lim = 0x7FFFFFFF;                 // buffer offsets and ranges are 32-bit
+    return A.K % 8 == 0 && A.K >= 8 && A.gs % 32 == 0 && al16(A.x) && al16(A.w) && al16(A.s) && al16(A.z) &&
+           (long)A.M * A.K * 2 < lim && (long)A.N * A.wpr * 4 < lim && (long)A.N * A.G * 2 < lim;
 }
 
 hipError_t launch_gemm_f16(const GemmArgs& A, hipStream_t stream) {
     const void* f = A.bits == 2 ? kernel_for<2>() : (A.bits == 3 ? kernel_for<3>() : kernel_for<4>());
-    const int lds = LDS_BYTES;
+    const int lds = A.bits == 2 ? lds_for<2>() : (A.bits == 3 ? lds_for<3>() : lds_for<4>());
     hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     const int tiles = ((A.M + BM - 1) / BM) * ((A.N + BN - 1) / BN);
