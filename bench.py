@@ -234,6 +234,7 @@ def main():
         out["gemv_sweep"] = gemv_sweep(torch, C, ops, dev)
         out["fused"] = fused_sweep(torch, C, ops, dev)
         out["gemm"] = gemm_sweep(torch, C, ops, dev)
+        out["llama2_7b_stack"] = stack_sweep(torch, C, ops, dev)
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch, base, xs)
@@ -343,6 +344,97 @@ def gemm_sweep(torch, C, ops, dev):
                              "pct_peak": round(100 * tfs / MFMA_F16_PEAK_TFS, 1)})
                 log(f"gemm M={M} K={K} N={N} W{bits}: {us:.1f} us {tfs:.1f} TFLOP/s")
     return rows
+
+
+STACK_H, STACK_I, STACK_BLOCKS = 4096, 11008, 32
+STACK_LINEARS = [("q", STACK_H, STACK_H), ("k", STACK_H, STACK_H), ("v", STACK_H, STACK_H), ("o", STACK_H, STACK_H),
+                 ("gate", STACK_I, STACK_H), ("up", STACK_I, STACK_H), ("down", STACK_H, STACK_I)]   # (name, N, K)
+
+
+def stack_sweep(torch, C, ops, dev, steps=20):
+    """Config 5: the Llama-2-7B linear stack at decode (M = 1), 32 blocks, bits per block
+    from default_rng(0).choice([2, 3, 4], 32); block i, linear j weights from a device
+    generator seeded 1000*i + j (quantized and packed on the GPU).  A step is, per block,
+    fused QKV, o, fused gate-up and down (ablation_decode.py:48-56); eager and as one
+    captured HIP graph, against the same stack as dense fp16 F.linear (the dequantized
+    weights) in a graph.  Inputs are fixed activations; the rest of the model (attention,
+    norms) is not part of the path."""
+    import numpy as np
+    import torch.nn.functional as F
+    from crispybits_kernels.ops import PackedLinearWeight
+    from crispybits_kernels.reference import dequantize, pack_codes, quantize_affine
+    bitmap = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], STACK_BLOCKS)]
+    blocks, dense = [], []
+    for i, bits in enumerate(bitmap):
+        pb, db = {}, {}
+        for j, (nm, N, K) in enumerate(STACK_LINEARS):
+            g = torch.Generator(device=dev).manual_seed(1000 * i + j)
+            W = torch.randn(N, K, generator=g, device=dev) * 0.02
+            q, s, z = quantize_affine(W, bits, GS)
+            s, z = s.half(), z.half()
+            pb[nm] = PackedLinearWeight(pack_codes(q, bits), s, z, bits, GS, K, N)
+            db[nm] = dequantize(q, s.float(), z.float(), GS).half()
+            del W, q
+        blocks.append(pb)
+        dense.append(db)
+    torch.cuda.synchronize()
+    xh = randx(torch, 1, STACK_H, 1, dev)
+    xi = randx(torch, 1, STACK_I, 2, dev)
+    packed_gb = sum(w.packed.numel() * 4 + w.scales.numel() * 4 for b in blocks for w in b.values()) / 1e9
+    step_bytes = sum(gemv_bytes(1, K, N, b["q"].bits) for b in blocks for _, N, K in STACK_LINEARS)
+
+    def step():
+        for b in blocks:
+            ops.fused_qkv(xh, b["q"], b["k"], b["v"])
+            ops.packed_linear(xh, b["o"])
+            ops.fused_gate_up(xh, b["gate"], b["up"])
+            ops.packed_linear(xi, b["down"])
+
+    def step_fp16():
+        for d in dense:
+            for nm in ("q", "k", "v", "o"):
+                F.linear(xh, d[nm])
+            F.silu(F.linear(xh, d["gate"])) * F.linear(xh, d["up"])
+            F.linear(xi, d["down"])
+
+    def wall(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n
+
+    def graphed(fn):
+        fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            fn()
+        torch.cuda.synchronize()
+        return gr
+
+    eager = wall(step, 5)
+    gr = graphed(step)
+    graph_t = wall(gr.replay, steps)
+    kern_ms, durs = timed_kernels(C, step, 4 * STACK_BLOCKS + 64)
+    del gr
+    gr16 = graphed(step_fp16)
+    fp16_t = wall(gr16.replay, steps)
+    del gr16
+    dense_gb = sum(t.numel() * 2 for d in dense for t in d.values()) / 1e9
+    res = {"workload": "Llama-2-7B linear stack, decode M=1, 32 blocks x (fused QKV, o, fused gate-up, down)",
+           "bitmap": bitmap, "mean_bits": round(float(np.mean(bitmap)), 3), "packed_GB": round(packed_gb, 3),
+           "launches_per_step": len(durs), "eager_us_per_step": round(eager * 1e6, 1),
+           "graph_us_per_step": round(graph_t * 1e6, 1), "kernel_us_per_step": round(kern_ms * 1e3, 1),
+           "GBps_graph": round(step_bytes / graph_t / 1e9, 1),
+           "fp16_dense_GB": round(dense_gb, 3), "fp16_graph_us_per_step": round(fp16_t * 1e6, 1),
+           "speedup_vs_fp16": round(fp16_t / graph_t, 2)}
+    log(f"llama2-7b stack: {res}")
+    del blocks, dense
+    torch.cuda.empty_cache()
+    return res
 
 
 if __name__ == "__main__":
