@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -270,6 +271,58 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
     return pl;
 }
 
+// Batch-1 streaming plan (gemv_stream.hip): fp16 x with 16-byte pieces, any group
+// size that is a multiple of 32, 32-bit byte offsets into every tensor, and for
+// mixed-width QKV workgroups that stay inside one projection.  The K range of a
+// split is cut into slices of 64 * STREAM_CPL chunks (one wave each, at most 8);
+// rows go 4 to a wave, RW row groups to a workgroup.  `rw` > 0 overrides RW.
+struct StreamPlan {
+    bool ok = false;
+    int P = 1, ks = 1, rw = 2, grid = 0, lds = 0;
+};
+
+// K splits of the streaming kernel: the requested split, raised until a split's
+// chunks fit 8 slices of 64 * STREAM_CPL.
+int stream_splits(int64_t C, int split_k) {
+    const int64_t slice = 64 * STREAM_CPL;
+    int64_t P = std::max<int64_t>(1, std::min<int64_t>(split_k, C));
+    while (ceil_div(ceil_div(C, P), slice) > 8 && P < C) ++P;
+    return (int)P;
+}
+
+StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k, int rw_override) {
+    StreamPlan sp;
+    const int64_t lim = INT32_MAX;
+    bool ok = A.M == 1 && dtype == CBK_F16 && A.gs % 32 == 0 && A.K % 8 == 0 &&
+              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.K * 2 < lim;
+    for (int i = 0; i < 3; ++i)
+        ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
+    if (!ok) return sp;
+    const int64_t slice = 64 * STREAM_CPL;
+    sp.P = stream_splits(A.C, split_k);
+    if ((int64_t)A.C * sp.P >= (1ll << 32)) return sp;     // split bounds C p / P in 32 bits
+    sp.ks = (int)ceil_div(ceil_div(A.C, sp.P), slice);
+    if (sp.ks > 8) return sp;
+    sp.rw = rw_override > 0 ? rw_override : (sp.ks <= 4 ? 4 : 2);
+    sp.rw = std::max(2, std::min(sp.rw, 16 / sp.ks));
+    const int rb = STREAM_RPW * sp.rw;
+    if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return sp;
+    const int64_t grid = ceil_div(A.V, rb) * sp.P;
+    if (grid >= lim) return sp;
+    sp.grid = (int)grid;
+    sp.lds = (int)(sp.ks * slice * 72 + (int64_t)sp.ks * rb * 4);
+    sp.ok = true;
+    return sp;
+}
+
+int stream_rw_override() {
+    static const int v = [] {
+        const char* e = std::getenv("CRISPYBITS_STREAM_RW");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
 std::mutex g_attr_mu;
 
 hipError_t ensure_lds(const void* f, int bytes) {
@@ -296,6 +349,33 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     bool xvec = (A.K % 8 == 0) && (reinterpret_cast<uintptr_t>(A.x) % 16 == 0);
     for (int i = 0; i < 3; ++i)
         xvec = xvec && reinterpret_cast<uintptr_t>(A.p[i].s) % 16 == 0 && reinterpret_cast<uintptr_t>(A.p[i].z) % 16 == 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const StreamPlan sp = plan_stream(A, dtype, mixed, split_k, stream_rw_override());
+    if (sp.ok) {
+        A.P = sp.P;
+        A.st_ks = sp.ks;
+        A.st_rw = sp.rw;
+        A.divP = make_fastdiv((uint32_t)A.P);
+        A.divRW = make_fastdiv((uint32_t)A.st_rw);
+        A.divGS = make_fastdiv((uint32_t)(A.gs / 32));
+        if (A.P > 1) {
+            if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
+            A.partial = partial;
+        } else {
+            A.partial = nullptr;
+        }
+        const void* f = gemv_stream_kernel_for(mode, A.p[0].bits, mixed);
+        hipError_t e = ensure_lds(f, sp.lds);
+        if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
+        void* args[] = {&A};
+        e = launch(f, dim3(sp.grid), dim3(64 * sp.ks * sp.rw), args, (size_t)sp.lds, s);
+        if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
+        if (A.P > 1) {
+            e = launch_gemv_reduce(A, dtype, mode, s);
+            if (e != hipSuccess) return hip_fail(e, "packed_gemv: reduce launch");
+        }
+        return CBK_OK;
+    }
     const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, max_bits(A), split_k, rho, cus, mfma_ok, xvec);
     A.P = pl.P;
     A.ntiles = pl.ntiles;
@@ -327,7 +407,6 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     } else {
         A.partial = nullptr;
     }
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t e;
     if (pl.mfma) {
         const void* f = gemv_mfma_kernel_for(mode, A.p[0].bits, mixed, pl.unit_rows ? 1 : 16);
@@ -459,6 +538,7 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
             }
         }
     }
+    if (M == 1) P = std::max(P, stream_splits(ceil_div(K, 32), split_k));
     return P > 1 ? (int64_t)P * M * V : 0;
 }
 

@@ -140,6 +140,12 @@ struct GemvArgs {
     int pad_;
     FastDiv divP, divT, divW, divG;   // by P, ntiles, nw and gs / 128 (MFMA kernel)
     FastDiv divNP;                    // by raw_np
+    // batch-1 streaming kernel (gemv_stream.hip)
+    int st_ks;             // K slices per job (waves per row group)
+    int st_rw;             // row groups per workgroup (4 rows each)
+    int st_xvec;           // x is 16-byte aligned with K % 8 == 0 (vector activation loads)
+    int pad2_;
+    FastDiv divRW, divGS;             // by st_rw and gs / 32
 };
 
 // Per-wave weight ring of the MFMA decode kernel (host and device).  A stage is

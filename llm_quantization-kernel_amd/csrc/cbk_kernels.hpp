@@ -15,6 +15,13 @@ hipError_t launch(const void* f, dim3 grid, dim3 block, void** args, size_t lds,
 // queries and the launch; max_batch <= 1 selects the single-row epilogue.
 const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);
 
+// gemv_stream.hip: batch 1, fp16, group size % 32 == 0.  A job is 4 * st_rw virtual
+// rows x one K split; its workgroup has st_ks * st_rw waves, each over STREAM_RPW rows
+// and one K slice of 64 * STREAM_CPL chunks.
+constexpr int STREAM_CPL = 2;
+constexpr int STREAM_RPW = 4;
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed);
+
 // gemv_generic.hip: any dtype / group size; 32 virtual rows x 1 batch row per job.
 constexpr int GENERIC_THREADS = 256;
 constexpr int GENERIC_ROWS = 32;

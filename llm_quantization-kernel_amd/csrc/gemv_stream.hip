@@ -1,0 +1,320 @@
+// gemv_stream.hip -- batch-1 fp16 decode GEMV that streams packed rows through VGPRs.
+//
+// Replaces cb_gemv_kernel (Kernel/csrc/packed_gemv.cu:83-163) and, when the K
+// range is split, the partial write that cb_reduce_kernel (:166-180) combines,
+// for one activation row (the decode step) in fp16 with any group size that is a
+// multiple of 32.  Plain, fused-QKV and fused gate-up modes share the body; the
+// epilogue is cb_epilogue's (:54-81, cbk_device.hpp).
+//
+// Job = (block of RB = 4 RW virtual rows, K split p).  A workgroup holds KS x RW
+// waves: wave (ks, rw) takes rows 4 rw .. 4 rw + 3 of the block over K slice ks
+// of the split, 128 chunks of 32 codes, lane l owning chunks l and l + 64 of the
+// slice.  Per wave:
+//   1. The thread's activation chunk is requested, then every packed
+//      chunk of the wave's rows (one buffer load of BITS dwords per row and lane
+//      chunk, 64 lanes = 64 consecutive chunks) and their (scale, zero) halves --
+//      the whole of the wave's weights is in flight before any arithmetic.
+//   2. Activations are converted to the operand order of the in-place decode
+//      (cbk_decode.hpp): pair p = (x_a 2^-e_a, x_b 2^-e_b) for the codes kappa and
+//      field offsets expo of the chunk's half slots, with the chunk's slot-offset
+//      sum B = 1024 sum_p X_p and its plain sum sum_j x_j, into LDS; one barrier
+//      publishes them to every wave of the workgroup.
+//   3. Per row and chunk: the BITS words decode into 16 fp16 pairs 1024 + 2^e q by
+//      one v_and_or_b32 each, 16 v_dot2_f32_f16 against the staged pairs give
+//      sum x q + B, and acc += s * (dot - B - z * sum x)  (packed_gemv.cu:113-138
+//      algebra: the zero point is applied per chunk against the activation sum).
+//   4. The 4 rows' lane sums meet by v_permlane32_swap, v_permlane16_swap and four
+//      DPP row rotations (every lane of a 16-lane row ends with one row's total).
+//   5. Row totals of the slices meet in LDS and are added in slice order (so the
+//      result does not depend on wave timing); the epilogue runs per row, or with
+//      P > 1 the fp32 partial is written for the split-K combine.
+#include "cbk_decode.hpp"
+#include "cbk_device.hpp"
+#include "cbk_kernels.hpp"
+
+namespace cbk {
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+constexpr int CPL = STREAM_CPL;          // chunks per lane of a slice
+constexpr int SLICE = 64 * CPL;          // chunks per K slice
+constexpr int RPW = STREAM_RPW;          // rows per wave
+constexpr int RAW = 0x00020000;          // buffer descriptor word 3: raw 32-bit data
+// A byte offset past every descriptor's range: such loads return zero.  Loads are
+// issued unconditionally (a branch around a load makes the compiler wait for it at
+// the join), and the ones that must not contribute read here.
+constexpr int OOR = 0x7FFFFF00;
+
+// The offset as an opaque VGPR value, so the compiler keeps the select in front of
+// the load instead of turning it into a branch around two loads.
+__device__ __forceinline__ int vofs(bool ok, int off) {
+    int v = ok ? off : OOR;
+    asm("" : "+v"(v));
+    return v;
+}
+
+// One chunk's BITS words at byte offset `off` of the packed tensor (zero past its end).
+template <int BITS>
+__device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t r, int off, uint32_t (&w)[BITS]) {
+    if constexpr (BITS == 4) {
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (BITS == 3) {
+        const u3 v = __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z;
+    } else {
+        const u2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        w[0] = v.x; w[1] = v.y;
+    }
+}
+
+struct ProjRes {
+    __amdgpu_buffer_rsrc_t w, s, z;
+};
+
+__device__ __forceinline__ ProjRes proj_res(const Proj& p, int G) {
+    ProjRes r;
+    r.w = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.w), (short)0, p.n * p.wpr * 4, RAW);
+    r.s = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.s), (short)0, p.n * G * 2, RAW);
+    r.z = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.z), (short)0, p.n * G * 2, RAW);
+    return r;
+}
+
+// Activation chunk at byte offset `off` of x as 16 words of fp16 pairs (x_2i, x_2i+1);
+// codes at k >= K, and the whole chunk when off is OOR, read as zero (the descriptor
+// spans exactly K halves, K % 8 == 0).
+__device__ __forceinline__ void load_x(__amdgpu_buffer_rsrc_t xr, int off, uint32_t (&x)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * i, 0, 0);
+        x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+    }
+}
+
+// Operand pairs of one chunk for the BITS decode, their slot-offset sum B and sum x.
+template <int BITS>
+__device__ __forceinline__ void convert_x(const uint32_t (&x)[16], u4 (&X)[4], float& B, float& xs) {
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    uint32_t o[16];
+    float b = 0.f, t = 0.f;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+        const int ka = Decode<BITS>::kappa(2 * p), kb = Decode<BITS>::kappa(2 * p + 1);
+        const int ea = Decode<BITS>::expo(2 * p), eb = Decode<BITS>::expo(2 * p + 1);
+        // low half = x[ka] (half ka & 1 of word ka >> 1), high half = x[kb]
+        const uint32_t sel = (uint32_t)(2 * (ka & 1)) | ((uint32_t)(2 * (ka & 1) + 1) << 8) |
+                             ((uint32_t)(4 + 2 * (kb & 1)) << 16) | ((uint32_t)(5 + 2 * (kb & 1)) << 24);
+        const uint32_t raw = __builtin_amdgcn_perm(x[kb >> 1], x[ka >> 1], sel);
+        const h2 sc = {(_Float16)(1.0f / (float)(1 << ea)), (_Float16)(1.0f / (float)(1 << eb))};
+        const h2 v = __builtin_bit_cast(h2, raw) * sc;      // exact: power-of-two scale
+        o[p] = __builtin_bit_cast(uint32_t, v);
+        b = __builtin_amdgcn_fdot2(v, one, b, false);
+        t = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x[p]), one, t, false);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) X[q] = u4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+    B = 1024.f * b;
+    xs = t;
+}
+
+// sum x q + B of one row's chunk: 16 decoded pairs against the staged operands.
+template <int BITS>
+__device__ __forceinline__ float chunk_dot(const uint32_t (&w)[BITS], const u4 (&X)[4], uint32_t g) {
+    uint32_t h[16];
+    Decode<BITS>::run(w, h, g);
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        // vector elements are copied to scalars first: clang's __builtin_bit_cast of an
+        // ext-vector element lvalue reads the vector's first element
+        const uint32_t x0 = X[q].x, x1 = X[q].y, x2 = X[q].z, x3 = X[q].w;
+        d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, h[4 * q + 0]), __builtin_bit_cast(h2, x0), d0, false);
+        d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, h[4 * q + 1]), __builtin_bit_cast(h2, x1), d1, false);
+        d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, h[4 * q + 2]), __builtin_bit_cast(h2, x2), d0, false);
+        d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, h[4 * q + 3]), __builtin_bit_cast(h2, x3), d1, false);
+    }
+    return d0 + d1;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Lane sums of 4 rows -> every lane of 16-lane row i holds the total of wave row
+// srow(i): rows (0, 2, 1, 3) for lane rows (0, 1, 2, 3).
+__device__ __forceinline__ float reduce4(const float (&a)[RPW]) {
+    const auto p01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[0]), __float_as_uint(a[1]), false, false);
+    const auto p23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[2]), __float_as_uint(a[3]), false, false);
+    const float s01 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);   // lanes 0-31 row 0, 32-63 row 1
+    const float s23 = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);   // lanes 0-31 row 2, 32-63 row 3
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(s01), __float_as_uint(s23), false, false);
+    float s = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+    s = dpp_add<0x128>(s);     // row_ror:8
+    s = dpp_add<0x124>(s);     // row_ror:4
+    s = dpp_add<0x122>(s);     // row_ror:2
+    s = dpp_add<0x121>(s);     // row_ror:1
+    return s;
+}
+
+__device__ __forceinline__ int lane_row(int lane) { return ((lane >> 5) & 1) | (((lane >> 4) & 1) << 1); }
+
+__device__ __forceinline__ void barrier_lds() {
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));    // lgkmcnt(0); leaves loads in flight
+    __builtin_amdgcn_s_barrier();
+}
+
+template <int BITS, int MODE>
+__device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KS = A.st_ks, RW = A.st_rw, RB = 4 * A.st_rw;
+    const int NCH = KS * SLICE;
+    const int ks = (int)fdiv((uint32_t)wave, A.divRW);
+    const int rw = wave - ks * RW;
+    const int blk = (int)fdiv(blockIdx.x, A.divP);     // job = blk * P + p (split fastest)
+    const int p = blockIdx.x - blk * A.P;
+    // split p covers chunks [C p / P, C (p + 1) / P)  (packed_gemv.cu:94-95)
+    const int c0 = (int)fdiv((uint32_t)(A.C * p), A.divP);
+    const int c1 = (int)fdiv((uint32_t)(A.C * (p + 1)), A.divP);
+    const int nrange = c1 - c0;
+    const int vbase = blk * RB;
+    const int v0 = vbase + RPW * rw;
+    const uint32_t g = magic_vreg();
+
+    // 1a. the thread's activation chunk (job chunk tid; the host keeps RW >= 2, so
+    // the 64 KS RW threads cover the KS * 128 staged chunks)
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.K * 2, RAW);
+    uint32_t xa[16];
+    load_x(xr, vofs(tid < nrange, 64 * (c0 + tid)), xa);
+
+    // 1b. the wave's packed chunks and their (scale, zero) halves
+    ProjRes R[3];
+    R[0] = proj_res(A.p[0], A.G);
+    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.p[1], A.G);
+    if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.p[1], A.G); R[2] = proj_res(A.p[2], A.G); }
+    int gi[CPL];
+    bool cin[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = ks * SLICE + lane + 64 * i;
+        cin[i] = c < nrange;
+        gi[i] = (int)fdiv((uint32_t)(c0 + c), A.divGS);       // group of the chunk
+    }
+    uint32_t w[RPW][CPL][BITS];
+    uint32_t sz[RPW][CPL][2];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        const int v = v0 + j;
+        const bool vin = v < A.V;
+        int proj, r;
+        vmap<MODE>(A, vin ? v : 0, proj, r);
+        const ProjRes& P = proj == 0 ? R[0] : (proj == 1 ? R[1] : R[2]);
+        const int wpr = CBK_SEL(A, proj, wpr);
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = ks * SLICE + lane + 64 * i;
+            const bool ok = vin && cin[i];
+            const int so = vofs(ok, 2 * (r * A.G + gi[i]));
+            load_chunk<BITS>(P.w, vofs(ok, 4 * (r * wpr + (c0 + c) * BITS)), w[j][i]);
+            sz[j][i][0] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
+            sz[j][i][1] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
+        }
+    }
+
+    // 2. activations -> LDS: piece q of chunk c at (q NCH + c) * 16, (B, sum x) at
+    // 64 NCH + 8 c; chunks past the split read as zero (they meet no weights)
+    u4* Xl = reinterpret_cast<u4*>(lds);
+    float2* XBl = reinterpret_cast<float2*>(lds + 64 * NCH);
+    float* red = reinterpret_cast<float*>(lds + 72 * NCH);
+    if (tid < NCH) {
+        u4 X[4];
+        float B, xs;
+        convert_x<BITS>(xa, X, B, xs);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) Xl[q * NCH + tid] = X[q];
+        XBl[tid] = make_float2(B, xs);
+    }
+    barrier_lds();
+
+    // 3. rows
+    u4 X[CPL][4];
+    float2 XB[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = ks * SLICE + lane + 64 * i;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) X[i][q] = Xl[q * NCH + c];
+        XB[i] = XBl[c];
+    }
+    float acc[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const float d = chunk_dot<BITS>(w[j][i], X[i], g);
+            const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[j][i][0]);
+            const float z = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[j][i][1]);
+            a = fmaf(s, d - fmaf(z, XB[i].y, XB[i].x), a);
+        }
+        acc[j] = a;
+    }
+
+    // 4. row totals of the wave
+    const float tot = reduce4(acc);
+    if ((lane & 15) == 0) red[ks * RB + RPW * rw + lane_row(lane)] = tot;
+    barrier_lds();
+
+    // 5. slices in order, then the epilogue (or the split's partial)
+    if (tid < RB) {
+        const int v = vbase + tid;
+        if (v < A.V) {
+            float mine = 0.f, partner = 0.f;
+            for (int k = 0; k < KS; ++k) {
+                mine += red[k * RB + tid];
+                partner += red[k * RB + (tid ^ 1)];
+            }
+            if (A.P == 1) epilogue<DT_F16, MODE>(A, 0, v, mine, partner);
+            else A.partial[(long)p * A.V + v] = mine;
+        }
+    }
+}
+
+// BITS = 0: fused QKV with a width per projection; the host keeps each
+// workgroup's rows inside one projection, so the width is uniform per workgroup.
+template <int MODE, int BITS>
+__global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    if constexpr (BITS != 0) {
+        stream_body<BITS, MODE>(A, lds);
+    } else {
+        int proj, r;
+        vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * 4 * A.st_rw, proj, r);
+        const int bits = CBK_SEL(A, proj, bits);
+        if (bits == 2) stream_body<2, MODE>(A, lds);
+        else if (bits == 3) stream_body<3, MODE>(A, lds);
+        else stream_body<4, MODE>(A, lds);
+    }
+}
+
+}  // namespace
+
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed) {
+    if (mixed) return reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_QKV, 0>);
+#define CBK_STREAM_K(M)                                                                            \
+    (bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 2>)                          \
+               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 3>)             \
+                            : reinterpret_cast<const void*>(&gemv_stream_kernel<M, 4>)))
+    if (mode == MODE_QKV) return CBK_STREAM_K(MODE_QKV);
+    if (mode == MODE_GATEUP) return CBK_STREAM_K(MODE_GATEUP);
+    return CBK_STREAM_K(MODE_GEMV);
+#undef CBK_STREAM_K
+}
+
+}  // namespace cbk
