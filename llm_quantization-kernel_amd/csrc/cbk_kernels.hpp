@@ -18,7 +18,10 @@ const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);
 // gemv_stream.hip: batch 1, fp16, group size % 32 == 0.  A job is 4 * st_rw virtual
 // rows x one K split; its workgroup has st_ks * st_rw waves, each over STREAM_RPW rows
 // and one K slice of 64 * STREAM_CPL chunks.
-constexpr int STREAM_CPL = 2;
+#ifndef CBK_STREAM_CPL
+#define CBK_STREAM_CPL 1
+#endif
+constexpr int STREAM_CPL = CBK_STREAM_CPL;
 constexpr int STREAM_RPW = 4;
 const void* gemv_stream_kernel_for(int mode, int bits, bool mixed);
 

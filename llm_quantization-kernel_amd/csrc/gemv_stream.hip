@@ -8,8 +8,8 @@
 //
 // Job = (block of RB = 4 RW virtual rows, K split p).  A workgroup holds KS x RW
 // waves: wave (ks, rw) takes rows 4 rw .. 4 rw + 3 of the block over K slice ks
-// of the split, 128 chunks of 32 codes, lane l owning chunks l and l + 64 of the
-// slice.  Per wave:
+// of the split, 64 CPL chunks of 32 codes, lane l owning chunks l + 64 i (i < CPL)
+// of the slice.  Per wave:
 //   1. The thread's activation chunk is requested, then every packed
 //      chunk of the wave's rows (one buffer load of BITS dwords per row and lane
 //      chunk, 64 lanes = 64 consecutive chunks) and their (scale, zero) halves --
@@ -186,8 +186,8 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     const int v0 = vbase + RPW * rw;
     const uint32_t g = magic_vreg();
 
-    // 1a. the thread's activation chunk (job chunk tid; the host keeps RW >= 2, so
-    // the 64 KS RW threads cover the KS * 128 staged chunks)
+    // 1a. the thread's activation chunk (job chunk tid; the host keeps RW >= CPL, so
+    // the 64 KS RW threads cover the KS * SLICE staged chunks)
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.K * 2, RAW);
     uint32_t xa[16];
@@ -225,6 +225,9 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
             sz[j][i][0] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
             sz[j][i][1] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
         }
+        // rows are issued in the order they are consumed, so row j's arithmetic
+        // waits for its own loads only
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // 2. activations -> LDS: piece q of chunk c at (q NCH + c) * 16, (B, sum x) at
