@@ -52,12 +52,13 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int NSTAGE = 6;                    // activation stages in LDS
+constexpr int BM = 128, BN = 128, BK = 128;
+constexpr int NSTAGE = 3;                    // activation stages in LDS
 constexpr int THREADS = 448;                 // 4 compute waves + 2 activation loaders + 1 weight loader
-constexpr int TILE = BM * BK * 2;            // bytes of an activation stage (16 KB)
+constexpr int TILE = BM * BK * 2;            // bytes of an activation stage (32 KB)
+constexpr int APR = BK * 2 / 16;             // 16-byte pieces per activation row of a stage
 constexpr int A_INSTR = TILE / 1024 / 2;     // instructions per activation loader per stage
-constexpr int WBLK = 4;                      // stages per weight block
+constexpr int WBLK = 2;                      // stages per weight block (256 codes)
 constexpr int SZG = 8;                       // groups per scale / zero window
 constexpr int SZ_INSTR = 2 * BN * 2 / 64;    // window: [tensor][row] x two 16-byte pieces
 constexpr int SZ_BUF = 2 * BN * 32;
@@ -77,7 +78,7 @@ template <int BITS> constexpr int SZ_OFF = W_OFF + 2 * WGeo<BITS>::BUF;
 template <int BITS> constexpr int FLAG_OFF = SZ_OFF<BITS> + 2 * SZ_BUF;   // tile zeros allow the fp16 form
 template <int BITS> constexpr int LDS_BYTES = FLAG_OFF<BITS> + 16;
 
-__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz(int r) { return r & (APR - 1); }
 
 template <int N>
 __device__ __forceinline__ void vmcnt() {
@@ -103,8 +104,9 @@ __device__ __forceinline__ void dma16(const void* g, char* lds) {
 // The loads go through a buffer descriptor over the activations: the lane's offset
 // (row clamped to M, piece) is fixed, the stage's column offset is a scalar, so a
 // stage costs no VALU.  Pieces past K read on into the next row (or, past the
-// tensor, zero), which meets zero weights -- except in the last stage, where they
-// re-read the row's own last piece so that no other row's values enter the sums.
+// tensor, zero), which meets zero weights -- except in the last stage, where pieces
+// at k >= K read as zero (K % 8 == 0, so a piece is wholly inside or outside), so
+// whatever the weight tile holds there contributes nothing.
 struct ALoader {
     __amdgpu_buffer_rsrc_t rsrc;
     int voff[A_INSTR];
@@ -119,12 +121,15 @@ __device__ __forceinline__ void a_setup(const GemmArgs& A, int m0, int half, int
 #pragma unroll
     for (int i = 0; i < A_INSTR; ++i) {
         const int q = 64 * (d.t0 + i) + lane;
-        const int r = q >> 3, p = (q & 7) ^ swz(r);
+        const int r = q / APR, p = (q & (APR - 1)) ^ swz(r);
         d.rowoff[i] = min(m0 + r, A.M - 1) * A.K * 2;
         d.pk[i] = 8 * p;
         d.voff[i] = d.rowoff[i] + 16 * p;
     }
 }
+
+// A byte offset past every buffer descriptor's range: such loads return zero.
+constexpr int OOR = 0x7FFFFFF0;
 
 // Stage s into slot s % NSTAGE; a stage past the last is issued as the last one,
 // so every iteration issues A_INSTR loads and the waits are constants.
@@ -133,9 +138,11 @@ __device__ __forceinline__ void issue_a(const GemmArgs& A, const ALoader& d, int
     s = min(s, nst - 1);
     if (s == nst - 1 && A.K % BK != 0) {
 #pragma unroll
-        for (int i = 0; i < A_INSTR; ++i)
+        for (int i = 0; i < A_INSTR; ++i) {
+            const int k = BK * s + d.pk[i];
             __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rsrc, (lds_void*)(dst + i * 1024), 16,
-                                                     d.rowoff[i] + 2 * min(BK * s + d.pk[i], A.K - 8), 0, 0, 0);
+                                                     k < A.K ? d.rowoff[i] + 2 * k : OOR, 0, 0, 0);
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < A_INSTR; ++i)
@@ -229,14 +236,17 @@ __device__ __forceinline__ bool scan_zeros(const GemmArgs& A, int n0, int lane) 
 }
 
 // ------------------------------------------------------------------ compute
-// The lane's packed chunk of a stage (chunk 2 s + h), of both of its columns, and
-// their scales and zeros as raw fp16 bits.
+// A compute wave owns a 128 x 32 slab of the tile: every row, columns
+// 32 wn .. 32 wn + 31 (wn = wave), so each column is dequantized by exactly one
+// wave.  Lane (r32 = lane & 31, hk = lane >> 5) holds column r32's B operand and
+// the A operands of rows 32 a + r32 (a < 4).  Step ks of a stage gives lane half hk
+// the codes 32 hk + 8 ks .. +7 (octet ks of chunk 2 s + hk), so a lane needs one
+// packed chunk and one (scale, zero) pair per stage.
+
+// The lane's two packed chunks of a stage and their scales and zeros as raw fp16 bits.
 template <int BITS>
 struct WStage {
     uint32_t w[2][BITS];
-};
-
-struct SZ {
     uint32_t s[2], z[2];
 };
 
@@ -288,166 +298,141 @@ template <> struct Octet<3> {
     }
 };
 
-// B operands of one stage: bw[ks][b] = codes 32 h + 8 ks .. +7 of column b.  FAST:
-// every zero point of the tile is an integer below 1024 in magnitude.  TAIL: the
-// stage may hold codes at k >= K (only the last one does), which become zero.
-template <int BITS, bool FAST, bool TAIL>
-__device__ __forceinline__ void dequant_stage(const WStage<BITS>& r, const SZ& q, int s, int K, int hk, uint32_t g,
-                                              u4 (&bw)[4][2]) {
-    const int k0 = BK * s + 32 * hk;             // first code of the lane's chunk
+// B operand of step ks: the lane's codes 64 hk + 8 ks .. +7 of its column (octet
+// ks & 3 of its chunk ks >> 2).  FAST: every zero point of the tile is an integer
+// below 1024 in magnitude.
+template <int BITS, bool FAST>
+__device__ __forceinline__ u4 dequant_octet(const WStage<BITS>& r, int ks, uint32_t g) {
+    const int c = ks >> 2;
+    const float zf = (float)half_of(r.z[c]);
+    const _Float16 cz = (_Float16)(1024.f + zf);      // exact when FAST: an integer below 2048
+    const _Float16 sh = half_of(r.s[c]);
+    const h2 c2 = {cz, cz}, s2 = {sh, sh};
+    const float sf = (float)sh;
+    uint32_t h[4];
+    Octet<BITS>::run(r.w[c], ks & 3, g, h);
+    uint32_t o[4];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const float zf = (float)half_of(q.z[b]);
-        const _Float16 cz = (_Float16)(1024.f + zf);      // exact when FAST: an integer below 2048
-        const _Float16 sh = half_of(q.s[b]);
-        const h2 c2 = {cz, cz}, s2 = {sh, sh};
-        const float sf = (float)sh;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            uint32_t h[4];
-            Octet<BITS>::run(r.w[b], ks, g, h);
-            uint32_t o[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if constexpr (FAST) {
-                    const h2 v = (__builtin_bit_cast(h2, h[i]) - c2) * s2;
-                    o[i] = __builtin_bit_cast(uint32_t, v);
-                } else {
-                    const float lo = ((float)(h[i] & 0x3FFu) - zf) * sf;
-                    const float hi = ((float)((h[i] >> 16) & 0x3FFu) - zf) * sf;
-                    const h2 v = {(_Float16)lo, (_Float16)hi};
-                    o[i] = __builtin_bit_cast(uint32_t, v);
-                }
-            }
-            if (TAIL && k0 + 8 * ks >= K) o[0] = o[1] = o[2] = o[3] = 0u;
-            bw[ks][b] = u4{o[0], o[1], o[2], o[3]};
-        }
-    }
-}
-
-// Activation operands of stage s: af[ks][a] = row 32 a + r32 of the wave tile,
-// codes 32 h + 8 ks .. +7 of the stage.
-__device__ __forceinline__ void read_a(const char* lds, int s, const int (&aoff)[2], int hk, int sw, u4 (&af)[4][2]) {
-    const u4* at = reinterpret_cast<const u4*>(lds + A_OFF + (s % NSTAGE) * TILE);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        const int p = (4 * hk + ks) ^ sw;
-#pragma unroll
-        for (int a = 0; a < 2; ++a) af[ks][a] = at[aoff[a] + p];
-    }
-}
-
-// One stage of the 64 x 64 wave tile: 4 k-steps x 2 x 2 blocks of 32 x 32.
-__device__ __forceinline__ void mma_stage(const u4 (&af)[4][2], const u4 (&bw)[4][2], f16x (&acc)[2][2]) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(&af[ks][a]),
-                                                                   *reinterpret_cast<const h8*>(&bw[ks][b]),
-                                                                   acc[a][b], 0, 0, 0);
-}
-
-// Per-lane constants of a compute wave's two columns b (tile rows wn*64 + 32b + r32).
-struct ColInfo {
-    int woff[2];      // LDS byte of the row in a weight buffer (row * PITCH + phase)
-    int soff[2];      // LDS byte of the row's scale span in a window buffer
-    long cg[2];       // col * G
-};
-
-template <int BITS>
-__device__ __forceinline__ void read_w(const char* lds, const ColInfo& ci, int j, int c, WStage<BITS>& r) {
-    const char* wb = lds + W_OFF + (j & 1) * WGeo<BITS>::BUF + c * (4 * BITS);
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const char* p = wb + ci.woff[b];
-        if constexpr (BITS == 4) {
-            const u4 v = *reinterpret_cast<const u4*>(p);
-            r.w[b][0] = v.x; r.w[b][1] = v.y; r.w[b][2] = v.z; r.w[b][3] = v.w;
-        } else if constexpr (BITS == 2) {
-            const u2 v = *reinterpret_cast<const u2*>(p);
-            r.w[b][0] = v.x; r.w[b][1] = v.y;
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (FAST) {
+            const h2 v = (__builtin_bit_cast(h2, h[i]) - c2) * s2;
+            o[i] = __builtin_bit_cast(uint32_t, v);
         } else {
-            const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
-            r.w[b][0] = w[0]; r.w[b][1] = w[1]; r.w[b][2] = w[2];
+            const float lo = ((float)(h[i] & 0x3FFu) - zf) * sf;
+            const float hi = ((float)((h[i] >> 16) & 0x3FFu) - zf) * sf;
+            const h2 v = {(_Float16)lo, (_Float16)hi};
+            o[i] = __builtin_bit_cast(uint32_t, v);
         }
     }
+    return u4{o[0], o[1], o[2], o[3]};
 }
 
-// Scale and zero of group gi (window w) of both columns.
-template <int BITS>
-__device__ __forceinline__ void read_sz(const GemmArgs& A, const char* lds, const ColInfo& ci, int w, int gi, SZ& q) {
-    const char* sb = lds + SZ_OFF<BITS> + (w & 1) * SZ_BUF;
+// A operands of step ks of stage s: af[a] = row 32 a + r32, codes 64 hk + 8 ks .. +7.
+__device__ __forceinline__ void read_a(const char* lds, int s, int ks, int aoff, int hk, int sw, u4 (&af)[4]) {
+    const u4* at = reinterpret_cast<const u4*>(lds + A_OFF + (s % NSTAGE) * TILE);
+    const int p = (8 * hk + ks) ^ sw;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const long span = (ci.cg[b] + SZG * w) & ~7L;
-        const int h = (int)(ci.cg[b] + gi - span);
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(sb + ci.soff[b]) + h;
-        q.s[b] = p[0];
-        q.z[b] = p[BN * 16];          // the zeros follow the scales' 128 rows x 32 bytes
+    for (int a = 0; a < 4; ++a) af[a] = at[aoff + a * 32 * APR + p];     // 32 rows apart
+}
+
+// Per-lane constants of a compute wave's column (tile row wn * 32 + r32).
+struct ColInfo {
+    int woff;         // LDS byte of the row in a weight buffer (row * PITCH + phase)
+    int soff;         // LDS byte of the row's scale span in a window buffer
+    long cg;          // col * G
+};
+
+// The lane's chunks (4 s + 2 hk + c, c < 2: chunks 4 (s % WBLK) + 2 hk + c of block
+// s / WBLK) and their (scale, zero) of stage s, as the weight loader filled its
+// buffer and window.
+template <int BITS>
+__device__ __forceinline__ void read_w(const GemmArgs& A, const char* lds, int s, const ColInfo& ci, int hk,
+                                       WStage<BITS>& r) {
+    const int j = s / WBLK;
+    const char* p = lds + W_OFF + (j & 1) * WGeo<BITS>::BUF + (4 * (s % WBLK) + 2 * hk) * (4 * BITS) + ci.woff;
+    if constexpr (BITS == 4) {
+        const u4 v0 = *reinterpret_cast<const u4*>(p), v1 = *reinterpret_cast<const u4*>(p + 16);
+        r.w[0][0] = v0.x; r.w[0][1] = v0.y; r.w[0][2] = v0.z; r.w[0][3] = v0.w;
+        r.w[1][0] = v1.x; r.w[1][1] = v1.y; r.w[1][2] = v1.z; r.w[1][3] = v1.w;
+    } else if constexpr (BITS == 2) {
+        const u4 v = *reinterpret_cast<const u4*>(p);
+        r.w[0][0] = v.x; r.w[0][1] = v.y; r.w[1][0] = v.z; r.w[1][1] = v.w;
+    } else {
+        const u2 v0 = *reinterpret_cast<const u2*>(p), v1 = *reinterpret_cast<const u2*>(p + 8);
+        const u2 v2 = *reinterpret_cast<const u2*>(p + 16);
+        r.w[0][0] = v0.x; r.w[0][1] = v0.y; r.w[0][2] = v1.x;
+        r.w[1][0] = v1.y; r.w[1][1] = v2.x; r.w[1][2] = v2.y;
+    }
+    const int w = (int)(fdiv((uint32_t)(j * 256), A.divG) >> 3);           // j / (gs / 32)
+    const char* sb = lds + SZ_OFF<BITS> + (w & 1) * SZ_BUF;
+    const long span = (ci.cg + SZG * w) & ~7L;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int gi = (int)fdiv((uint32_t)((4 * s + 2 * hk + c) * 32), A.divG);
+        const uint16_t* q = reinterpret_cast<const uint16_t*>(sb + ci.soff) + (int)(ci.cg + gi - span);
+        r.s[c] = q[0];
+        r.z[c] = q[BN * 16];      // the zeros follow the scales' 128 rows x 32 bytes
     }
 }
 
-// A compute wave's LDS operands of one stage.
-template <int BITS>
-struct StageRegs {
-    u4 af[4][2];
-    WStage<BITS> w;
-    SZ q;
-};
-
-// Issues the LDS reads of stage s: its activation slot, and the lane's chunk and
-// (scale, zero) of block s / WBLK (buffer and window as the weight loader filled them).
-template <int BITS>
-__device__ __forceinline__ void read_stage(const GemmArgs& A, const char* lds, int s, const ColInfo& ci, int hk,
-                                           int sw, const int (&aoff)[2], StageRegs<BITS>& r) {
-    const int j = s / WBLK;
-    read_a(lds, s, aoff, hk, sw, r.af);
-    read_w<BITS>(lds, ci, j, 2 * (s % WBLK) + hk, r.w);
-    const int w = (int)(fdiv((uint32_t)(j * 256), A.divG) >> 3);          // j / (gs / 32)
-    const int gi = (int)fdiv((uint32_t)((2 * s + hk) * 32), A.divG);
-    read_sz<BITS>(A, lds, ci, w, gi, r.q);
+// One k-step: 4 MFMAs of 32 x 32 x 16 (rows 32 a .. of the slab, the lane's column).
+__device__ __forceinline__ void mma_step(const u4 (&af)[4], const u4& bw, f16x (&acc)[4]) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+        acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(&af[a]),
+                                                        *reinterpret_cast<const h8*>(&bw), acc[a], 0, 0, 0);
 }
 
-template <int BITS, bool FAST, bool TAIL>
-__device__ __forceinline__ void run_stage(const GemmArgs& A, const StageRegs<BITS>& r, int s, int hk, uint32_t g,
-                                          f16x (&acc)[2][2]) {
-    u4 bw[4][2];
-    dequant_stage<BITS, FAST, TAIL>(r.w, r.q, s, A.K, hk, g, bw);
-    mma_stage(r.af, bw, acc);
+// One stage, as a software pipeline over its 8 k-steps: the A operands of step ks
+// are read two steps ahead (a[ks & 3] of four rotating sets) and its B operand
+// dequantized one step ahead, so each step's 4 MFMAs find their operands in
+// registers while the dequant VALU of the next step and the LDS reads of the step
+// after it go out between them.  On entry a[0], a[1] hold steps 0 and 1, bw step
+// 0, wc the chunks of stage s.  NEXT: the wave meets barrier s + 1 after step 5 --
+// every read of stage s's activation slot has been issued by then, and
+// barrier_lds waits for them, so the loaders may refill it -- then reads steps 0
+// and 1 of stage s + 1 and its chunks (wn), and dequantizes its step 0, leaving
+// the entry state of stage s + 1.
+template <int BITS, bool FAST, bool NEXT>
+__device__ __forceinline__ void run_stage(const GemmArgs& A, const char* lds, int s, const ColInfo& ci, int hk,
+                                          int sw, int aoff, uint32_t g, u4 (&a)[4][4], u4& bw,
+                                          const WStage<BITS>& wc, WStage<BITS>& wn, f16x (&acc)[4]) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        if (ks + 2 < 8) read_a(lds, s, ks + 2, aoff, hk, sw, a[(ks + 2) & 3]);
+        else if (NEXT) read_a(lds, s + 1, ks - 6, aoff, hk, sw, a[(ks + 2) & 3]);
+        if (NEXT && ks == 6) read_w<BITS>(A, lds, s + 1, ci, hk, wn);
+        u4 bwn = bw;
+        if (ks + 1 < 8) bwn = dequant_octet<BITS, FAST>(wc, ks + 1, g);
+        else if (NEXT) bwn = dequant_octet<BITS, FAST>(wn, 0, g);
+        mma_step(a[ks & 3], bw, acc);
+        bw = bwn;
+        if (NEXT && ks == 5) barrier_lds();       // stage s + 1 published
+    }
 }
 
-// The compute waves' stages, software-pipelined across the barrier: barrier s + 1
-// publishes stage s + 1, whose LDS reads are then issued before stage s is
-// dequantized and multiplied from registers.  Barrier s + 1 also tells the loaders
-// that stage s's LDS reads have completed (barrier_lds waits for them), so the
-// slot and block reuse rules are those of one stage per barrier.  Unrolled by two
-// so the two register sets alternate without copies.
+// The compute waves' stages, unrolled by two so the chunk registers of stage s and
+// stage s + 1 alternate without copies; the last stage is peeled.
 template <int BITS, bool FAST>
 __device__ __forceinline__ void compute_loop(const GemmArgs& A, const char* lds, int nst, const ColInfo& ci, int hk,
-                                             int sw, const int (&aoff)[2], uint32_t g, f16x (&acc)[2][2]) {
-    StageRegs<BITS> r0, r1;
+                                             int sw, int aoff, uint32_t g, f16x (&acc)[4]) {
+    u4 a[4][4], bw;
+    WStage<BITS> w0, w1;
     barrier_lds();                                // stage 0 published
-    read_stage<BITS>(A, lds, 0, ci, hk, sw, aoff, r0);
+    read_a(lds, 0, 0, aoff, hk, sw, a[0]);
+    read_a(lds, 0, 1, aoff, hk, sw, a[1]);
+    read_w<BITS>(A, lds, 0, ci, hk, w0);
+    bw = dequant_octet<BITS, FAST>(w0, 0, g);
     int s = 0;
     for (; s + 2 < nst; s += 2) {
-        barrier_lds();
-        read_stage<BITS>(A, lds, s + 1, ci, hk, sw, aoff, r1);
-        run_stage<BITS, FAST, false>(A, r0, s, hk, g, acc);
-        barrier_lds();
-        read_stage<BITS>(A, lds, s + 2, ci, hk, sw, aoff, r0);
-        run_stage<BITS, FAST, false>(A, r1, s + 1, hk, g, acc);
+        run_stage<BITS, FAST, true>(A, lds, s, ci, hk, sw, aoff, g, a, bw, w0, w1, acc);
+        run_stage<BITS, FAST, true>(A, lds, s + 1, ci, hk, sw, aoff, g, a, bw, w1, w0, acc);
     }
-    // the last one or two stages (only the last can hold codes at k >= K)
     if (s + 1 < nst) {
-        barrier_lds();
-        read_stage<BITS>(A, lds, s + 1, ci, hk, sw, aoff, r1);
-        run_stage<BITS, FAST, false>(A, r0, s, hk, g, acc);
-        run_stage<BITS, FAST, true>(A, r1, s + 1, hk, g, acc);
+        run_stage<BITS, FAST, true>(A, lds, s, ci, hk, sw, aoff, g, a, bw, w0, w1, acc);
+        run_stage<BITS, FAST, false>(A, lds, s + 1, ci, hk, sw, aoff, g, a, bw, w1, w0, acc);
     } else {
-        run_stage<BITS, FAST, true>(A, r0, s, hk, g, acc);
+        run_stage<BITS, FAST, false>(A, lds, s, ci, hk, sw, aoff, g, a, bw, w0, w1, acc);
     }
 }
 
@@ -489,6 +474,7 @@ __global__ void __launch_bounds__(THREADS) gemm_f16_kernel(const GemmArgs A) {
         vmcnt<0>();
         barrier_lds();                            // weight block 0 and the zero-point flag
         for (int s = 0; s < nst; ++s) {
+            if (s % WBLK == 0) vmcnt<0>();        // block s / WBLK landed: published by barrier s
             barrier_lds();                        // every wave is past stage s-1
             if (s % WBLK == 0) {
                 const int j = s / WBLK + 1;       // the next block: its buffer held block j - 2
@@ -497,40 +483,33 @@ __global__ void __launch_bounds__(THREADS) gemm_f16_kernel(const GemmArgs A) {
                     if (j % rp == 0) issue_sz<BITS>(dw, j / rp, lds);
                 }
             }
-            if (s % WBLK == WBLK - 1) vmcnt<0>();     // landed before the next block's first barrier
         }
         vmcnt<0>();
         return;
     }
 
-    // compute wave: 32 x 32 block (a, b) of the wave tile at rows wm*64 + 32a,
-    // columns wn*64 + 32b
-    const int wm = wave >> 1, wn = wave & 1;
+    // compute wave: the 128 x 32 slab at columns wn * 32 of the tile
+    const int wn = wave;
     const int r32 = lane & 31;
     const int hk = lane >> 5;
     ColInfo ci;
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const int r = wn * 64 + 32 * b + r32;
+    {
+        const int r = wn * 32 + r32;
         const int col = min(n0 + r, A.N - 1);
         const uintptr_t row = reinterpret_cast<uintptr_t>(A.w) + (uintptr_t)col * A.wpr * 4;
-        ci.woff[b] = r * WGeo<BITS>::PITCH + (int)(row & 15);
-        ci.soff[b] = r * 32;
-        ci.cg[b] = (long)col * A.G;
+        ci.woff = r * WGeo<BITS>::PITCH + (int)(row & 15);
+        ci.soff = r * 32;
+        ci.cg = (long)col * A.G;
     }
     const uint32_t g = magic_vreg();
 
-    f16x acc[2][2];
+    f16x acc[4];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
+        for (int v = 0; v < 16; ++v) acc[a][v] = 0.f;
 
-    int aoff[2];
-#pragma unroll
-    for (int a = 0; a < 2; ++a) aoff[a] = (wm * 64 + a * 32 + r32) * 8;
+    const int aoff = r32 * APR;                   // u4 index of row r32 in a stage
     const int sw = swz(r32);                      // rows are 32-aligned + r32
 
     barrier_lds();                                // weight block 0 and the zero-point flag
@@ -539,20 +518,17 @@ __global__ void __launch_bounds__(THREADS) gemm_f16_kernel(const GemmArgs A) {
     else
         compute_loop<BITS, false>(A, lds, nst, ci, hk, sw, aoff, g, acc);
 
-    // D layout of the 32x32 block: lane (j = lane & 31, h = lane >> 5), register
-    // 4g + r holds row 8g + 4h + r, column j
+    // D layout of a 32x32 block: lane (j = lane & 31, h = lane >> 5), register
+    // 4q + r holds row 8q + 4h + r, column j
+    const int n = n0 + wn * 32 + r32;
+    if (n >= A.N) return;
+    const float bias = A.b ? load_f<DT_F16>(A.b, n) : 0.f;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const int n = n0 + wn * 64 + b * 32 + r32;
-        if (n >= A.N) continue;
-        const float bias = A.b ? load_f<DT_F16>(A.b, n) : 0.f;
+    for (int a = 0; a < 4; ++a) {
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = m0 + wm * 64 + a * 32 + 8 * (v >> 2) + 4 * hk + (v & 3);
-                if (m < A.M) store_f<DT_F16>(A.out, (long)m * A.N + n, apply_act(acc[a][b][v] + bias, A.act));
-            }
+        for (int v = 0; v < 16; ++v) {
+            const int m = m0 + 32 * a + 8 * (v >> 2) + 4 * hk + (v & 3);
+            if (m < A.M) store_f<DT_F16>(A.out, (long)m * A.N + n, apply_act(acc[a][v] + bias, A.act));
         }
     }
 }
