@@ -216,7 +216,7 @@ def main():
     achieved = step_bytes / (total_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                "kernel": "gemv_mfma_kernel<3,GEMV,1> (W3 decode GEMV, M=1)",
+                "kernel": "gemv_stream_kernel<GEMV, 3> (W3 decode GEMV, M=1)",
                 "bytes_per_launch_avg": round(step_bytes / (3 * LAYERS)),
                 "avg_launch_us": round(total_ms * 1e3 / (3 * LAYERS), 3), "per_shape": per_shape}
     log(f"roofline: {achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of HBM peak; {per_shape}")

@@ -275,7 +275,7 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
 // size that is a multiple of 32, 32-bit byte offsets into every tensor, and for
 // mixed-width QKV workgroups that stay inside one projection.  The K range of a
 // split is cut into slices of 64 * STREAM_CPL chunks (one wave each, at most 8);
-// rows go 4 to a wave, RW row groups to a workgroup.  `rw` > 0 overrides RW.
+// rows go 4 to a wave, RW row groups to a workgroup.
 struct StreamPlan {
     bool ok = false;
     int P = 1, ks = 1, rw = 2, grid = 0, lds = 0;
@@ -290,7 +290,7 @@ int stream_splits(int64_t C, int split_k) {
     return (int)P;
 }
 
-StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k, int rw_override) {
+StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k) {
     StreamPlan sp;
     const int64_t lim = INT32_MAX;
     bool ok = A.M == 1 && dtype == CBK_F16 && A.gs % 32 == 0 && A.K % 8 == 0 &&
@@ -303,7 +303,7 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k, in
     if ((int64_t)A.C * sp.P >= (1ll << 32)) return sp;     // split bounds C p / P in 32 bits
     sp.ks = (int)ceil_div(ceil_div(A.C, sp.P), slice);
     if (sp.ks > 8) return sp;
-    sp.rw = rw_override > 0 ? rw_override : (sp.ks <= 4 ? 4 : 2);
+    sp.rw = sp.ks <= 4 ? 4 : 2;
     sp.rw = std::max(2, std::min(sp.rw, 16 / sp.ks));
     const int rb = STREAM_RPW * sp.rw;
     if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return sp;
@@ -313,14 +313,6 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k, in
     sp.lds = (int)(sp.ks * slice * 72 + (int64_t)sp.ks * rb * 4);
     sp.ok = true;
     return sp;
-}
-
-int stream_rw_override() {
-    static const int v = [] {
-        const char* e = std::getenv("CRISPYBITS_STREAM_RW");
-        return e ? std::atoi(e) : 0;
-    }();
-    return v;
 }
 
 std::mutex g_attr_mu;
@@ -350,7 +342,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     for (int i = 0; i < 3; ++i)
         xvec = xvec && reinterpret_cast<uintptr_t>(A.p[i].s) % 16 == 0 && reinterpret_cast<uintptr_t>(A.p[i].z) % 16 == 0;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const StreamPlan sp = plan_stream(A, dtype, mixed, split_k, stream_rw_override());
+    const StreamPlan sp = plan_stream(A, dtype, mixed, split_k);
     if (sp.ok) {
         A.P = sp.P;
         A.st_ks = sp.ks;
