@@ -271,46 +271,57 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
     return pl;
 }
 
-// Batch-1 streaming plan (gemv_stream.hip): fp16 x with 16-byte pieces, any group
+// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16 x with 16-byte pieces, any group
 // size that is a multiple of 32, 32-bit byte offsets into every tensor, and for
 // mixed-width QKV workgroups that stay inside one projection.  The K range of a
 // split is cut into slices of 64 * STREAM_CPL chunks (one wave each, at most 8);
 // rows go 4 to a wave, RW row groups to a workgroup.
 struct StreamPlan {
     bool ok = false;
-    int P = 1, ks = 1, rw = 2, grid = 0, lds = 0;
+    int P = 1, ks = 1, rw = 2, mb = 1, grid = 0, lds = 0;
 };
 
+// Slices a streaming job may hold: one wave each within the launch bound (16 waves),
+// and staged activations of 72 bytes per chunk and batch row plus the row-sum area
+// (at most 16 slices x 2 rows x 16 rows x 4 bytes) in the LDS.
+int stream_max_slices(int mb) {
+    const int waves = 16 / STREAM_CPL;
+    const int lds = (LDS_BUDGET - 16 * 2 * 16 * 4) / (64 * STREAM_CPL * 72 * mb);
+    return std::max(1, std::min(waves, lds));
+}
+
 // K splits of the streaming kernel: the requested split, raised until a split's
-// chunks fit 8 slices of 64 * STREAM_CPL.
-int stream_splits(int64_t C, int split_k) {
+// chunks fit `max_slices` slices of 64 * STREAM_CPL.
+int stream_splits(int64_t C, int split_k, int max_slices) {
     const int64_t slice = 64 * STREAM_CPL;
     int64_t P = std::max<int64_t>(1, std::min<int64_t>(split_k, C));
-    while (ceil_div(ceil_div(C, P), slice) > 8 && P < C) ++P;
+    while (ceil_div(ceil_div(C, P), slice) > max_slices && P < C) ++P;
     return (int)P;
 }
 
 StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k) {
     StreamPlan sp;
     const int64_t lim = INT32_MAX;
-    bool ok = A.M == 1 && dtype == CBK_F16 && A.gs % 32 == 0 && A.K % 8 == 0 &&
-              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.K * 2 < lim;
+    bool ok = A.M >= 1 && A.M <= 2 && dtype == CBK_F16 && A.gs % 32 == 0 && A.K % 8 == 0 &&
+              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
     for (int i = 0; i < 3; ++i)
         ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
     if (!ok) return sp;
+    sp.mb = A.M;
+    const int max_waves = 16;                           // the kernel's launch bound: 1024 threads
     const int64_t slice = 64 * STREAM_CPL;
-    sp.P = stream_splits(A.C, split_k);
+    sp.P = stream_splits(A.C, split_k, stream_max_slices(sp.mb));
     if ((int64_t)A.C * sp.P >= (1ll << 32)) return sp;     // split bounds C p / P in 32 bits
     sp.ks = (int)ceil_div(ceil_div(A.C, sp.P), slice);
-    if (sp.ks > 8) return sp;
-    sp.rw = sp.ks <= 4 ? 4 : 2;
-    sp.rw = std::max(2, std::min(sp.rw, 16 / sp.ks));
+    if (sp.ks * STREAM_CPL > max_waves) return sp;
+    sp.rw = sp.ks <= 2 ? 4 : 2;
+    sp.rw = std::max(STREAM_CPL, std::min(sp.rw, max_waves / sp.ks));
     const int rb = STREAM_RPW * sp.rw;
     if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return sp;
     const int64_t grid = ceil_div(A.V, rb) * sp.P;
     if (grid >= lim) return sp;
     sp.grid = (int)grid;
-    sp.lds = (int)(sp.ks * slice * 72 + (int64_t)sp.ks * rb * 4);
+    sp.lds = (int)(sp.ks * slice * 72 * sp.mb + (int64_t)sp.ks * sp.mb * rb * 4);
     sp.ok = true;
     return sp;
 }
@@ -356,7 +367,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
         } else {
             A.partial = nullptr;
         }
-        const void* f = gemv_stream_kernel_for(mode, A.p[0].bits, mixed);
+        const void* f = gemv_stream_kernel_for(mode, A.p[0].bits, mixed, sp.mb);
         hipError_t e = ensure_lds(f, sp.lds);
         if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
         void* args[] = {&A};
@@ -530,7 +541,7 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
             }
         }
     }
-    if (M == 1) P = std::max(P, stream_splits(ceil_div(K, 32), split_k));
+    if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M)));
     return P > 1 ? (int64_t)P * M * V : 0;
 }
 

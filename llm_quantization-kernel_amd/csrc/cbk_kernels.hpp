@@ -15,7 +15,7 @@ hipError_t launch(const void* f, dim3 grid, dim3 block, void** args, size_t lds,
 // queries and the launch; max_batch <= 1 selects the single-row epilogue.
 const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);
 
-// gemv_stream.hip: batch 1, fp16, group size % 32 == 0.  A job is 4 * st_rw virtual
+// gemv_stream.hip: batch 1 or 2 (mb staged activation rows), fp16, group size % 32 == 0.  A job is 4 * st_rw virtual
 // rows x one K split; its workgroup has st_ks * st_rw waves, each over STREAM_RPW rows
 // and one K slice of 64 * STREAM_CPL chunks.
 #ifndef CBK_STREAM_CPL
@@ -23,7 +23,7 @@ const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);
 #endif
 constexpr int STREAM_CPL = CBK_STREAM_CPL;
 constexpr int STREAM_RPW = 4;
-const void* gemv_stream_kernel_for(int mode, int bits, bool mixed);
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb);
 
 // gemv_generic.hip: any dtype / group size; 32 virtual rows x 1 batch row per job.
 constexpr int GENERIC_THREADS = 256;

@@ -2,7 +2,7 @@
 //
 // Replaces cb_gemv_kernel (Kernel/csrc/packed_gemv.cu:83-163) and, when the K
 // range is split, the partial write that cb_reduce_kernel (:166-180) combines,
-// for one activation row (the decode step) in fp16 with any group size that is a
+// for one or two activation rows (the decode step) in fp16 with any group size that is a
 // multiple of 32.  Plain, fused-QKV and fused gate-up modes share the body; the
 // epilogue is cb_epilogue's (:54-81, cbk_device.hpp).
 //
@@ -49,6 +49,7 @@ constexpr int RAW = 0x00020000;          // buffer descriptor word 3: raw 32-bit
 // the join), and the ones that must not contribute read here.
 constexpr int OOR = 0x7FFFFF00;
 
+
 // The offset as an opaque VGPR value, so the compiler keeps the select in front of
 // the load instead of turning it into a branch around two loads.
 __device__ __forceinline__ int vofs(bool ok, int off) {
@@ -84,13 +85,14 @@ __device__ __forceinline__ ProjRes proj_res(const Proj& p, int G) {
     return r;
 }
 
-// Activation chunk at byte offset `off` of x as 16 words of fp16 pairs (x_2i, x_2i+1);
-// codes at k >= K, and the whole chunk when off is OOR, read as zero (the descriptor
-// spans exactly K halves, K % 8 == 0).
-__device__ __forceinline__ void load_x(__amdgpu_buffer_rsrc_t xr, int off, uint32_t (&x)[16]) {
+// Activation chunk ca of batch row b as 16 words of fp16 pairs (x_2i, x_2i+1).  Each
+// 16-byte piece holds 8 codes; K % 8 == 0, so a piece lies wholly before or past K,
+// and pieces past K (and every piece when `ok` is false) read as zero.
+__device__ __forceinline__ void load_x(__amdgpu_buffer_rsrc_t xr, bool ok, int b, int ca, int K, uint32_t (&x)[16]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16 * i, 0, 0);
+        const int k = 32 * ca + 8 * i;
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, vofs(ok && k < K, 2 * (b * K + k)), 0, 0);
         x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
     }
 }
@@ -121,11 +123,9 @@ __device__ __forceinline__ void convert_x(const uint32_t (&x)[16], u4 (&X)[4], f
     xs = t;
 }
 
-// sum x q + B of one row's chunk: 16 decoded pairs against the staged operands.
-template <int BITS>
-__device__ __forceinline__ float chunk_dot(const uint32_t (&w)[BITS], const u4 (&X)[4], uint32_t g) {
-    uint32_t h[16];
-    Decode<BITS>::run(w, h, g);
+// sum x q + B of one row's chunk: its 16 decoded pairs against one batch row's
+// staged operands.
+__device__ __forceinline__ float pairs_dot(const uint32_t (&h)[16], const u4 (&X)[4]) {
     float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -168,7 +168,7 @@ __device__ __forceinline__ void barrier_lds() {
     __builtin_amdgcn_s_barrier();
 }
 
-template <int BITS, int MODE>
+template <int BITS, int MODE, int MB>
 __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -186,12 +186,14 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     const int v0 = vbase + RPW * rw;
     const uint32_t g = magic_vreg();
 
-    // 1a. the thread's activation chunk (job chunk tid; the host keeps RW >= CPL, so
-    // the 64 KS RW threads cover the KS * SLICE staged chunks)
+    // 1a. the thread's activation chunk of every batch row (job chunk tid; the host
+    // keeps RW >= CPL, so the 64 KS RW threads cover the KS * SLICE staged chunks);
+    // batch rows past M read as zero
     const __amdgpu_buffer_rsrc_t xr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.K * 2, RAW);
-    uint32_t xa[16];
-    load_x(xr, vofs(tid < nrange, 64 * (c0 + tid)), xa);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * 2, RAW);
+    uint32_t xa[MB][16];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) load_x(xr, tid < nrange && b < A.M, b, c0 + tid, A.K, xa[b]);
 
     // 1b. the wave's packed chunks and their (scale, zero) halves
     ProjRes R[3];
@@ -230,94 +232,118 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // 2. activations -> LDS: piece q of chunk c at (q NCH + c) * 16, (B, sum x) at
-    // 64 NCH + 8 c; chunks past the split read as zero (they meet no weights)
+    // 2. activations -> LDS: piece q of chunk c of batch row b at ((b * 4 + q) NCH + c) * 16,
+    // (B, sum x) at 64 MB NCH + 8 (b NCH + c); chunks past the split read as zero (they
+    // meet no weights)
     u4* Xl = reinterpret_cast<u4*>(lds);
-    float2* XBl = reinterpret_cast<float2*>(lds + 64 * NCH);
-    float* red = reinterpret_cast<float*>(lds + 72 * NCH);
+    float2* XBl = reinterpret_cast<float2*>(lds + 64 * MB * NCH);
+    float* red = reinterpret_cast<float*>(lds + 72 * MB * NCH);
     if (tid < NCH) {
-        u4 X[4];
-        float B, xs;
-        convert_x<BITS>(xa, X, B, xs);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) Xl[q * NCH + tid] = X[q];
-        XBl[tid] = make_float2(B, xs);
+        for (int b = 0; b < MB; ++b) {
+            u4 X[4];
+            float B, xs;
+            convert_x<BITS>(xa[b], X, B, xs);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) Xl[(b * 4 + q) * NCH + tid] = X[q];
+            XBl[b * NCH + tid] = make_float2(B, xs);
+        }
     }
     barrier_lds();
 
-    // 3. rows
-    u4 X[CPL][4];
-    float2 XB[CPL];
+    // 3. rows: each chunk is decoded once and meets every batch row's activations
+    u4 X[MB][CPL][4];
+    float2 XB[MB][CPL];
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        const int c = ks * SLICE + lane + 64 * i;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) X[i][q] = Xl[q * NCH + c];
-        XB[i] = XBl[c];
-    }
-    float acc[RPW];
-#pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-        float a = 0.f;
+    for (int b = 0; b < MB; ++b) {
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
-            const float d = chunk_dot<BITS>(w[j][i], X[i], g);
+            const int c = ks * SLICE + lane + 64 * i;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) X[b][i][q] = Xl[(b * 4 + q) * NCH + c];
+            XB[b][i] = XBl[b * NCH + c];
+        }
+    }
+    float acc[MB][RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[b][j] = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            uint32_t h[16];
+            Decode<BITS>::run(w[j][i], h, g);
             const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[j][i][0]);
             const float z = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[j][i][1]);
-            a = fmaf(s, d - fmaf(z, XB[i].y, XB[i].x), a);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                const float d = pairs_dot(h, X[b][i]);
+                acc[b][j] = fmaf(s, d - fmaf(z, XB[b][i].y, XB[b][i].x), acc[b][j]);
+            }
         }
-        acc[j] = a;
     }
 
-    // 4. row totals of the wave
-    const float tot = reduce4(acc);
-    if ((lane & 15) == 0) red[ks * RB + RPW * rw + lane_row(lane)] = tot;
+    // 4. row totals of the wave, per batch row
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        const float tot = reduce4(acc[b]);
+        if ((lane & 15) == 0) red[(ks * MB + b) * RB + RPW * rw + lane_row(lane)] = tot;
+    }
     barrier_lds();
 
     // 5. slices in order, then the epilogue (or the split's partial)
-    if (tid < RB) {
-        const int v = vbase + tid;
-        if (v < A.V) {
+    for (int t = tid; t < MB * RB; t += 64 * KS * RW) {
+        const int b = t / RB, row = t - b * RB;
+        const int v = vbase + row;
+        if (b < A.M && v < A.V) {
             float mine = 0.f, partner = 0.f;
             for (int k = 0; k < KS; ++k) {
-                mine += red[k * RB + tid];
-                partner += red[k * RB + (tid ^ 1)];
+                mine += red[(k * MB + b) * RB + row];
+                partner += red[(k * MB + b) * RB + (row ^ 1)];
             }
-            if (A.P == 1) epilogue<DT_F16, MODE>(A, 0, v, mine, partner);
-            else A.partial[(long)p * A.V + v] = mine;
+            if (A.P == 1) epilogue<DT_F16, MODE>(A, b, v, mine, partner);
+            else A.partial[((long)p * A.M + b) * A.V + v] = mine;
         }
     }
 }
 
 // BITS = 0: fused QKV with a width per projection; the host keeps each
 // workgroup's rows inside one projection, so the width is uniform per workgroup.
-template <int MODE, int BITS>
+// MB batch rows (1 or 2; rows past M are zero).  Wider batches stage MB copies of
+// the activations, which at K = 11008 leaves one workgroup per CU; they take the
+// batch-rows MFMA kernel instead.
+template <int MODE, int BITS, int MB>
 __global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
-        stream_body<BITS, MODE>(A, lds);
+        stream_body<BITS, MODE, MB>(A, lds);
     } else {
         int proj, r;
         vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * 4 * A.st_rw, proj, r);
         const int bits = CBK_SEL(A, proj, bits);
-        if (bits == 2) stream_body<2, MODE>(A, lds);
-        else if (bits == 3) stream_body<3, MODE>(A, lds);
-        else stream_body<4, MODE>(A, lds);
+        if (bits == 2) stream_body<2, MODE, MB>(A, lds);
+        else if (bits == 3) stream_body<3, MODE, MB>(A, lds);
+        else stream_body<4, MODE, MB>(A, lds);
     }
 }
 
-}  // namespace
-
-const void* gemv_stream_kernel_for(int mode, int bits, bool mixed) {
-    if (mixed) return reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_QKV, 0>);
+template <int MB>
+const void* stream_kernel(int mode, int bits, bool mixed) {
+    if (mixed) return reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_QKV, 0, MB>);
 #define CBK_STREAM_K(M)                                                                            \
-    (bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 2>)                          \
-               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 3>)             \
-                            : reinterpret_cast<const void*>(&gemv_stream_kernel<M, 4>)))
+    (bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 2, MB>)                      \
+               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 3, MB>)         \
+                            : reinterpret_cast<const void*>(&gemv_stream_kernel<M, 4, MB>)))
     if (mode == MODE_QKV) return CBK_STREAM_K(MODE_QKV);
     if (mode == MODE_GATEUP) return CBK_STREAM_K(MODE_GATEUP);
     return CBK_STREAM_K(MODE_GEMV);
 #undef CBK_STREAM_K
+}
+
+}  // namespace
+
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb) {
+    return mb <= 1 ? stream_kernel<1>(mode, bits, mixed) : stream_kernel<2>(mode, bits, mixed);
 }
 
 }  // namespace cbk
