@@ -326,6 +326,65 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k) {
     return sp;
 }
 
+// Batched streaming plan (gemv_stream.hip, bstream), batch 3..16: fp16 x with
+// 16-byte pieces, group sizes that are multiples of 128 (a unit of 128 codes is one
+// group), 32-bit offsets, and rows that keep every 16-row tile inside one projection
+// (fused QKV: Q and K widths multiples of 16; mixed widths: of the workgroup's rows).
+// K is split over units; a split's units are cut into slices of STREAM_BSU (one wave
+// each, at most 16 waves); the split grows until the staged activations
+// (64 bytes per chunk and batch row), the unit sums and the row sums fit the LDS.
+struct BStreamPlan {
+    bool ok = false;
+    int P = 1, ks = 1, rw = 1, grid = 0, lds = 0;
+};
+
+int64_t bstream_lds(int64_t ks, int64_t M, int64_t rw) {
+    const int64_t nu = ks * STREAM_BSU;
+    return 64 * 4 * nu * M + 2 * 16 * nu * 4 + 4 * ks * M * 16 * rw;
+}
+
+// K splits of the batched streaming kernel (also the partial-buffer bound).
+int bstream_splits(int64_t C, int64_t M, int split_k, int rw) {
+    const int64_t U = ceil_div(C, 4);
+    int64_t P = std::max<int64_t>(1, std::min<int64_t>(split_k, U));
+    while (P < U) {
+        const int64_t ks = ceil_div(ceil_div(U, P), STREAM_BSU);
+        if (ks * rw <= 16 && bstream_lds(ks, M, rw) <= LDS_BUDGET) break;
+        ++P;
+    }
+    return (int)P;
+}
+
+BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k) {
+    BStreamPlan bp;
+    const int64_t lim = INT32_MAX;
+    bool ok = A.M >= 3 && A.M <= 16 && dtype == CBK_F16 && A.gs % 128 == 0 && A.K % 8 == 0 &&
+              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
+    for (int i = 0; i < 3; ++i)
+        ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
+    if (mode == CBK_MODE_QKV) ok = ok && A.p[0].n % 16 == 0 && A.p[1].n % 16 == 0;
+    if (!ok) return bp;
+    // row groups: enough threads to stage the activations two items per thread
+    // (4 STREAM_BSU M items over 64 threads per wave), and for gate-up an even count
+    // (one wave per projection of 16 pair rows)
+    bp.rw = (int)std::max<int64_t>(1, ceil_div(A.M * STREAM_BSU, 32));
+    if (mode == CBK_MODE_GATEUP) bp.rw = (bp.rw + 1) & ~1;
+    const int64_t U = ceil_div(A.C, 4);
+    bp.P = bstream_splits(A.C, A.M, split_k, bp.rw);
+    if ((int64_t)U * bp.P >= (1ll << 32)) return bp;
+    bp.ks = (int)ceil_div(ceil_div(U, bp.P), STREAM_BSU);
+    if (bp.ks * bp.rw > 16) return bp;
+    bp.lds = (int)bstream_lds(bp.ks, A.M, bp.rw);
+    if (bp.lds > LDS_BUDGET) return bp;
+    const int rb = 16 * bp.rw;
+    if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return bp;
+    const int64_t grid = ceil_div(A.V, rb) * bp.P;
+    if (grid >= lim) return bp;
+    bp.grid = (int)grid;
+    bp.ok = true;
+    return bp;
+}
+
 std::mutex g_attr_mu;
 
 hipError_t ensure_lds(const void* f, int bytes) {
@@ -372,6 +431,32 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
         if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
         void* args[] = {&A};
         e = launch(f, dim3(sp.grid), dim3(64 * sp.ks * sp.rw), args, (size_t)sp.lds, s);
+        if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
+        if (A.P > 1) {
+            e = launch_gemv_reduce(A, dtype, mode, s);
+            if (e != hipSuccess) return hip_fail(e, "packed_gemv: reduce launch");
+        }
+        return CBK_OK;
+    }
+    const BStreamPlan bp = plan_bstream(A, dtype, mode, mixed, split_k);
+    if (bp.ok) {
+        A.P = bp.P;
+        A.st_ks = bp.ks;
+        A.st_rw = bp.rw;
+        A.divP = make_fastdiv((uint32_t)A.P);
+        A.divRW = make_fastdiv((uint32_t)A.st_rw);
+        A.divG = make_fastdiv((uint32_t)(A.gs / 128));
+        if (A.P > 1) {
+            if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
+            A.partial = partial;
+        } else {
+            A.partial = nullptr;
+        }
+        const void* f = gemv_bstream_kernel_for(mode, A.p[0].bits, mixed);
+        hipError_t e = ensure_lds(f, bp.lds);
+        if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
+        void* args[] = {&A};
+        e = launch(f, dim3(bp.grid), dim3(64 * bp.ks * bp.rw), args, (size_t)bp.lds, s);
         if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
         if (A.P > 1) {
             e = launch_gemv_reduce(A, dtype, mode, s);
@@ -542,6 +627,8 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
         }
     }
     if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M)));
+    if (M >= 3 && M <= 16)
+        P = std::max(P, bstream_splits(ceil_div(K, 32), M, split_k, (int)((ceil_div(M * STREAM_BSU, 32) + 1) & ~1)));
     return P > 1 ? (int64_t)P * M * V : 0;
 }
 

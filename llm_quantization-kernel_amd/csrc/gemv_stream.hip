@@ -36,6 +36,8 @@ namespace cbk {
 namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u3 __attribute__((ext_vector_type(3)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
@@ -307,6 +309,189 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     }
 }
 
+// ------------------------------------------------------------------ batch rows 3..16
+// Job = (block of RB = 16 RW virtual rows, K split p over 128-code units).  A
+// workgroup holds KS x RW waves: wave (ks, rw) takes 16 rows of the block over K
+// slice ks, BSU units; lane (j = l & 15, kq = l >> 4) owns chunk 4 u + kq of row j
+// for each unit u of the slice, so one buffer load per unit moves 16 rows x 4
+// consecutive chunks.  The decoded chunk is the B operand of four
+// v_mfma_f32_16x16x32_f16 whose A operand holds the M activation rows staged in
+// the decode's operand order:
+//   D[i][j] = sum_k x[i][k] (B(k) + q[j][k]) over the unit,
+//   acc[i][j] += s[j] (D[i][j] - XB[i] - z[j] X[i])
+// with X = sum x and XB = sum x B(k) over the unit (a unit is one group: the host
+// requires g % 128 == 0).  The MFMA sums over k, so no cross-lane reduction is
+// needed; lane (j, kq) holds batch rows 4 kq .. 4 kq + 3 of row j.  Gate-up rows
+// alternate between the waves of a workgroup (even waves gate, odd waves up, the
+// same 16 pair rows), so every wave's rows lie in one projection and its buffer
+// descriptors stay uniform.
+constexpr int BSU = STREAM_BSU;           // units per K slice
+
+template <int BITS, int MODE>
+__device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KS = A.st_ks, RW = A.st_rw, RB = 16 * A.st_rw, M = A.M;
+    const int NU = KS * BSU, NCH = 4 * NU;
+    const int nthr = 64 * KS * RW;
+    const int ks = (int)fdiv((uint32_t)wave, A.divRW);
+    const int rw = wave - ks * RW;
+    const int blk = (int)fdiv(blockIdx.x, A.divP);     // job = blk * P + p (split fastest)
+    const int p = blockIdx.x - blk * A.P;
+    // split p covers units [U p / P, U (p + 1) / P) of the row's U = ceil(C / 4)
+    const int U = (A.C + 3) >> 2;
+    const int u0 = (int)fdiv((uint32_t)(U * p), A.divP);
+    const int u1 = (int)fdiv((uint32_t)(U * (p + 1)), A.divP);
+    const int c0 = 4 * u0;                        // first chunk of the split
+    const int nrange = min(4 * u1, A.C) - c0;     // its chunks
+    const int vbase = blk * RB;
+    const int j = lane & 15, kq = lane >> 4;
+    const uint32_t g = magic_vreg();
+
+    // the wave's 16 rows: virtual rows vbase + 16 rw + j, or for gate-up projection
+    // rw & 1 of pair rows vbase / 2 + 16 (rw >> 1) + j (virtual rows 2 n + (rw & 1))
+    int roff, vfirst;
+    if constexpr (MODE == MODE_GATEUP) {
+        vfirst = vbase + 32 * (rw >> 1) + (rw & 1);
+        roff = 32 * (rw >> 1) + 2 * j + (rw & 1);
+    } else {
+        vfirst = vbase + 16 * rw;
+        roff = 16 * rw + j;
+    }
+    const int vrow = vbase + roff;
+    int proj, rfirst;
+    vmap<MODE>(A, min(vfirst, A.V - 1), proj, rfirst);
+    const int r = rfirst + j;                     // the lane's row in its projection
+    const bool vin = vrow < A.V;
+
+    // 1a. the thread's activation items t = tid + e * nthr, e < 2: (job chunk c, batch row
+    // i) = (t mod NCH, t / NCH); the host keeps NCH * M <= 2 * nthr, so these are all of
+    // them, and they are requested before the weights so that the staging waits for
+    // them only
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * 2, RAW);
+    uint32_t xa[2][16];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int t = tid + e * nthr, i = t / NCH, c = t - i * NCH;
+        load_x(xr, i < M && c < nrange, i, c0 + c, A.K, xa[e]);
+    }
+
+    // 1b. the wave's packed chunks and the (scale, zero) of each unit's group
+    ProjRes R[3];
+    R[0] = proj_res(A.p[0], A.G);
+    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.p[1], A.G);
+    if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.p[1], A.G); R[2] = proj_res(A.p[2], A.G); }
+    const ProjRes& P = proj == 0 ? R[0] : (proj == 1 ? R[1] : R[2]);
+    const int wpr = CBK_SEL(A, proj, wpr);
+    uint32_t w[BSU][BITS];
+    uint32_t sz[BSU][2];
+#pragma unroll
+    for (int u = 0; u < BSU; ++u) {
+        const int c = 4 * (ks * BSU + u) + kq;
+        const bool ok = vin && c < nrange;
+        const int gu = (int)fdiv((uint32_t)(u0 + ks * BSU + u), A.divG);    // the unit's group
+        const int so = vofs(vin && 4 * (ks * BSU + u) < nrange, 2 * (r * A.G + gu));
+        load_chunk<BITS>(P.w, vofs(ok, 4 * (r * wpr + (c0 + c) * BITS)), w[u]);
+        sz[u][0] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
+        sz[u][1] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);        // units issued in the order they are consumed
+    }
+
+    // 2. activations -> LDS: piece m of chunk c of batch row i at ((m NCH + c) M + i) * 16;
+    // per unit and batch row its sums X (at XSu[u * 16 + i]) and XB (XBu[u * 16 + i])
+    u4* Xl = reinterpret_cast<u4*>(lds);
+    float* XSu = reinterpret_cast<float*>(lds + 64 * NCH * M);
+    float* XBu = XSu + 16 * NU;
+    float* red = XBu + 16 * NU;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int t = tid + e * nthr, i = t / NCH, c = t - i * NCH;
+        if (t >= NCH * M) break;                  // whole quads of threads leave together (NCH % 4 == 0)
+        u4 X[4];
+        float B, xs;
+        convert_x<BITS>(xa[e], X, B, xs);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) Xl[(m * NCH + c) * M + i] = X[m];
+        // the 4 chunks of a unit are 4 consecutive threads (NCH % 4 == 0)
+        B += __shfl_xor(B, 1, 64);
+        xs += __shfl_xor(xs, 1, 64);
+        B += __shfl_xor(B, 2, 64);
+        xs += __shfl_xor(xs, 2, 64);
+        if ((c & 3) == 0) {
+            XSu[(c >> 2) * 16 + i] = xs;
+            XBu[(c >> 2) * 16 + i] = B;
+        }
+    }
+    barrier_lds();
+
+    // 3. units: A operands of batch row min(j, M - 1) (rows past M repeat a staged row;
+    // their D rows are not stored)
+    const int ia = min(j, M - 1);
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < BSU; ++u) {
+        const int uj = ks * BSU + u;              // job-local unit
+        const int c = 4 * uj + kq;
+        u4 a[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) a[m] = Xl[(m * NCH + c) * M + ia];
+        const f4 X4 = *reinterpret_cast<const f4*>(XSu + uj * 16 + 4 * kq);
+        const f4 XB4 = *reinterpret_cast<const f4*>(XBu + uj * 16 + 4 * kq);
+        uint32_t h[16];
+        Decode<BITS>::run(w[u], h, g);
+        f4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const u4 bw = {h[4 * m], h[4 * m + 1], h[4 * m + 2], h[4 * m + 3]};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8*>(&a[m]),
+                                                       *reinterpret_cast<const h8*>(&bw), d, 0, 0, 0);
+        }
+        const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[u][0]);
+        const float ze = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[u][1]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = fmaf(sc, fmaf(-ze, X4[q], d[q] - XB4[q]), acc[q]);
+    }
+
+    // 4. row totals per slice: lane (j, kq) holds batch rows 4 kq + q of row j
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = 4 * kq + q;
+        if (i < M) red[(ks * M + i) * RB + roff] = acc[q];
+    }
+    barrier_lds();
+
+    // 5. slices in order, then the epilogue (or the split's partial)
+    for (int t = tid; t < M * RB; t += nthr) {
+        const int b = t / RB, ro = t - b * RB;
+        const int v = vbase + ro;
+        if (v < A.V) {
+            float mine = 0.f, partner = 0.f;
+            for (int k = 0; k < KS; ++k) {
+                mine += red[(k * M + b) * RB + ro];
+                partner += red[(k * M + b) * RB + (ro ^ 1)];
+            }
+            if (A.P == 1) epilogue<DT_F16, MODE>(A, b, v, mine, partner);
+            else A.partial[((long)p * A.M + b) * A.V + v] = mine;
+        }
+    }
+}
+
+template <int MODE, int BITS>
+__global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    if constexpr (BITS != 0) {
+        bstream_body<BITS, MODE>(A, lds);
+    } else {
+        int proj, r;
+        vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * 16 * A.st_rw, proj, r);
+        const int bits = CBK_SEL(A, proj, bits);
+        if (bits == 2) bstream_body<2, MODE>(A, lds);
+        else if (bits == 3) bstream_body<3, MODE>(A, lds);
+        else bstream_body<4, MODE>(A, lds);
+    }
+}
+
 // BITS = 0: fused QKV with a width per projection; the host keeps each
 // workgroup's rows inside one projection, so the width is uniform per workgroup.
 // MB batch rows (1 or 2; rows past M are zero).  Wider batches stage MB copies of
@@ -344,6 +529,18 @@ const void* stream_kernel(int mode, int bits, bool mixed) {
 
 const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb) {
     return mb <= 1 ? stream_kernel<1>(mode, bits, mixed) : stream_kernel<2>(mode, bits, mixed);
+}
+
+const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed) {
+    if (mixed) return reinterpret_cast<const void*>(&gemv_bstream_kernel<MODE_QKV, 0>);
+#define CBK_BSTREAM_K(M)                                                                           \
+    (bits == 2 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 2>)                         \
+               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 3>)            \
+                            : reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 4>)))
+    if (mode == MODE_QKV) return CBK_BSTREAM_K(MODE_QKV);
+    if (mode == MODE_GATEUP) return CBK_BSTREAM_K(MODE_GATEUP);
+    return CBK_BSTREAM_K(MODE_GEMV);
+#undef CBK_BSTREAM_K
 }
 
 }  // namespace cbk
