@@ -205,11 +205,16 @@ def main():
     log(f"timed: {args.steps} steps, {ms_per_step:.4f} ms/step, {value:.1f} GB/s")
 
     # ---------------------------------------------------------------- roofline of the dominant kernel
-    total_ms, durs = timed_kernels(C, step_eager, 3 * LAYERS)
-    per_shape = []
+    # per shape: the 32 calls of that shape, timed per dispatch; a call's time is the sum
+    # of its dispatches (a split-K call also launches the combine)
+    total_ms, per_shape = 0.0, []
     for s, (K, N) in enumerate(SHAPES):
-        d = durs[s::3]
-        us = statistics.mean(d) * 1e3
+        def run_shape():
+            for lw in layers:
+                ops.packed_linear(xs[s], lw[s], cfg[s][0], cfg[s][1])
+        t, _ = timed_kernels(C, run_shape, 2 * LAYERS)
+        total_ms += t
+        us = t * 1e3 / LAYERS
         per_shape.append({"K": K, "N": N, "bits": bits, "M": 1, "us": round(us, 3),
                           "GBps": round(gemv_bytes(1, K, N, bits) / (us * 1e-6) / 1e9, 1),
                           "split_k": cfg[s][0], "rho": cfg[s][1]})
@@ -289,7 +294,7 @@ def gemv_sweep(torch, C, ops, dev):
                 run = lambda: [ops.packed_linear(x, w, sk, rho) for w in ws]
                 run()
                 total, durs = timed_kernels(C, run, 2 * len(ws))
-                us = total * 1e3 / len(durs)
+                us = total * 1e3 / len(ws)          # per call: a split-K call also launches the combine
                 gbs = gemv_bytes(M, K, N, bits) / (us * 1e-6) / 1e9
                 rows.append({"bits": bits, "M": M, "K": K, "N": N, "us": round(us, 3), "GBps": round(gbs, 1),
                              "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "split_k": sk, "rho": rho})
@@ -309,7 +314,7 @@ def fused_sweep(torch, C, ops, dev):
     run = lambda: [ops.fused_qkv(x, *ws) for ws in sets]
     run()
     total, durs = timed_kernels(C, run, 2 * len(sets))
-    us = total * 1e3 / len(durs)
+    us = total * 1e3 / len(sets)
     nbytes = sum(gemv_bytes(1, 4096, 4096, b) for b in qkv_bits) - 2 * 4096 * 2
     res["qkv"] = {"bits": qkv_bits, "K": 4096, "N": [4096] * 3, "us": round(us, 3),
                   "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
@@ -319,7 +324,7 @@ def fused_sweep(torch, C, ops, dev):
     run = lambda: [ops.fused_gate_up(x, g, u) for g, u in pairs]
     run()
     total, durs = timed_kernels(C, run, 2 * len(pairs))
-    us = total * 1e3 / len(durs)
+    us = total * 1e3 / len(pairs)
     nbytes = 2 * gemv_bytes(1, 4096, 11008, 3) - 4096 * 2 - 11008 * 2
     res["gate_up"] = {"bits": 3, "K": 4096, "N": [11008, 11008], "us": round(us, 3),
                       "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
@@ -337,8 +342,8 @@ def gemm_sweep(torch, C, ops, dev):
                 ws += [clone_weight(ws[0]) for _ in range(2)]
                 run = lambda: [ops.packed_linear(x, w) for w in ws * 2]
                 run()
-                total, durs = timed_kernels(C, run, len(ws) * 2)
-                us = total * 1e3 / len(durs)
+                total, durs = timed_kernels(C, run, len(ws) * 4)
+                us = total * 1e3 / (2 * len(ws))
                 tfs = 2.0 * M * N * K / (us * 1e-6) / 1e12
                 rows.append({"M": M, "K": K, "N": N, "bits": bits, "us": round(us, 2), "TFLOPs": round(tfs, 1),
                              "pct_peak": round(100 * tfs / MFMA_F16_PEAK_TFS, 1)})

@@ -330,26 +330,36 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k) {
 // 16-byte pieces, group sizes that are multiples of 128 (a unit of 128 codes is one
 // group), 32-bit offsets, and rows that keep every 16-row tile inside one projection
 // (fused QKV: Q and K widths multiples of 16; mixed widths: of the workgroup's rows).
-// K is split over units; a split's units are cut into slices of STREAM_BSU (one wave
-// each, at most 16 waves); the split grows until the staged activations
-// (64 bytes per chunk and batch row), the unit sums and the row sums fit the LDS.
+// K is split over units; a split's units are cut into slices of bsu units (one wave
+// each, at most 16 waves): 4 where that needs no split, else 8 (a split costs a
+// second launch).  The split grows until the staged activations (64 bytes per chunk
+// and batch row), the unit sums and the row sums fit the LDS.
 struct BStreamPlan {
     bool ok = false;
-    int P = 1, ks = 1, rw = 1, grid = 0, lds = 0;
+    int P = 1, ks = 1, rw = 1, bsu = 4, grid = 0, lds = 0;
 };
 
-int64_t bstream_lds(int64_t ks, int64_t M, int64_t rw) {
-    const int64_t nu = ks * STREAM_BSU;
+int64_t bstream_lds(int64_t ks, int64_t M, int64_t rw, int bsu) {
+    const int64_t nu = ks * bsu;
     return 64 * 4 * nu * M + 2 * 16 * nu * 4 + 4 * ks * M * 16 * rw;
 }
 
-// K splits of the batched streaming kernel (also the partial-buffer bound).
-int bstream_splits(int64_t C, int64_t M, int split_k, int rw) {
+// Row groups: enough threads to stage the activations two items per thread (4 bsu M
+// items over 64 threads per wave), and for gate-up an even count (one wave per
+// projection of 16 pair rows).
+int bstream_rw(int64_t M, int bsu, bool gateup) {
+    int rw = (int)std::max<int64_t>(1, ceil_div(M * bsu, 32));
+    if (gateup) rw = (rw + 1) & ~1;
+    return rw;
+}
+
+// K splits of the batched streaming kernel for slices of bsu units.
+int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu) {
     const int64_t U = ceil_div(C, 4);
     int64_t P = std::max<int64_t>(1, std::min<int64_t>(split_k, U));
     while (P < U) {
-        const int64_t ks = ceil_div(ceil_div(U, P), STREAM_BSU);
-        if (ks * rw <= 16 && bstream_lds(ks, M, rw) <= LDS_BUDGET) break;
+        const int64_t ks = ceil_div(ceil_div(U, P), bsu);
+        if (ks * rw <= 16 && bstream_lds(ks, M, rw, bsu) <= LDS_BUDGET) break;
         ++P;
     }
     return (int)P;
@@ -364,17 +374,24 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
         ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
     if (mode == CBK_MODE_QKV) ok = ok && A.p[0].n % 16 == 0 && A.p[1].n % 16 == 0;
     if (!ok) return bp;
-    // row groups: enough threads to stage the activations two items per thread
-    // (4 STREAM_BSU M items over 64 threads per wave), and for gate-up an even count
-    // (one wave per projection of 16 pair rows)
-    bp.rw = (int)std::max<int64_t>(1, ceil_div(A.M * STREAM_BSU, 32));
-    if (mode == CBK_MODE_GATEUP) bp.rw = (bp.rw + 1) & ~1;
+    const bool gateup = mode == CBK_MODE_GATEUP;
     const int64_t U = ceil_div(A.C, 4);
-    bp.P = bstream_splits(A.C, A.M, split_k, bp.rw);
+    bp.bsu = 4;
+    bp.rw = bstream_rw(A.M, 4, gateup);
+    bp.P = bstream_splits(A.C, A.M, split_k, bp.rw, 4);
+    if (bp.P > std::max(split_k, 1)) {           // 4-unit slices would add a split: try 8
+        const int rw8 = bstream_rw(A.M, 8, gateup);
+        const int p8 = bstream_splits(A.C, A.M, split_k, rw8, 8);
+        if (p8 < bp.P) {
+            bp.bsu = 8;
+            bp.rw = rw8;
+            bp.P = p8;
+        }
+    }
     if ((int64_t)U * bp.P >= (1ll << 32)) return bp;
-    bp.ks = (int)ceil_div(ceil_div(U, bp.P), STREAM_BSU);
+    bp.ks = (int)ceil_div(ceil_div(U, bp.P), bp.bsu);
     if (bp.ks * bp.rw > 16) return bp;
-    bp.lds = (int)bstream_lds(bp.ks, A.M, bp.rw);
+    bp.lds = (int)bstream_lds(bp.ks, A.M, bp.rw, bp.bsu);
     if (bp.lds > LDS_BUDGET) return bp;
     const int rb = 16 * bp.rw;
     if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return bp;
@@ -452,7 +469,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
         } else {
             A.partial = nullptr;
         }
-        const void* f = gemv_bstream_kernel_for(mode, A.p[0].bits, mixed);
+        const void* f = gemv_bstream_kernel_for(mode, A.p[0].bits, mixed, bp.bsu);
         hipError_t e = ensure_lds(f, bp.lds);
         if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
         void* args[] = {&A};
@@ -627,8 +644,8 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
         }
     }
     if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M)));
-    if (M >= 3 && M <= 16)
-        P = std::max(P, bstream_splits(ceil_div(K, 32), M, split_k, (int)((ceil_div(M * STREAM_BSU, 32) + 1) & ~1)));
+    if (M >= 3 && M <= 16)    // 4-unit slices split at least as often as 8-unit ones; gate-up rows
+        P = std::max(P, bstream_splits(ceil_div(K, 32), M, split_k, bstream_rw(M, 4, true), 4));
     return P > 1 ? (int64_t)P * M * V : 0;
 }
 

@@ -26,12 +26,8 @@ constexpr int STREAM_RPW = 4;
 const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb);
 // gemv_stream.hip: batch 3..16, fp16, group size % 128 == 0.  A job is 16 * st_rw virtual
 // rows x one K split (over 128-code units); its workgroup has st_ks * st_rw waves, each
-// over 16 rows and one K slice of STREAM_BSU units.
-#ifndef CBK_STREAM_BSU
-#define CBK_STREAM_BSU 4
-#endif
-constexpr int STREAM_BSU = CBK_STREAM_BSU;
-const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed);
+// over 16 rows and one K slice of bsu (4 or 8) units.
+const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu);
 
 // gemv_generic.hip: any dtype / group size; 32 virtual rows x 1 batch row per job.
 constexpr int GENERIC_THREADS = 256;

@@ -312,7 +312,7 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
 // ------------------------------------------------------------------ batch rows 3..16
 // Job = (block of RB = 16 RW virtual rows, K split p over 128-code units).  A
 // workgroup holds KS x RW waves: wave (ks, rw) takes 16 rows of the block over K
-// slice ks, BSU units; lane (j = l & 15, kq = l >> 4) owns chunk 4 u + kq of row j
+// slice ks, BSU (4 or 8) units; lane (j = l & 15, kq = l >> 4) owns chunk 4 u + kq of row j
 // for each unit u of the slice, so one buffer load per unit moves 16 rows x 4
 // consecutive chunks.  The decoded chunk is the B operand of four
 // v_mfma_f32_16x16x32_f16 whose A operand holds the M activation rows staged in
@@ -325,9 +325,8 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
 // alternate between the waves of a workgroup (even waves gate, odd waves up, the
 // same 16 pair rows), so every wave's rows lie in one projection and its buffer
 // descriptors stay uniform.
-constexpr int BSU = STREAM_BSU;           // units per K slice
 
-template <int BITS, int MODE>
+template <int BITS, int MODE, int BSU>
 __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -384,17 +383,24 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.p[1], A.G); R[2] = proj_res(A.p[2], A.G); }
     const ProjRes& P = proj == 0 ? R[0] : (proj == 1 ? R[1] : R[2]);
     const int wpr = CBK_SEL(A, proj, wpr);
+    // the (scale, zero) of unit 4 e + kq's group of row j: BSU / 4 2-byte gathers each per
+    // wave (lanes of a row then share them by ds_bpermute), rather than one per unit
+    static_assert(BSU % 4 == 0, "whole units per lane quarter");
+    uint32_t s_own[BSU / 4], z_own[BSU / 4];
+#pragma unroll
+    for (int e = 0; e < BSU / 4; ++e) {
+        const int ul = ks * BSU + 4 * e + kq;
+        const int gu = (int)fdiv((uint32_t)(u0 + ul), A.divG);   // the unit's group
+        const int so = vofs(vin && 4 * ul < nrange, 2 * (r * A.G + gu));
+        s_own[e] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
+        z_own[e] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
+    }
     uint32_t w[BSU][BITS];
-    uint32_t sz[BSU][2];
 #pragma unroll
     for (int u = 0; u < BSU; ++u) {
         const int c = 4 * (ks * BSU + u) + kq;
         const bool ok = vin && c < nrange;
-        const int gu = (int)fdiv((uint32_t)(u0 + ks * BSU + u), A.divG);    // the unit's group
-        const int so = vofs(vin && 4 * (ks * BSU + u) < nrange, 2 * (r * A.G + gu));
         load_chunk<BITS>(P.w, vofs(ok, 4 * (r * wpr + (c0 + c) * BITS)), w[u]);
-        sz[u][0] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
-        sz[u][1] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
         __builtin_amdgcn_sched_barrier(0);        // units issued in the order they are consumed
     }
 
@@ -447,8 +453,11 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
             d = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8*>(&a[m]),
                                                        *reinterpret_cast<const h8*>(&bw), d, 0, 0, 0);
         }
-        const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[u][0]);
-        const float ze = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[u][1]);
+        // unit u's scale and zero sit in lane (j, u % 4), set u / 4
+        const uint32_t su = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (j + 16 * (u & 3)), (int)s_own[u >> 2]);
+        const uint32_t zu = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (j + 16 * (u & 3)), (int)z_own[u >> 2]);
+        const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)su);
+        const float ze = (float)__builtin_bit_cast(_Float16, (uint16_t)zu);
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[q] = fmaf(sc, fmaf(-ze, X4[q], d[q] - XB4[q]), acc[q]);
     }
@@ -477,18 +486,18 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     }
 }
 
-template <int MODE, int BITS>
+template <int MODE, int BITS, int BSU>
 __global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
-        bstream_body<BITS, MODE>(A, lds);
+        bstream_body<BITS, MODE, BSU>(A, lds);
     } else {
         int proj, r;
         vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * 16 * A.st_rw, proj, r);
         const int bits = CBK_SEL(A, proj, bits);
-        if (bits == 2) bstream_body<2, MODE>(A, lds);
-        else if (bits == 3) bstream_body<3, MODE>(A, lds);
-        else bstream_body<4, MODE>(A, lds);
+        if (bits == 2) bstream_body<2, MODE, BSU>(A, lds);
+        else if (bits == 3) bstream_body<3, MODE, BSU>(A, lds);
+        else bstream_body<4, MODE, BSU>(A, lds);
     }
 }
 
@@ -525,22 +534,28 @@ const void* stream_kernel(int mode, int bits, bool mixed) {
 #undef CBK_STREAM_K
 }
 
+template <int BSU>
+const void* bstream_kernel(int mode, int bits, bool mixed) {
+    if (mixed) return reinterpret_cast<const void*>(&gemv_bstream_kernel<MODE_QKV, 0, BSU>);
+#define CBK_BSTREAM_K(M)                                                                           \
+    (bits == 2 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 2, BSU>)                    \
+               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 3, BSU>)       \
+                            : reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 4, BSU>)))
+    if (mode == MODE_QKV) return CBK_BSTREAM_K(MODE_QKV);
+    if (mode == MODE_GATEUP) return CBK_BSTREAM_K(MODE_GATEUP);
+    return CBK_BSTREAM_K(MODE_GEMV);
+#undef CBK_BSTREAM_K
+}
+
 }  // namespace
 
 const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb) {
     return mb <= 1 ? stream_kernel<1>(mode, bits, mixed) : stream_kernel<2>(mode, bits, mixed);
 }
 
-const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed) {
-    if (mixed) return reinterpret_cast<const void*>(&gemv_bstream_kernel<MODE_QKV, 0>);
-#define CBK_BSTREAM_K(M)                                                                           \
-    (bits == 2 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 2>)                         \
-               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 3>)            \
-                            : reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 4>)))
-    if (mode == MODE_QKV) return CBK_BSTREAM_K(MODE_QKV);
-    if (mode == MODE_GATEUP) return CBK_BSTREAM_K(MODE_GATEUP);
-    return CBK_BSTREAM_K(MODE_GEMV);
-#undef CBK_BSTREAM_K
+const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu) {
+    return bsu == 8 ? bstream_kernel<8>(mode, bits, mixed) : bstream_kernel<4>(mode, bits, mixed);
 }
+
 
 }  // namespace cbk
