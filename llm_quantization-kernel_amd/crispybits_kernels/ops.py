@@ -3,8 +3,9 @@ behaviour as the reference's Kernel/crispybits_kernels/ops.py:1-321, running on
 the gfx950 kernels of ``_C`` (libcrispybits_hip.so).
 
 Differences from the reference, all additive or retuned constants:
-  * DECODE_THRESHOLD is 8: the MFMA decode GEMV serves up to 16 batch rows at
-    the cost of one, so M = 1..8 stays on it (the reference uses 4, ops.py:23).
+  * DECODE_THRESHOLD is 16: the decode GEMV streams each weight once for up to 16
+    batch rows (16-row MFMA tiles), 3-4x faster than the prefill GEMM's 128-row
+    tiles at M = 9..16, so M = 1..16 stays on it (the reference uses 4, ops.py:23).
   * fused_qkv accepts per-projection widths (the reference raises ValueError,
     ops.py:240-241); the kernel dispatches the width per 16-row tile.
   * The split-K rule counts decode jobs as ceil(batch/16) batch tiles, matching
@@ -36,7 +37,7 @@ _C = _CUDA
 if os.environ.get("CRISPYBITS_BACKEND", "").lower() == "emulator":
     warnings.warn("CRISPYBITS_BACKEND=emulator: no CPU emulator ships with the MI355X build; using the HIP kernels")
 
-DECODE_THRESHOLD = 8
+DECODE_THRESHOLD = 16
 ACT = {"none": 0, None: 0, "relu": 1, "silu": 2}
 KINDS = ("gemv", "qkv", "gate_up")
 BATCH_TILE = 16          # batch rows one decode job covers

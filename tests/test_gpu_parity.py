@@ -149,7 +149,7 @@ def test_deterministic_repeat(hip):
 # ------------------------------------------------------------------ fused decode
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
-@pytest.mark.parametrize("B", [1, 4])
+@pytest.mark.parametrize("B", [1, 2, 4, 12])
 @pytest.mark.parametrize("split_k", [1, 3])
 def test_fused_gate_up(hip, bits, B, split_k):
     g, G64, _, _ = make(1376, 512, bits, torch.float16, seed=1)
@@ -160,9 +160,11 @@ def test_fused_gate_up(hip, bits, B, split_k):
 
 
 def test_fused_gate_up_prefill_fallback(hip):
+    """Past the decode threshold (16 rows; the reference test uses 9 with its 4) the
+    two projections take the prefill GEMM and are multiplied in fp16."""
     g, G64, _, _ = make(384, 256, 4, torch.float16, seed=1)
     u, U64, _, _ = make(384, 256, 4, torch.float16, seed=2)
-    x = randx(9, 256, torch.float16)
+    x = randx(ops.DECODE_THRESHOLD + 1, 256, torch.float16)
     gv, uv = ref_linear(x, G64), ref_linear(x, U64)
     close(fused_gate_up(x, g, u), gv / (1 + np.exp(-gv)) * uv, torch.float16)
 
@@ -181,7 +183,7 @@ def _rope64(y, cos, sin, hd):
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, (4, 2, 3)])
-@pytest.mark.parametrize("B", [1, 3, 6])
+@pytest.mark.parametrize("B", [1, 3, 6, 12, 20])
 @pytest.mark.parametrize("split_k", [1, 5])
 @pytest.mark.parametrize("rope,head_dim", [(False, 0), (False, 128), (True, 128), (True, 64)])
 @pytest.mark.parametrize("bias", [False, True])
