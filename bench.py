@@ -64,11 +64,11 @@ def gemv_bytes(M, K, N, bits, gs=GS):
 def make_weight(torch, N, K, bits, seed, device):
     """BASELINE inputs: W = randn(N, K, seed) * 0.02, group-affine quantized and packed."""
     from crispybits_kernels.ops import PackedLinearWeight
-    from crispybits_kernels.reference import pack_codes, quantize_affine
+    from crispybits_kernels.reference import quantize_pack
     g = torch.Generator().manual_seed(seed)
     W = (torch.randn(N, K, generator=g) * 0.02).to(device)
-    q, s, z = quantize_affine(W, bits, GS)
-    return PackedLinearWeight(pack_codes(q, bits), s.half(), z.half(), bits, GS, K, N)
+    packed, s, z = quantize_pack(W, bits, GS)
+    return PackedLinearWeight(packed, s, z, bits, GS, K, N)
 
 
 def clone_weight(w):
@@ -240,6 +240,7 @@ def main():
         out["fused"] = fused_sweep(torch, C, ops, dev)
         out["gemm"] = gemm_sweep(torch, C, ops, dev)
         out["llama2_7b_stack"] = stack_sweep(torch, C, ops, dev)
+        out["producer"] = producer_sweep(torch, C, dev)
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch, base, xs)
@@ -332,6 +333,29 @@ def fused_sweep(torch, C, ops, dev):
     return res
 
 
+def producer_sweep(torch, C, dev):
+    """The on-device quantizer + packer (cbk_quantize_pack) over the decode shapes' fp16
+    weights, W2/W3/W4, g=128: kernel us per weight and its HBM rate counting the weight
+    read once plus the packed words and fp16 scales/zeros written."""
+    rows = []
+    for K, N in SHAPES:
+        g = torch.Generator(device=dev).manual_seed(7)
+        W = (torch.randn(N, K, generator=g, device=dev) * 0.02).half()
+        for bits in (4, 3, 2):
+            run = lambda: [C.quantize_pack(W, bits, GS) for _ in range(8)]
+            run()
+            torch.cuda.synchronize()
+            total, _ = timed_kernels(C, run, 8)
+            us = total * 1e3 / 8
+            nbytes = N * K * 2 + N * math.ceil(K / 32) * bits * 4 + N * math.ceil(K / GS) * 4
+            gbs = nbytes / (us * 1e-6) / 1e9
+            rows.append({"bits": bits, "K": K, "N": N, "us": round(us, 2), "GBps": round(gbs, 1),
+                         "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1)})
+        del W
+    log(f"producer: {rows}")
+    return rows
+
+
 def gemm_sweep(torch, C, ops, dev):
     rows = []
     for M in (1024, 2048):
@@ -359,7 +383,7 @@ STACK_LINEARS = [("q", STACK_H, STACK_H), ("k", STACK_H, STACK_H), ("v", STACK_H
 def stack_sweep(torch, C, ops, dev, steps=20):
     """Config 5: the Llama-2-7B linear stack at decode (M = 1), 32 blocks, bits per block
     from default_rng(0).choice([2, 3, 4], 32); block i, linear j weights from a device
-    generator seeded 1000*i + j (quantized and packed on the GPU).  A step is, per block,
+    generator seeded 1000*i + j (quantized and packed on the GPU by the HIP producer).  A step is, per block,
     fused QKV, o, fused gate-up and down (ablation_decode.py:48-56); eager and as one
     captured HIP graph, against the same stack as dense fp16 F.linear (the dequantized
     weights) in a graph.  Inputs are fixed activations; the rest of the model (attention,
@@ -367,7 +391,8 @@ def stack_sweep(torch, C, ops, dev, steps=20):
     import numpy as np
     import torch.nn.functional as F
     from crispybits_kernels.ops import PackedLinearWeight
-    from crispybits_kernels.reference import dequantize, pack_codes, quantize_affine
+    from crispybits_kernels import _C
+    from crispybits_kernels.reference import dequantize, quantize_pack
     bitmap = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], STACK_BLOCKS)]
     blocks, dense = [], []
     for i, bits in enumerate(bitmap):
@@ -375,11 +400,10 @@ def stack_sweep(torch, C, ops, dev, steps=20):
         for j, (nm, N, K) in enumerate(STACK_LINEARS):
             g = torch.Generator(device=dev).manual_seed(1000 * i + j)
             W = torch.randn(N, K, generator=g, device=dev) * 0.02
-            q, s, z = quantize_affine(W, bits, GS)
-            s, z = s.half(), z.half()
-            pb[nm] = PackedLinearWeight(pack_codes(q, bits), s, z, bits, GS, K, N)
-            db[nm] = dequantize(q, s.float(), z.float(), GS).half()
-            del W, q
+            packed, s, z = quantize_pack(W, bits, GS)
+            pb[nm] = PackedLinearWeight(packed, s, z, bits, GS, K, N)
+            db[nm] = dequantize(_C.unpack_codes(packed, bits, K), s.float(), z.float(), GS).half()
+            del W
         blocks.append(pb)
         dense.append(db)
     torch.cuda.synchronize()

@@ -2,8 +2,8 @@
 
 Drop-in for the reference's pybind11 module (Kernel/csrc/bindings.cpp:32-40): the
 same seven functions with the same argument order, tensors in and tensors out,
-plus two additive entries (``unpack_codes``, ``fused_qkv`` with per-projection
-widths).  Tensor checks restate host_utils.h:38-87 and raise ``RuntimeError``
+plus additive entries (``unpack_codes``, ``fused_qkv`` with per-projection
+widths, ``quantize_pack``).  Tensor checks restate host_utils.h:38-87 and raise ``RuntimeError``
 like ``TORCH_CHECK``; the kernels run on torch's current HIP stream of x's device.
 
 The compute is libcrispybits_hip.so (include/crispybits_hip.h); importing this
@@ -47,6 +47,7 @@ _SIGS = {
                                  _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "cbk_packed_gemm": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P, _I, _P]),
     "cbk_unpack_codes": (_I, [_P, _L, _L, _I, _P, _I, _P]),
+    "cbk_quantize_pack": (_I, [_P, _I, _L, _L, _I, _I, _P, _P, _P, _I, _I, _P]),
     "cbk_timer_start": (_I, [_I]),
     "cbk_timer_stop": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
 }
@@ -240,6 +241,25 @@ def unpack_codes(packed, bits, in_features):
     _raise(_lib.cbk_unpack_codes(packed.data_ptr(), packed.size(0), K, bits, out.data_ptr(), packed.device.index,
                                  _stream(packed)))
     return out
+
+
+def quantize_pack(weight, bits, group_size=128, dtype=torch.float16):
+    """Additive: the format producer on the device -- (packed int32 [N, ceil(K/32)*bits],
+    scales, zeros [N, ceil(K/g)] in ``dtype``) of a CUDA weight [N, K], bit-identical to
+    reference.quantize_affine + pack_codes (reference.py:10-55) on the CPU."""
+    bits, gs = int(bits), int(group_size)
+    _check(weight.is_cuda and weight.dim() == 2, "weight must be a 2-D CUDA tensor")
+    _check(weight.dtype in _DT, "weight must be fp16/bf16/fp32")
+    _check(dtype in _DT, "scales/zeros dtype must be fp16/bf16/fp32")
+    w = weight.contiguous()
+    N, K = w.shape
+    G = math.ceil(K / gs) if gs > 0 else 0
+    packed = torch.empty((N, math.ceil(K / 32) * bits), dtype=torch.int32, device=w.device)
+    scales = torch.empty((N, G), dtype=dtype, device=w.device)
+    zeros = torch.empty((N, G), dtype=dtype, device=w.device)
+    _raise(_lib.cbk_quantize_pack(w.data_ptr(), _DT[w.dtype], N, K, bits, gs, packed.data_ptr(),
+                                  scales.data_ptr(), zeros.data_ptr(), _DT[dtype], w.device.index, _stream(w)))
+    return packed, scales, zeros
 
 
 def _device_index() -> int:

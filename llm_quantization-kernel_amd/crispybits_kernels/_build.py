@@ -23,7 +23,7 @@ LIB_NAME = "libcrispybits_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = os.environ.get("CRISPYBITS_ARCH", "gfx950")
 
-SOURCES = ["abi.cpp", "gemv_mfma.hip", "gemv_stream.hip", "gemv_generic.hip", "gemm.hip", "gemm_f16.hip", "unpack.hip"]
+SOURCES = ["abi.cpp", "gemv_mfma.hip", "gemv_stream.hip", "gemv_generic.hip", "gemm.hip", "gemm_f16.hip", "unpack.hip", "quant.hip"]
 
 # -packed-fp32-ops is disabled: the kernels never rely on v_pk_*_f32.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-munsafe-fp-atomics",

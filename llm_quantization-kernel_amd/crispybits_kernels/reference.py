@@ -9,7 +9,8 @@ it is never called by the op path (ops.py), which runs only the HIP kernels.
 The quantizer formula is the format definition and follows reference.py:10-27
 step for step (fp32, round-half-even, clamp); the bit packing is vectorised over
 bit planes: a chunk's 32 codes are expanded to their 32*bits LSB-first bits, which
-regrouped 32 at a time are exactly the chunk's ``bits`` words.
+regrouped 32 at a time are exactly the chunk's ``bits`` words.  For a CUDA weight,
+``quantize_pack`` / ``pack_linear_dict`` run the HIP producer instead (quant.hip).
 """
 from __future__ import annotations
 
@@ -83,11 +84,23 @@ def unpack_codes(packed: torch.Tensor, bits: int, K: int) -> torch.Tensor:
     return out
 
 
+def quantize_pack(weight: torch.Tensor, bits: int, group_size: int = 128, dtype=torch.float16):
+    """(packed, scales, zeros) of one weight on its own device.  A CUDA weight is
+    quantized and packed by the HIP producer (``_C.quantize_pack``), bit-identical to
+    this module's CPU path -- torch's own GPU division by a scalar is a multiply by the
+    reciprocal, which moves some scales by an ulp and with them some codes."""
+    if weight.is_cuda:
+        from . import _C
+        return _C.quantize_pack(weight.detach(), bits, group_size, dtype)
+    q, s, z = quantize_affine(weight, bits, group_size)
+    return pack_codes(q, bits), s.to(dtype), z.to(dtype)
+
+
 def pack_linear_dict(weight: torch.Tensor, bits: int, group_size: int = 128,
                      bias: Optional[torch.Tensor] = None, dtype=torch.float16) -> Dict:
     """One linear -> the on-disk dict (packed/scales/zeros/bits/group_size/in/out/bias)."""
-    q, s, z = quantize_affine(weight, bits, group_size)
-    return dict(packed=pack_codes(q, bits).cpu(), scales=s.to(dtype).cpu(), zeros=z.to(dtype).cpu(),
+    packed, s, z = quantize_pack(weight, bits, group_size, dtype)
+    return dict(packed=packed.cpu(), scales=s.cpu(), zeros=z.cpu(),
                 bits=bits, group_size=group_size, in_features=weight.shape[1], out_features=weight.shape[0],
                 bias=None if bias is None else bias.detach().to(dtype).cpu())
 

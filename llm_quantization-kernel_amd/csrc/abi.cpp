@@ -751,6 +751,35 @@ int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K, const int32_
     return CBK_OK;
 }
 
+int cbk_quantize_pack(const void* w, int dtype, int64_t N, int64_t K, int bits, int group_size,
+                      int32_t* packed, void* scales, void* zeros, int meta_dtype, int device, void* stream) {
+    if (!valid_dtype(dtype)) return fail(CBK_EINVAL, "quantize_pack: weights must be fp16/bf16/fp32");
+    if (!valid_dtype(meta_dtype)) return fail(CBK_EINVAL, "quantize_pack: scales/zeros must be fp16/bf16/fp32");
+    if (bits != 2 && bits != 3 && bits != 4) return fail(CBK_EINVAL, "quantize_pack: bits must be 2/3/4");
+    if (group_size <= 0 || group_size % 32 != 0)
+        return fail(CBK_EINVAL, "quantize_pack: group_size must be a positive multiple of 32");
+    if (N < 0 || K <= 0 || N > (1 << 30) || K > (1 << 24)) return fail(CBK_EINVAL, "quantize_pack: bad shape");
+    if (N == 0) return CBK_OK;
+    if (!w || !packed || !scales || !zeros) return fail(CBK_EINVAL, "quantize_pack: pointers must be non-null");
+    if ((int64_t)N * ceil_div(K, group_size) >= (1ll << 31)) return fail(CBK_EINVAL, "quantize_pack: too many groups");
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    QuantArgs A;
+    A.w = w;
+    A.packed = reinterpret_cast<uint32_t*>(packed);
+    A.scales = scales;
+    A.zeros = zeros;
+    A.N = (int)N;
+    A.K = (int)K;
+    A.G = (int)ceil_div(K, group_size);
+    A.gs = group_size;
+    A.bits = bits;
+    A.wpr = (int)(ceil_div(K, 32) * bits);
+    const hipError_t e = launch_quant_pack(A, dtype, meta_dtype, reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "quantize_pack: launch");
+    return CBK_OK;
+}
+
 int cbk_unpack_codes(const int32_t* packed, int64_t N, int64_t K, int bits, int32_t* codes, int device,
                      void* stream) {
     if (!packed || !codes) return fail(CBK_EINVAL, "unpack_codes: pointers must be non-null");

@@ -58,6 +58,16 @@ hipError_t launch_gemm_valu(const GemmArgs& A, int dt, hipStream_t stream);
 bool gemm_f16_supported(const GemmArgs& A);
 hipError_t launch_gemm_f16(const GemmArgs& A, hipStream_t stream);
 
+// quant.hip: group-affine quantizer + bit packer (the format's producer).
+struct QuantArgs {
+    const void* w;          // [N, K] weights (fp16 / bf16 / fp32)
+    uint32_t* packed;       // [N, wpr]
+    void* scales;           // [N, G] in the metadata dtype
+    void* zeros;            // [N, G]
+    int N, K, G, gs, bits, wpr;
+};
+hipError_t launch_quant_pack(const QuantArgs& A, int dt, int mdt, hipStream_t stream);
+
 // unpack.hip
 hipError_t launch_unpack(const uint32_t* packed, int N, int K, int bits, int32_t* codes, hipStream_t stream);
 

@@ -19,7 +19,7 @@ def _declared():
 def test_header_declares_expected_entry_points():
     names = _declared()
     for n in ("cbk_packed_gemv", "cbk_packed_gemm", "cbk_fused_gate_up", "cbk_fused_qkv", "cbk_sm_count",
-              "cbk_tile_n", "cbk_max_rho", "cbk_unpack_codes"):
+              "cbk_tile_n", "cbk_max_rho", "cbk_unpack_codes", "cbk_quantize_pack"):
         assert n in names
 
 
@@ -81,6 +81,26 @@ def test_gemm_and_unpack_argument_errors():
     assert "group_size" in _err()
     assert lib.cbk_unpack_codes(ALIGNED, 4, 64, 1, ALIGNED, 0, None) == 1
     assert "bits" in _err()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(dtype=5), "weights must be fp16/bf16/fp32"),
+    (dict(mdt=9), "scales/zeros must be fp16/bf16/fp32"),
+    (dict(bits=1), "bits must be 2/3/4"),
+    (dict(gs=100), "positive multiple of 32"),
+    (dict(K=0), "bad shape"),
+    (dict(zeros=None), "non-null"),
+])
+def test_quantize_pack_argument_errors(kw, msg):
+    a = dict(w=ALIGNED, dtype=0, N=8, K=256, bits=3, gs=128, packed=ALIGNED, scales=ALIGNED, zeros=ALIGNED, mdt=0,
+             device=0, stream=None)
+    a.update(kw)
+    assert _lib().cbk_quantize_pack(*a.values()) == 1
+    assert msg in _err()
+
+
+def test_quantize_pack_empty_weight_is_a_no_op():
+    assert _lib().cbk_quantize_pack(None, 0, 0, 256, 4, 128, None, None, None, 0, 0, None) == 0
 
 
 def test_fused_qkv_rope_checks():
