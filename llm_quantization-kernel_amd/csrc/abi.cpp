@@ -775,7 +775,7 @@ int cbk_quantize_pack(const void* w, int dtype, int64_t N, int64_t K, int bits, 
     A.gs = group_size;
     A.bits = bits;
     A.wpr = (int)(ceil_div(K, 32) * bits);
-    const hipError_t e = launch_quant_pack(A, dtype, meta_dtype, reinterpret_cast<hipStream_t>(stream));
+    const hipError_t e = launch_quant_pack(A, dtype, meta_dtype, cu_count(device), reinterpret_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "quantize_pack: launch");
     return CBK_OK;
 }

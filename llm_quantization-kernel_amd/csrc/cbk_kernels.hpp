@@ -66,7 +66,7 @@ struct QuantArgs {
     void* zeros;            // [N, G]
     int N, K, G, gs, bits, wpr;
 };
-hipError_t launch_quant_pack(const QuantArgs& A, int dt, int mdt, hipStream_t stream);
+hipError_t launch_quant_pack(const QuantArgs& A, int dt, int mdt, int cus, hipStream_t stream);
 
 // unpack.hip
 hipError_t launch_unpack(const uint32_t* packed, int N, int K, int bits, int32_t* codes, hipStream_t stream);

@@ -17,7 +17,9 @@ from oracle import reference as R
 
 pytestmark = pytest.mark.gpu
 
-CASES = [(7, 32, 32), (5, 200, 64), (33, 4128, 128), (300, 640, 128), (3, 96, 256), (2, 250, 256), (64, 11008, 128)]
+# vector path: group size 32..512 dividing 512, K % 8 == 0; the rest take the general path
+CASES = [(7, 32, 32), (5, 200, 64), (33, 4128, 128), (300, 640, 128), (3, 96, 256), (2, 250, 256), (64, 11008, 128),
+         (9, 1000, 512), (4, 2080, 1024), (6, 544, 96), (1, 8, 32)]
 
 
 def _oracle(w32, bits, gs, mdt):
@@ -67,6 +69,17 @@ def test_rounding_ties_and_constant_groups(hip, bits):
     w[4, 128:] = -2.5
     _check(torch.from_numpy(w), bits, 32, torch.float32)
     _check(torch.from_numpy(w), bits, 128, torch.float16)
+
+
+def test_unaligned_weight_takes_the_general_path(hip):
+    g = torch.Generator().manual_seed(3)
+    buf = (torch.randn(24 * 256 + 1, generator=g) * 0.02).half().cuda()
+    w = buf[1:].view(24, 256)                       # contiguous, 2 bytes past a 16-byte boundary
+    packed, s, z = _C.quantize_pack(w, 3, 128)
+    torch.cuda.synchronize()
+    po, so, zo = _oracle(w.float().cpu().numpy(), 3, 128, torch.float16)
+    assert np.array_equal(packed.cpu().numpy(), po)
+    assert np.array_equal(s.float().cpu().numpy(), so) and np.array_equal(z.float().cpu().numpy(), zo)
 
 
 def test_full_size_weight_matches_cpu_producer(hip):
