@@ -115,10 +115,12 @@ int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K,
 
 /* Format producer on the device: group-affine quantization of w[N,K] (fp16 / bf16 /
  * fp32) to `bits`-bit codes, packed as the kernels read them, with fp16 / bf16 / fp32
- * scales and zeros [N, ceil(K/group_size)].  Bit-identical to the reference's
- * quantize_affine + pack_codes (reference.py:10-27, 37-55; pack_linear_dict :70-82),
- * which run on the host CPU in the reference; no counterpart in its _C. */
-int cbk_quantize_pack(const void* w, int dtype, int64_t N, int64_t K, int bits, int group_size,
+ * scales and zeros [N, ceil(K/group_size)].  scheme 0 is bit-identical to the reference's
+ * quantize_affine + pack_codes (Kernel/crispybits_kernels/reference.py:10-27, 37-55;
+ * pack_linear_dict :70-82), scheme 1 to the paper quantizer
+ * quantization/crispybits_quant/affine.py:28-71 (codes in the same chunked layout).  Both
+ * run on the host CPU in the reference; no counterpart in its _C. */
+int cbk_quantize_pack(const void* w, int dtype, int64_t N, int64_t K, int bits, int group_size, int scheme,
                       int32_t* packed, void* scales, void* zeros, int meta_dtype, int device, void* stream);
 
 /* Additive test hook: codes[N,K] (int32) of a packed matrix, for the bit-exact

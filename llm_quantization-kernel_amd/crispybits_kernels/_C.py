@@ -47,7 +47,7 @@ _SIGS = {
                                  _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "cbk_packed_gemm": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P, _I, _P]),
     "cbk_unpack_codes": (_I, [_P, _L, _L, _I, _P, _I, _P]),
-    "cbk_quantize_pack": (_I, [_P, _I, _L, _L, _I, _I, _P, _P, _P, _I, _I, _P]),
+    "cbk_quantize_pack": (_I, [_P, _I, _L, _L, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
     "cbk_timer_start": (_I, [_I]),
     "cbk_timer_stop": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
 }
@@ -243,11 +243,12 @@ def unpack_codes(packed, bits, in_features):
     return out
 
 
-def quantize_pack(weight, bits, group_size=128, dtype=torch.float16):
+def quantize_pack(weight, bits, group_size=128, dtype=torch.float16, scheme=0):
     """Additive: the format producer on the device -- (packed int32 [N, ceil(K/32)*bits],
     scales, zeros [N, ceil(K/g)] in ``dtype``) of a CUDA weight [N, K], bit-identical to
-    reference.quantize_affine + pack_codes (reference.py:10-55) on the CPU."""
-    bits, gs = int(bits), int(group_size)
+    reference.quantize_affine + pack_codes (reference.py:10-55) on the CPU (scheme 0), or
+    to the paper quantizer crispybits_quant/affine.py:28-71 (scheme 1)."""
+    bits, gs, scheme = int(bits), int(group_size), int(scheme)
     _check(weight.is_cuda and weight.dim() == 2, "weight must be a 2-D CUDA tensor")
     _check(weight.dtype in _DT, "weight must be fp16/bf16/fp32")
     _check(dtype in _DT, "scales/zeros dtype must be fp16/bf16/fp32")
@@ -257,7 +258,7 @@ def quantize_pack(weight, bits, group_size=128, dtype=torch.float16):
     packed = torch.empty((N, math.ceil(K / 32) * bits), dtype=torch.int32, device=w.device)
     scales = torch.empty((N, G), dtype=dtype, device=w.device)
     zeros = torch.empty((N, G), dtype=dtype, device=w.device)
-    _raise(_lib.cbk_quantize_pack(w.data_ptr(), _DT[w.dtype], N, K, bits, gs, packed.data_ptr(),
+    _raise(_lib.cbk_quantize_pack(w.data_ptr(), _DT[w.dtype], N, K, bits, gs, scheme, packed.data_ptr(),
                                   scales.data_ptr(), zeros.data_ptr(), _DT[dtype], w.device.index, _stream(w)))
     return packed, scales, zeros
 

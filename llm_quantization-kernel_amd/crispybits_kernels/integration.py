@@ -209,16 +209,38 @@ def _fuse_block(block: nn.Module, tuning: Dict, i: int, fuse_rope: bool):
         block.activation_fn = nn.Identity()
 
 
+def _block_file(packed_dir: Path, i: int, bits: int) -> Path:
+    """block_{i:03d}_w{bits}.pt (write_packed_dir, reference.py:85-94), else the single-width
+    block_{i:03d}.pt of the paper's pack_checkpoint.py:26."""
+    per_width = packed_dir / f"block_{i:03d}_w{bits}.pt"
+    if per_width.exists():
+        return per_width
+    single = packed_dir / f"block_{i:03d}.pt"
+    if single.exists():
+        return single
+    raise FileNotFoundError(f"neither {per_width.name} nor {single.name} in {packed_dir}")
+
+
 def install_bitmap(model: nn.Module, packed_dir: str, bitmap, device="cuda", dtype=torch.float16,
                    tuning: Optional[Dict] = None, fuse: bool = True, fuse_rope: bool = True):
-    """Replace every linear of block i with the packed weights of width bitmap[i]."""
+    """Replace every linear of block i with the packed weights of width bitmap[i].
+
+    Reads write_packed_dir's block_{i:03d}_w{bits}.pt, or pack_checkpoint.py's block_{i:03d}.pt
+    (one width per block, continuous bitstream; its manifest.json supplies the bitmap when
+    ``bitmap`` is None)."""
+    packed_dir = Path(packed_dir)
+    if bitmap is None:
+        with open(packed_dir / "manifest.json") as f:
+            bitmap = json.load(f)["bitmap"]
     blocks = _blocks(model)
     if len(blocks) != len(bitmap):
         raise ValueError("bitmap length does not match model")
     tuning = tuning or {}
     for i, (block, bits) in enumerate(zip(blocks, bitmap)):
-        data = torch.load(Path(packed_dir) / f"block_{i:03d}_w{int(bits)}.pt", map_location="cpu", weights_only=True)
+        data = torch.load(_block_file(packed_dir, i, int(bits)), map_location="cpu", weights_only=True)
         for name, d in data.items():
+            if int(d["bits"]) != int(bits):
+                raise ValueError(f"block {i}: '{name}' is packed at W{int(d['bits'])}, the bitmap asks for W{int(bits)}")
             if not isinstance(_get(block, name), nn.Linear):
                 raise ValueError(f"block {i}: '{name}' is not an nn.Linear in this model")
             w = from_packed_dict(d, device=device, dtype=dtype)

@@ -751,13 +751,14 @@ int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K, const int32_
     return CBK_OK;
 }
 
-int cbk_quantize_pack(const void* w, int dtype, int64_t N, int64_t K, int bits, int group_size,
+int cbk_quantize_pack(const void* w, int dtype, int64_t N, int64_t K, int bits, int group_size, int scheme,
                       int32_t* packed, void* scales, void* zeros, int meta_dtype, int device, void* stream) {
     if (!valid_dtype(dtype)) return fail(CBK_EINVAL, "quantize_pack: weights must be fp16/bf16/fp32");
     if (!valid_dtype(meta_dtype)) return fail(CBK_EINVAL, "quantize_pack: scales/zeros must be fp16/bf16/fp32");
     if (bits != 2 && bits != 3 && bits != 4) return fail(CBK_EINVAL, "quantize_pack: bits must be 2/3/4");
     if (group_size <= 0 || group_size % 32 != 0)
         return fail(CBK_EINVAL, "quantize_pack: group_size must be a positive multiple of 32");
+    if (scheme != 0 && scheme != 1) return fail(CBK_EINVAL, "quantize_pack: scheme must be 0 (kernel) or 1 (affine)");
     if (N < 0 || K <= 0 || N > (1 << 30) || K > (1 << 24)) return fail(CBK_EINVAL, "quantize_pack: bad shape");
     if (N == 0) return CBK_OK;
     if (!w || !packed || !scales || !zeros) return fail(CBK_EINVAL, "quantize_pack: pointers must be non-null");
@@ -775,6 +776,7 @@ int cbk_quantize_pack(const void* w, int dtype, int64_t N, int64_t K, int bits, 
     A.gs = group_size;
     A.bits = bits;
     A.wpr = (int)(ceil_div(K, 32) * bits);
+    A.scheme = scheme;
     const hipError_t e = launch_quant_pack(A, dtype, meta_dtype, cu_count(device), reinterpret_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "quantize_pack: launch");
     return CBK_OK;

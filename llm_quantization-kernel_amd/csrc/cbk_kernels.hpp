@@ -65,6 +65,7 @@ struct QuantArgs {
     void* scales;           // [N, G] in the metadata dtype
     void* zeros;            // [N, G]
     int N, K, G, gs, bits, wpr;
+    int scheme;             // 0: reference.py quantize_affine, 1: crispybits_quant affine
 };
 hipError_t launch_quant_pack(const QuantArgs& A, int dt, int mdt, int cus, hipStream_t stream);
 

@@ -8,6 +8,10 @@
 // as an LSB-first bitstream of ceil(K/32) chunks of `bits` words, codes past K zero.
 // The reference pads K to whole groups by repeating the last column; a repeated value
 // is already in its group, so the min/max over the group's real columns are the same.
+// Scheme 1 is the paper quantizer of quantization/crispybits_quant/affine.py:28-71 instead:
+// min clamped to <= 0 and max to >= 0, scale 1 where (max - min) / qmax < 1e-8, and
+// q = clamp(round(w / scale + zero), 0, qmax) (the zero added before rounding); the
+// output layout is the same chunked bitstream.
 //
 // Vector path (group size 32..512 dividing 512, K % 8 == 0, 16-byte aligned weights): the
 // weights are cut into pieces of 512 consecutive elements of a row, one 16-byte octet per
@@ -134,7 +138,8 @@ __device__ __forceinline__ uint32_t chunk_word(const uint32_t (&f)[4]) {
 // codes, and the chunk words.  rint(v / scale) must be that of the IEEE quotient X:
 // y = fma(v, inv, zero), inv = 1/scale after a Newton step, satisfies
 // |y - (X + zero)| <= (|X| + zero) 2^-22 < tol = (max|v| inv + qmax + 1) 2^-21, so a y
-// farther than tol from every half-integer rounds to rint(X) + zero; a lane holding a
+// farther than tol from every half-integer rounds to rint(X) + zero, and (scheme 1) to
+// rint(fl(X + zero)), which lies within |X + zero| 2^-24 of X + zero; a lane holding a
 // code within tol of a half-integer redoes its 8 with the IEEE division.
 template <int DT, int L, int BITS>
 __device__ __forceinline__ void quant_piece(const QuantArgs& A, int mdt, const RawOctet<DT>& raw, int row, int k,
@@ -152,7 +157,13 @@ __device__ __forceinline__ void quant_piece(const QuantArgs& A, int mdt, const R
         }
     }
     group_minmax<L>(lo, hi);
-    const float scale = fmaxf((hi - lo) / qmax, 1e-8f);
+    const bool paper = A.scheme == 1;
+    if (paper) {
+        lo = fminf(lo, 0.f);
+        hi = fmaxf(hi, 0.f);
+    }
+    float scale = (hi - lo) / qmax;
+    scale = paper ? (scale < 1e-8f ? 1.f : scale) : fmaxf(scale, 1e-8f);
     const float zero = __builtin_amdgcn_fmed3f(rintf(-lo / scale), 0.f, qmax);
     if (ok && (lane & (L - 1)) == 0)
         store_meta2(mdt, A.scales, A.zeros, (long)row * A.G + k / (8 * L), scale, zero);
@@ -167,8 +178,13 @@ __device__ __forceinline__ void quant_piece(const QuantArgs& A, int mdt, const R
         dmax = fmaxf(dmax, fabsf(y - r[e]));
     }
     if (!(dmax < lim)) {
+        if (paper) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r[e] = rintf(v[e] / scale) + zero;
+            for (int e = 0; e < 8; ++e) r[e] = rintf(v[e] / scale + zero);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) r[e] = rintf(v[e] / scale) + zero;
+        }
     }
     uint32_t field = 0;                                        // code e at bit e*BITS (8*BITS <= 32)
 #pragma unroll
@@ -251,7 +267,13 @@ __global__ void __launch_bounds__(64 * WAVES) quant_pack_kernel(const QuantArgs 
         hi = fmaxf(hi, __shfl_xor(hi, off, 64));
     }
     const float qmax = (float)((1 << A.bits) - 1);
-    const float scale = fmaxf((hi - lo) / qmax, 1e-8f);
+    const bool paper = A.scheme == 1;
+    if (paper) {
+        lo = fminf(lo, 0.f);
+        hi = fmaxf(hi, 0.f);
+    }
+    float scale = (hi - lo) / qmax;
+    scale = paper ? (scale < 1e-8f ? 1.f : scale) : fmaxf(scale, 1e-8f);
     const float zero = fminf(fmaxf(rintf(-lo / scale), 0.f), qmax);
     if (lane == 0) {
         store_f<MDT>(A.scales, (long)n * A.G + g, scale);
@@ -267,7 +289,8 @@ __global__ void __launch_bounds__(64 * WAVES) quant_pack_kernel(const QuantArgs 
         uint32_t q = 0;
         if (cc < ce && k < k1) {
             const float v = load_f<DT>(A.w, row + k);
-            q = (uint32_t)fminf(fmaxf(rintf(v / scale) + zero, 0.f), qmax);
+            const float r = paper ? rintf(v / scale + zero) : rintf(v / scale) + zero;
+            q = (uint32_t)fminf(fmaxf(r, 0.f), qmax);
         }
         if (j < 4) words[wv][h][j] = 0u;
         __builtin_amdgcn_wave_barrier();

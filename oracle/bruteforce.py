@@ -56,3 +56,38 @@ def quantize_row(row, bits: int, group_size: int):
         ss.append(float(scale))
         zs.append(float(zero))
     return qs[:K], ss, zs
+
+
+def pack_row_continuous(codes, bits: int) -> list:
+    """One row -> ceil(K*bits/32) uint32 words of the unpadded LSB-first bitstream
+    (quantization/crispybits_quant/packing.py:24-25,45-54)."""
+    stream = 0
+    for k, c in enumerate(codes):
+        stream |= (int(c) & ((1 << bits) - 1)) << (k * bits)
+    nwords = (len(codes) * bits + 31) // 32
+    return [(stream >> (32 * i)) & 0xFFFFFFFF for i in range(nwords)]
+
+
+def affine_quantize_row(row, bits: int, group_size: int, eps: float = 1e-8):
+    """Scalar fp32 zero-inclusive quantization of one row (crispybits_quant/affine.py:28-71):
+    per group of real columns, min <= 0 <= max, scale = (max - min) / qmax (1 if below eps),
+    zero = clamp(rne(-min / scale), 0, qmax), q = clamp(rne(w / scale + zero), 0, qmax)."""
+    f32 = np.float32
+    K = len(row)
+    qmax = f32((1 << bits) - 1)
+    qs, ss, zs = [], [], []
+    for s in range(0, K, group_size):
+        grp = [f32(v) for v in row[s:s + group_size]]
+        mn = min(min(grp), f32(0))
+        mx = max(max(grp), f32(0))
+        scale = f32(mx - mn) / qmax
+        if scale < f32(eps):
+            scale = f32(1)
+        zero = min(max(f32(np.rint(f32(-mn) / scale)), f32(0)), qmax)
+        for v in grp:
+            y = f32(f32(v / scale) + zero)
+            qs.append(int(min(max(f32(np.rint(y)), f32(0)), qmax)))
+        ss.append(float(scale))
+        zs.append(float(zero))
+    return qs, ss, zs
+

@@ -10,7 +10,9 @@ import math
 import numpy as np
 
 __all__ = ["quantize_affine", "dequantize", "pack_codes", "unpack_codes", "pack_linear_dict",
-           "dequantized_weight", "chunk_code", "code_to_float", "words_per_row"]
+           "dequantized_weight", "chunk_code", "code_to_float", "words_per_row",
+           "affine_quantize_weight", "pack_codes_continuous", "unpack_codes_continuous",
+           "continuous_to_chunked"]
 
 
 def words_per_row(K: int, bits: int) -> int:
@@ -122,3 +124,71 @@ def dequantized_weight(d: dict) -> np.ndarray:
     q = unpack_codes(d["packed"], d["bits"], d["in_features"])
     return dequantize(q, np.asarray(d["scales"], np.float32), np.asarray(d["zeros"], np.float32),
                       d["group_size"])
+
+
+# ---------------------------------------------------------------- the second producer
+# quantization/crispybits_quant (the paper's offline quantizer, used by
+# quantization/scripts/pack_checkpoint.py): a zero-inclusive affine quantizer and a
+# continuous bitstream packer.  The kernels consume the chunked format above; these two
+# restatements let the product's converter and device producer be checked against them.
+
+def affine_quantize_weight(w: np.ndarray, bits: int, group_size: int = 128, eps: float = 1e-8):
+    """Zero-inclusive affine quantization (crispybits_quant/affine.py:28-71).
+
+    Per row and group [s, e) of the real columns (no padding): min clamped to <= 0 and
+    max to >= 0 (affine.py:51-52), scale = (max - min) / qmax replaced by 1 where it is
+    below eps (affine.py:53-55), zero = clamp(round(-min / scale), 0, qmax), and
+    q = clamp(round(w / scale + zero), 0, qmax) -- the zero is added before rounding
+    (affine.py:57-58).  All fp32.  Returns (q int32 [N, K], scale fp32 [N, G], zero fp32 [N, G]).
+    """
+    assert bits in (2, 3, 4)
+    w = np.asarray(w, dtype=np.float32)
+    N, K = w.shape
+    G = math.ceil(K / group_size)
+    qmax = np.float32((1 << bits) - 1)
+    q = np.empty((N, K), dtype=np.int32)
+    scale = np.empty((N, G), dtype=np.float32)
+    zero = np.empty((N, G), dtype=np.float32)
+    for g in range(G):
+        s, e = g * group_size, min(K, (g + 1) * group_size)
+        wg = w[:, s:e]
+        mn = np.minimum(wg.min(1), np.float32(0))
+        mx = np.maximum(wg.max(1), np.float32(0))
+        sc = ((mx - mn) / qmax).astype(np.float32)
+        sc = np.where(sc < np.float32(eps), np.float32(1), sc).astype(np.float32)
+        zr = np.clip(np.rint(-mn / sc), 0, qmax).astype(np.float32)
+        y = (wg / sc[:, None]).astype(np.float32) + zr[:, None]
+        q[:, s:e] = np.clip(np.rint(y), 0, qmax).astype(np.int32)
+        scale[:, g], zero[:, g] = sc, zr
+    return q, scale, zero
+
+
+def pack_codes_continuous(q: np.ndarray, bits: int) -> np.ndarray:
+    """One LSB-first bitstream per row with no chunk padding: ceil(K * bits / 32) words
+    (crispybits_quant/packing.py:24-25,45-54).  Equal to pack_codes when K % 32 == 0."""
+    assert bits in (2, 3, 4)
+    q = np.asarray(q)
+    N, K = q.shape
+    W = (K * bits + 31) // 32
+    words = np.zeros((N, W + 1), dtype=np.uint64)
+    for k in range(K):
+        pos = k * bits
+        wi, off = pos // 32, pos % 32
+        v = (q[:, k].astype(np.uint64) & np.uint64((1 << bits) - 1)) << np.uint64(off)
+        words[:, wi] |= v & np.uint64(0xFFFFFFFF)
+        words[:, wi + 1] |= v >> np.uint64(32)
+    assert not words[:, W].any()
+    return words[:, :W].astype(np.uint32).view(np.int32).copy()
+
+
+def unpack_codes_continuous(packed: np.ndarray, K: int, bits: int) -> np.ndarray:
+    """Inverse of pack_codes_continuous (packing.py:62-80): int32 [N, K].  The bit
+    arithmetic is the same random access as unpack_codes -- in both formats code k sits
+    at bit k*bits of the row -- only the row length in words differs."""
+    return unpack_codes(packed, bits, K)
+
+
+def continuous_to_chunked(packed: np.ndarray, bits: int, K: int) -> np.ndarray:
+    """Re-pack a continuous-bitstream row set into the kernels' chunked format."""
+    return pack_codes(unpack_codes_continuous(packed, K, bits), bits)
+

@@ -90,17 +90,18 @@ def test_gemm_and_unpack_argument_errors():
     (dict(gs=100), "positive multiple of 32"),
     (dict(K=0), "bad shape"),
     (dict(zeros=None), "non-null"),
+    (dict(scheme=2), "scheme must be 0"),
 ])
 def test_quantize_pack_argument_errors(kw, msg):
-    a = dict(w=ALIGNED, dtype=0, N=8, K=256, bits=3, gs=128, packed=ALIGNED, scales=ALIGNED, zeros=ALIGNED, mdt=0,
-             device=0, stream=None)
+    a = dict(w=ALIGNED, dtype=0, N=8, K=256, bits=3, gs=128, scheme=0, packed=ALIGNED, scales=ALIGNED, zeros=ALIGNED,
+             mdt=0, device=0, stream=None)
     a.update(kw)
     assert _lib().cbk_quantize_pack(*a.values()) == 1
     assert msg in _err()
 
 
 def test_quantize_pack_empty_weight_is_a_no_op():
-    assert _lib().cbk_quantize_pack(None, 0, 0, 256, 4, 128, None, None, None, 0, 0, None) == 0
+    assert _lib().cbk_quantize_pack(None, 0, 0, 256, 4, 128, 0, None, None, None, 0, 0, None) == 0
 
 
 def test_fused_qkv_rope_checks():

@@ -101,3 +101,45 @@ def test_empty_weight_is_a_no_op(hip):
     packed, s, z = _C.quantize_pack(torch.empty(0, 256, device="cuda"), 4, 128)
     torch.cuda.synchronize()
     assert packed.shape == (0, 32) and s.shape == (0, 2)
+
+
+# ---------------------------------------------------------------- scheme 1: the paper quantizer
+
+def _check_affine(w, bits, gs, mdt):
+    packed, s, z = _C.quantize_pack(w.cuda(), bits, gs, mdt, scheme=1)
+    torch.cuda.synchronize()
+    q, so, zo = R.affine_quantize_weight(w.float().numpy(), bits, gs)
+    assert np.array_equal(packed.cpu().numpy(), R.pack_codes(q, bits))
+    assert np.array_equal(s.float().cpu().numpy(), torch.from_numpy(so).to(mdt).float().numpy())
+    assert np.array_equal(z.float().cpu().numpy(), torch.from_numpy(zo).to(mdt).float().numpy())
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("N,K,gs", [(7, 32, 32), (5, 257, 128), (33, 4128, 128), (300, 640, 64), (6, 544, 96),
+                                    (64, 11008, 128)])
+def test_affine_scheme_bit_exact(hip, bits, N, K, gs):
+    g = torch.Generator().manual_seed(bits * 17 + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    w[0] = 0.37                                   # positive row: min clamps to 0
+    w[1] = 0.0                                    # zero row: scale 1
+    w[2, : min(K, 100)] = -2.0
+    _check_affine(w, bits, gs, torch.float16)
+
+
+@pytest.mark.parametrize("wdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_affine_scheme_dtypes_and_ties(hip, wdt):
+    g = torch.Generator().manual_seed(9)
+    _check_affine((torch.randn(40, 300, generator=g) * 0.05).to(wdt), 3, 128, wdt)
+    tie = torch.zeros(4, 64)
+    tie[:, :4] = torch.tensor([-1.0, 0.5, 2.0, 1.5])     # scale 1, zero 1: round(0.5 + 1) = 2
+    _check_affine(tie, 2, 32, torch.float32)
+
+
+def test_pack_block_on_the_device_matches_cpu(hip):
+    from crispybits_kernels.reference import pack_block
+    blk = torch.nn.Sequential(torch.nn.Linear(200, 48), torch.nn.Linear(256, 16)).half()
+    cpu = pack_block(blk, 3, 64)
+    dev = pack_block(blk.cuda(), 3, 64)
+    for name in cpu:
+        for key in ("packed", "scales", "zeros", "bias"):
+            assert torch.equal(cpu[name][key], dev[name][key]), (name, key)

@@ -232,3 +232,31 @@ def test_proxy_mismatch_raises(emu):
     owner.prime(x, torch.ones(1, 64), torch.zeros(1, 64))
     with pytest.raises(RuntimeError):
         _QKVProxy(owner, 0)(x.clone())
+
+
+def test_paper_checkpoint_dir_installs(emu, tmp_path):
+    """pack_checkpoint.py's layout (block_{i:03d}.pt + manifest.json, continuous bitstream,
+    the paper quantizer) installs through install_bitmap with the manifest's bitmap, and the
+    model matches the same weights dequantized on the CPU."""
+    from crispybits_kernels.reference import write_checkpoint_dir
+    from oracle import reference as R
+    torch.manual_seed(0)
+    dtype = torch.float32
+    base = _tiny("llama").to(dtype).eval()
+    bitmap = [3, 2, 4]
+    write_checkpoint_dir(base, tmp_path, bitmap, group_size=128, model_name="tiny-llama")
+    assert sorted(p.name for p in tmp_path.iterdir()) == ["block_000.pt", "block_001.pt", "block_002.pt",
+                                                          "manifest.json"]
+    ref = copy.deepcopy(base)
+    for block, bits in zip(_blocks(ref), bitmap):
+        for _, m in block.named_modules():
+            if isinstance(m, torch.nn.Linear):
+                q, s, z = R.affine_quantize_weight(m.weight.detach().float().numpy(), bits, 128)
+                m.weight.data.copy_(torch.from_numpy(R.dequantize(q, s, z, 128)).to(m.weight))
+    model = install_bitmap(copy.deepcopy(base), tmp_path, None, device="cpu", dtype=dtype, fuse=True)
+    ids = torch.randint(0, 512, (1, 12))
+    with torch.no_grad():
+        la, lb = ref(ids).logits[:, -1], model(ids).logits[:, -1]
+    assert (la - lb).abs().max() / la.abs().max() < 2e-2
+    with pytest.raises(ValueError):
+        install_bitmap(copy.deepcopy(base), tmp_path, [4, 2, 4], device="cpu", dtype=dtype)

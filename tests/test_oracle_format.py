@@ -240,3 +240,91 @@ def test_bruteforce_and_numpy_packers_agree_on_random_rows():
         for r in range(5):
             assert (p[r].view(np.uint32).tolist() == bruteforce.pack_row(q[r].tolist(), bits))
             assert bruteforce.unpack_row(p[r].view(np.uint32).tolist(), bits, 77) == q[r].tolist()
+
+
+# ---------------------------------------------------------------- the paper quantizer's format
+# quantization/crispybits_quant/affine.py and packing.py: pinned by the brute-force fixtures
+# and the inline checks of quantization/tests/test_affine_pack.py.
+
+@pytest.mark.parametrize("case", json.load(open(os.path.join(GOLDEN, "packing_continuous.json"))),
+                         ids=lambda c: f"W{c['bits']}-K{c['K']}")
+def test_continuous_pack_matches_golden(case):
+    q = np.array(case["codes"])
+    p = R.pack_codes_continuous(q, case["bits"])
+    assert p.shape[1] == (case["K"] * case["bits"] + 31) // 32          # packing.py:24-25
+    assert np.array_equal(p, _words(case["words"]))
+    assert np.array_equal(R.unpack_codes_continuous(p, case["K"], case["bits"]), q)
+
+
+@pytest.mark.parametrize("case", json.load(open(os.path.join(GOLDEN, "affine_quantize.json"))),
+                         ids=lambda c: f"W{c['bits']}-K{c['K']}-g{c['group_size']}")
+def test_affine_quantize_matches_golden(case):
+    w = np.stack([_h2f(r) for r in case["w"]])
+    q, s, z = R.affine_quantize_weight(w, case["bits"], case["group_size"])
+    for i, row in enumerate(case["rows"]):
+        assert np.array_equal(q[i], row["q"])
+        assert np.array_equal(s[i], _h2f(row["scale"]))
+        assert np.array_equal(z[i], _h2f(row["zero"]))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_continuous_roundtrip_and_chunked_equivalence(bits):
+    # quantization/tests/test_affine_pack.py:6-12 (K = 259), and the two formats agree iff K % 32 == 0
+    rng = np.random.default_rng(bits)
+    q = rng.integers(0, 1 << bits, size=(7, 259)).astype(np.int32)
+    p = R.pack_codes_continuous(q, bits)
+    assert np.array_equal(R.unpack_codes_continuous(p, 259, bits), q)
+    assert np.array_equal(R.continuous_to_chunked(p, bits, 259), R.pack_codes(q, bits))
+    q32 = q[:, :256]
+    assert np.array_equal(R.pack_codes_continuous(q32, bits), R.pack_codes(q32, bits))
+
+
+def test_affine_shapes():
+    # quantization/tests/test_affine_pack.py:15-20
+    q, s, z = R.affine_quantize_weight(np.random.default_rng(0).standard_normal((5, 257)).astype(np.float32), 3, 128)
+    assert q.shape == (5, 257) and s.shape == (5, 3) and z.shape == (5, 3)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_affine_groups_not_spanning_zero(bits):
+    # quantization/tests/test_affine_pack.py:23-38: error <= half a step of the zero-inclusive range
+    rng = np.random.default_rng(0)
+    qmax = (1 << bits) - 1
+    for w in (rng.random((3, 128), dtype=np.float32) + 1.0, -(rng.random((3, 128), dtype=np.float32) + 1.0),
+              np.full((3, 128), 0.37, np.float32), np.full((3, 128), -0.37, np.float32),
+              np.zeros((3, 128), np.float32)):
+        q, s, z = R.affine_quantize_weight(w, bits, 128)
+        wh = R.dequantize(q, s, z, 128)
+        step = (np.maximum(w, 0).max(1) - np.minimum(w, 0).min(1)) / qmax
+        assert np.all(np.abs(wh - w).max(1) <= step / 2 + 1e-5)
+        assert np.all((z >= 0) & (z <= qmax))
+        # zero-inclusive: an exact 0 weight maps to the zero code and dequantizes to 0 exactly
+        q0, s0, z0 = R.affine_quantize_weight(np.concatenate([w[:, :127], np.zeros((3, 1), np.float32)], 1), bits, 128)
+        assert np.all(R.dequantize(q0, s0, z0, 128)[:, 127] == 0)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_affine_zero_spanning_groups_match_plain_minmax(bits):
+    # quantization/tests/test_affine_pack.py:41-55: where each group spans zero, the clamps
+    # are inactive and the codes are round(w/s + z) of the plain min/max scale
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((4, 256)) * 0.02).astype(np.float32)
+    w[:, 0], w[:, 128], w[:, 1], w[:, 129] = -0.05, 0.05, 0.05, -0.05
+    q, _, _ = R.affine_quantize_weight(w, bits, 128)
+    qmax = np.float32((1 << bits) - 1)
+    for g in range(2):
+        wg = w[:, g * 128:(g + 1) * 128]
+        s = ((wg.max(1) - wg.min(1)) / qmax).astype(np.float32)
+        z = np.clip(np.rint(-wg.min(1) / s), 0, qmax).astype(np.float32)
+        ref = np.clip(np.rint((wg / s[:, None]).astype(np.float32) + z[:, None]), 0, qmax)
+        assert np.array_equal(q[:, g * 128:(g + 1) * 128], ref.astype(np.int32))
+
+
+def test_affine_tie_differs_from_kernel_quantizer():
+    # the two quantizers differ on ties when the zero is odd: round(w/s + z) vs round(w/s) + z
+    w = np.zeros((1, 32), np.float32)
+    w[0, :4] = [-1.0, 0.5, 2.0, 1.5]
+    qa, sa, za = R.affine_quantize_weight(w, 2, 32)
+    qk, sk, zk = R.quantize_affine(w, 2, 32)
+    assert sa[0, 0] == sk[0, 0] == 1.0 and za[0, 0] == zk[0, 0] == 1.0
+    assert qa[0, 1] == 2 and qk[0, 1] == 1
