@@ -72,7 +72,15 @@ def _ptr(t):
     return None if t is None or t.numel() == 0 else t.data_ptr()
 
 
+try:                                                   # the raw handle without a Stream object
+    _raw_stream = torch._C._cuda_getCurrentRawStream
+except AttributeError:                                 # pragma: no cover
+    _raw_stream = None
+
+
 def _stream(x: torch.Tensor) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(x.get_device())
     return torch.cuda.current_stream(x.device).cuda_stream
 
 
@@ -82,6 +90,8 @@ def _check(cond: bool, msg: str):
 
 
 def _check_x(x: torch.Tensor, K: int):
+    if x.is_cuda and x.dim() == 2 and x.is_contiguous() and x.size(1) == K and x.dtype in _DT:
+        return
     _check(x.is_cuda, "x must be CUDA")
     _check(x.dim() == 2, "x must be [B,K]")
     _check(x.is_contiguous(), "x must be contiguous")
@@ -89,7 +99,20 @@ def _check_x(x: torch.Tensor, K: int):
     _check(x.dtype in _DT, "x must be fp16/bf16/fp32")
 
 
+def _weight_ok(x, packed, scales, zeros, bits, K, group_size) -> bool:
+    """Every condition of _check_weight at once (the common, passing case)."""
+    dev, dt = x.device, x.dtype
+    return (packed.dtype == torch.int32 and packed.device == dev and scales.device == dev and zeros.device == dev
+            and scales.dtype == dt and zeros.dtype == dt and packed.dim() == 2 and scales.dim() == 2
+            and packed.is_contiguous() and scales.is_contiguous() and zeros.is_contiguous()
+            and scales.shape == zeros.shape and scales.size(0) == packed.size(0) and bits in (2, 3, 4)
+            and group_size > 0 and group_size % 32 == 0 and packed.size(1) == -(-K // 32) * bits
+            and scales.size(1) == -(-K // group_size))
+
+
 def _check_weight(x, packed, scales, zeros, bits, K, group_size, name):
+    if x.is_cuda and _weight_ok(x, packed, scales, zeros, bits, K, group_size):
+        return
     _check(packed.is_cuda and scales.is_cuda and zeros.is_cuda, f"{name}: tensors must be CUDA")
     _check(packed.device == x.device, f"{name}: weight and activation on different devices")
     _check(scales.device == x.device and zeros.device == x.device, f"{name}: weight and activation on different devices")
@@ -125,8 +148,14 @@ def _workspace(ws, x):
     return None
 
 
+_PARTIAL_FLOATS = {}
+
+
 def _partial(x, M, V, K, group_size, split_k):
-    n = _lib.cbk_gemv_partial_floats(_DT[x.dtype], M, V, K, group_size, int(split_k))
+    key = (_DT[x.dtype], M, V, K, group_size, int(split_k))
+    n = _PARTIAL_FLOATS.get(key)
+    if n is None:
+        n = _PARTIAL_FLOATS[key] = _lib.cbk_gemv_partial_floats(*key)
     return torch.empty(n, dtype=torch.float32, device=x.device) if n > 0 else None
 
 
@@ -145,7 +174,7 @@ def packed_gemv(x, packed, scales, zeros, bias, bits, in_features, group_size, s
     part = _partial(x, x.size(0), N, K, gs, split_k)
     _raise(_lib.cbk_packed_gemv(x.data_ptr(), _DT[x.dtype], x.size(0), K, packed.data_ptr(), scales.data_ptr(),
                                 zeros.data_ptr(), _ptr(b), N, bits, gs, split_k, rho, act, _ptr(ws), _ptr(part),
-                                out.data_ptr(), x.device.index, _stream(x)))
+                                out.data_ptr(), x.get_device(), _stream(x)))
     return out
 
 
@@ -164,7 +193,7 @@ def fused_gate_up(x, wg, sg, zg, wu, su, zu, bits, in_features, group_size, spli
     part = _partial(x, x.size(0), 2 * N, K, gs, split_k)
     _raise(_lib.cbk_fused_gate_up(x.data_ptr(), _DT[x.dtype], x.size(0), K, wg.data_ptr(), sg.data_ptr(),
                                   zg.data_ptr(), wu.data_ptr(), su.data_ptr(), zu.data_ptr(), N, bits, gs, split_k,
-                                  rho, _ptr(ws), _ptr(part), out.data_ptr(), x.device.index, _stream(x)))
+                                  rho, _ptr(ws), _ptr(part), out.data_ptr(), x.get_device(), _stream(x)))
     return out
 
 
@@ -207,7 +236,7 @@ def fused_qkv(x, wq, sq, zq, bq, wk, sk, zk, bk, wv, sv, zv, bv, rope_cos, rope_
               wv.data_ptr(), sv.data_ptr(), zv.data_ptr(), _ptr(b[2]), nv,
               _ptr(rc), _ptr(rs), head_dim if rope else 0, perm_hd)
     tail = (_ptr(ws), _ptr(part), outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(),
-            x.device.index, _stream(x))
+            x.get_device(), _stream(x))
     if bq_ == bk_ == bv_:
         _raise(_lib.cbk_fused_qkv(*common, bq_, gs, split_k, rho, *tail))
     else:
@@ -227,7 +256,7 @@ def packed_gemm(x, packed, scales, zeros, bias, bits, in_features, group_size, a
         return out
     _raise(_lib.cbk_packed_gemm(x.data_ptr(), _DT[x.dtype], x.size(0), K, packed.data_ptr(), scales.data_ptr(),
                                 zeros.data_ptr(), _ptr(b), N, bits, gs, act, 1 if use_tensor_cores else 0,
-                                out.data_ptr(), x.device.index, _stream(x)))
+                                out.data_ptr(), x.get_device(), _stream(x)))
     return out
 
 

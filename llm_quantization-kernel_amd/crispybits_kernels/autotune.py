@@ -6,7 +6,8 @@ every split in EXHAUSTIVE_PK is timed too.  ``best`` is the fastest rule pick,
 Candidates that launch the same (split, workgroup count) are timed once.
 
 Retuned for MI355X: splits are in units of the MFMA kernel's 128-code K unit, so
-the grid stops at 32 (a 4096-wide row has 32 units).
+the grid stops at 32 (a 4096-wide row has 32 units); candidates are ranked by kernel
+time from the library's per-dispatch timer (see ``_time``).
 """
 from __future__ import annotations
 
@@ -44,10 +45,34 @@ class TuneReport:
         return self.best.ms / self.oracle.ms - 1.0
 
 
+def _kernel_timer():
+    """The HIP library's per-dispatch timer when the ops run on it, else None."""
+    from . import ops
+    C = ops._C
+    if C is not None and C is ops._CUDA and hasattr(C, "timer_start"):
+        return C
+    return None
+
+
 def _time(fn: Callable[[], object], warmup: int, iters: int) -> float:
-    """Mean ms per call: device events on a GPU, wall clock otherwise."""
+    """Mean ms per call.  On the HIP library: the summed durations of the call's kernel
+    launches (events recorded inside each dispatch; a split-K call counts its combine
+    launch too), so the ranking sees the kernels and not the host's launch rate -- events
+    around back-to-back calls (the reference's autotune.py:40-48) read the Python
+    dispatch cost here, ~12 us per call, above every decode kernel.  Otherwise device
+    events, or the wall clock on the CPU."""
     for _ in range(warmup):
         fn()
+    C = _kernel_timer()
+    if C is not None:
+        torch.cuda.synchronize()
+        C.timer_start(4 * iters + 16)
+        try:
+            for _ in range(iters):
+                fn()
+        finally:
+            total, _ = C.timer_stop()
+        return total / iters
     if torch.cuda.is_available() and torch.cuda.is_initialized():
         torch.cuda.synchronize()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -98,11 +98,12 @@ def _empty(x: torch.Tensor) -> torch.Tensor:
 
 
 def _bias_tensor(w: PackedLinearWeight, x: torch.Tensor):
-    return w.bias if w.bias is not None else _empty(x)
+    """The bias, or None for none (the backends take None or an empty tensor alike)."""
+    return w.bias
 
 
 def _ws(workspace, x):
-    return workspace if workspace is not None else torch.empty(0, device=x.device, dtype=torch.int32)
+    return workspace
 
 
 def new_workspace(device) -> torch.Tensor:
@@ -281,7 +282,7 @@ def fused_qkv(x: torch.Tensor, q: PackedLinearWeight, k: PackedLinearWeight, v: 
         v_rows = virtual_rows("qkv", q.out_features, k.out_features, v.out_features)
         pk = _resolve(split_k, rho, M, v_rows, q.in_features, x2.device)
         if rope is None:
-            rc, rs, hd = _empty(x2), _empty(x2), 0
+            rc, rs, hd = None, None, 0
         else:
             rc, rs, hd = cos2.float().contiguous(), sin2.float().contiguous(), head_dim
         bits = q.bits if q.bits == k.bits == v.bits else (q.bits, k.bits, v.bits)
