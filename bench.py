@@ -380,6 +380,35 @@ STACK_LINEARS = [("q", STACK_H, STACK_H), ("k", STACK_H, STACK_H), ("v", STACK_H
                  ("gate", STACK_I, STACK_H), ("up", STACK_I, STACK_H), ("down", STACK_H, STACK_I)]   # (name, N, K)
 
 
+def stack_energy(torch, gr, gr16, seconds=4.0):
+    """Energy per decode step of the graph-captured stack and of its fp16 dense twin, from
+    the GPU's energy accumulator over a steady back-to-back run (crispybits_kernels.energy;
+    the paper's energy-per-request metric restricted to the linear stack).  None when
+    AMD-SMI is not usable on the box."""
+    from crispybits_kernels.energy import AMDSMIPowerSampler, steady_energy
+    try:
+        sampler = AMDSMIPowerSampler(torch.cuda.current_device())
+    except RuntimeError as e:
+        log(f"energy: skipped ({e})")
+        return None
+    try:
+        out = {}
+        for name, g in (("packed", gr), ("fp16_dense", gr16)):
+            m = steady_energy(g.replay, sampler, seconds=seconds, synchronize=torch.cuda.synchronize)
+            out[name] = {"J_per_step": round(m.joules, 4), "mean_W": round(m.mean_watts, 1),
+                         "steps": m.samples, "counter_window_s": round(m.seconds, 3)}
+        out["energy_ratio_fp16_over_packed"] = round(out["fp16_dense"]["J_per_step"] / out["packed"]["J_per_step"], 2)
+        out["method"] = ("AMD-SMI energy accumulator between two counter updates inside a ~4 s back-to-back "
+                         "run of the step graph; J/step = mean W x wall time per step")
+        log(f"energy: {out}")
+        return out
+    except RuntimeError as e:
+        log(f"energy: failed ({e})")
+        return None
+    finally:
+        sampler.close()
+
+
 def stack_sweep(torch, C, ops, dev, steps=20):
     """Config 5: the Llama-2-7B linear stack at decode (M = 1), 32 blocks, bits per block
     from default_rng(0).choice([2, 3, 4], 32); block i, linear j weights from a device
@@ -448,10 +477,10 @@ def stack_sweep(torch, C, ops, dev, steps=20):
     gr = graphed(step)
     graph_t = wall(gr.replay, steps)
     kern_ms, durs = timed_kernels(C, step, 4 * STACK_BLOCKS + 64)
-    del gr
     gr16 = graphed(step_fp16)
     fp16_t = wall(gr16.replay, steps)
-    del gr16
+    energy = stack_energy(torch, gr, gr16)
+    del gr, gr16
     dense_gb = sum(t.numel() * 2 for d in dense for t in d.values()) / 1e9
     res = {"workload": "Llama-2-7B linear stack, decode M=1, 32 blocks x (fused QKV, o, fused gate-up, down)",
            "bitmap": bitmap, "mean_bits": round(float(np.mean(bitmap)), 3), "packed_GB": round(packed_gb, 3),
@@ -459,7 +488,7 @@ def stack_sweep(torch, C, ops, dev, steps=20):
            "graph_us_per_step": round(graph_t * 1e6, 1), "kernel_us_per_step": round(kern_ms * 1e3, 1),
            "GBps_graph": round(step_bytes / graph_t / 1e9, 1),
            "fp16_dense_GB": round(dense_gb, 3), "fp16_graph_us_per_step": round(fp16_t * 1e6, 1),
-           "speedup_vs_fp16": round(fp16_t / graph_t, 2)}
+           "speedup_vs_fp16": round(fp16_t / graph_t, 2), "energy": energy}
     log(f"llama2-7b stack: {res}")
     del blocks, dense
     torch.cuda.empty_cache()
