@@ -145,6 +145,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="timed step + roofline only (no sweeps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--sweeps", default="gemv,fused,gemm,stack,producer",
+                    help="comma-separated extra sweeps after the timed step (ignored with --quick)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the fixed launch sequence of the counter passes and exit")
     args = ap.parse_args()
@@ -236,11 +238,17 @@ def main():
 
     del graph
     if not args.quick:
-        out["gemv_sweep"] = gemv_sweep(torch, C, ops, dev)
-        out["fused"] = fused_sweep(torch, C, ops, dev)
-        out["gemm"] = gemm_sweep(torch, C, ops, dev)
-        out["llama2_7b_stack"] = stack_sweep(torch, C, ops, dev)
-        out["producer"] = producer_sweep(torch, C, dev)
+        todo = {w.strip() for w in args.sweeps.split(",") if w.strip()}
+        if "gemv" in todo:
+            out["gemv_sweep"] = gemv_sweep(torch, C, ops, dev)
+        if "fused" in todo:
+            out["fused"] = fused_sweep(torch, C, ops, dev)
+        if "gemm" in todo:
+            out["gemm"] = gemm_sweep(torch, C, ops, dev)
+        if "stack" in todo:
+            out["llama2_7b_stack"] = stack_sweep(torch, C, ops, dev)
+        if "producer" in todo:
+            out["producer"] = producer_sweep(torch, C, dev)
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch, base, xs)
