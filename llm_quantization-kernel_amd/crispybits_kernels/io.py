@@ -2,8 +2,9 @@
 
 Besides the kernels' own chunked layout (reference.py:37-55, ceil(K/32)*bits words per row)
 this accepts the continuous bitstream that the paper's checkpoint packer writes
-(quantization/crispybits_quant/packing.py:24-25, ceil(K*bits/32) words per row) and re-packs
-it into the chunked layout; the two coincide when K % 32 == 0.
+(quantization/crispybits_quant/packing.py:24-25, ceil(K*bits/32) words per row) and pads its
+rows to the chunked length (code k sits at bit k*bits in both); the two coincide when
+K % 32 == 0.
 """
 import math
 

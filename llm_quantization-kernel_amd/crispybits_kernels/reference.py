@@ -143,11 +143,15 @@ def unpack_codes_continuous(packed: torch.Tensor, K: int, bits: int) -> torch.Te
 
 
 def continuous_to_chunked(packed: torch.Tensor, bits: int, K: int) -> torch.Tensor:
-    """A continuous-bitstream weight (crispybits_quant/packing.py) in the kernels' format:
-    the same codes re-packed with each row padded to whole 32-code chunks."""
-    if K % 32 == 0:
-        return packed.to(torch.int32).contiguous()
-    return pack_codes(unpack_codes_continuous(packed, K, bits), bits)
+    """A continuous-bitstream weight (crispybits_quant/packing.py) in the kernels' format.
+    Both put code k at bit k*bits of the row's bitstream and leave the bits past K*bits
+    zero; the chunked rows are only longer (whole 32-code chunks), so the conversion is a
+    zero pad of each row to ceil(K/32)*bits words."""
+    chunked = math.ceil(K / 32) * bits
+    p = packed.to(torch.int32)
+    if p.shape[1] < chunked:
+        p = torch.nn.functional.pad(p, (0, chunked - p.shape[1]))
+    return p.contiguous()
 
 
 SCHEMES = ("kernel", "affine")
