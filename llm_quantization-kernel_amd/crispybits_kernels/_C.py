@@ -100,9 +100,11 @@ def _check_x(x: torch.Tensor, K: int):
 
 
 def _weight_ok(x, packed, scales, zeros, bits, K, group_size) -> bool:
-    """Every condition of _check_weight at once (the common, passing case)."""
-    dev, dt = x.device, x.dtype
-    return (packed.dtype == torch.int32 and packed.device == dev and scales.device == dev and zeros.device == dev
+    """Every condition of _check_weight at once (the common, passing case; devices compared
+    by index, -1 for a CPU tensor)."""
+    dev, dt = x.get_device(), x.dtype
+    return (packed.dtype == torch.int32 and packed.get_device() == dev and scales.get_device() == dev
+            and zeros.get_device() == dev
             and scales.dtype == dt and zeros.dtype == dt and packed.dim() == 2 and scales.dim() == 2
             and packed.is_contiguous() and scales.is_contiguous() and zeros.is_contiguous()
             and scales.shape == zeros.shape and scales.size(0) == packed.size(0) and bits in (2, 3, 4)
@@ -131,7 +133,9 @@ def _check_weight(x, packed, scales, zeros, bits, K, group_size, name):
 
 
 def _bias(bias, x, N):
-    if bias is None or bias.numel() == 0:
+    if bias is None:
+        return None
+    if bias.numel() == 0:
         return None
     _check(bias.is_cuda and bias.device == x.device, "bias must be on x's device")
     _check(bias.numel() == N, "bias length must equal out_features")
@@ -141,7 +145,9 @@ def _bias(bias, x, N):
 
 
 def _workspace(ws, x):
-    if ws is not None and ws.numel() >= 2:
+    if ws is None:
+        return None
+    if ws.numel() >= 2:
         _check(ws.is_cuda and ws.device == x.device, "workspace must be on x's device")
         _check(ws.dtype == torch.int32 and ws.is_contiguous(), "workspace must be contiguous int32")
         return ws
@@ -165,16 +171,19 @@ def packed_gemv(x, packed, scales, zeros, bias, bits, in_features, group_size, s
     _check_weight(x, packed, scales, zeros, bits, K, gs, "packed_gemv")
     _check(split_k >= 1, "split_k must be >= 1")
     _check(0 <= act <= 2, "act must be 0 (none), 1 (relu) or 2 (silu)")
-    N = packed.size(0)
+    N, M = packed.size(0), x.size(0)
     b = _bias(bias, x, N)
     ws = _workspace(workspace, x)
-    out = torch.empty((x.size(0), N), dtype=x.dtype, device=x.device)
-    if x.size(0) == 0:
+    out = x.new_empty((M, N))
+    if M == 0:
         return out
-    part = _partial(x, x.size(0), N, K, gs, split_k)
-    _raise(_lib.cbk_packed_gemv(x.data_ptr(), _DT[x.dtype], x.size(0), K, packed.data_ptr(), scales.data_ptr(),
-                                zeros.data_ptr(), _ptr(b), N, bits, gs, split_k, rho, act, _ptr(ws), _ptr(part),
-                                out.data_ptr(), x.get_device(), _stream(x)))
+    part = _partial(x, M, N, K, gs, split_k)
+    dev = x.get_device()
+    rc = _lib.cbk_packed_gemv(x.data_ptr(), _DT[x.dtype], M, K, packed.data_ptr(), scales.data_ptr(),
+                              zeros.data_ptr(), _ptr(b), N, bits, gs, split_k, rho, act, _ptr(ws), _ptr(part),
+                              out.data_ptr(), dev, _raw_stream(dev) if _raw_stream is not None else _stream(x))
+    if rc:
+        _raise(rc)
     return out
 
 
@@ -186,14 +195,16 @@ def fused_gate_up(x, wg, sg, zg, wu, su, zu, bits, in_features, group_size, spli
     _check(wg.shape == wu.shape, "gate/up packed shapes must match")
     _check(split_k >= 1, "split_k must be >= 1")
     ws = _workspace(workspace, x)
-    N = wg.size(0)
-    out = torch.empty((x.size(0), N), dtype=x.dtype, device=x.device)
-    if x.size(0) == 0:
+    N, M = wg.size(0), x.size(0)
+    out = x.new_empty((M, N))
+    if M == 0:
         return out
-    part = _partial(x, x.size(0), 2 * N, K, gs, split_k)
-    _raise(_lib.cbk_fused_gate_up(x.data_ptr(), _DT[x.dtype], x.size(0), K, wg.data_ptr(), sg.data_ptr(),
-                                  zg.data_ptr(), wu.data_ptr(), su.data_ptr(), zu.data_ptr(), N, bits, gs, split_k,
-                                  rho, _ptr(ws), _ptr(part), out.data_ptr(), x.get_device(), _stream(x)))
+    part = _partial(x, M, 2 * N, K, gs, split_k)
+    rc = _lib.cbk_fused_gate_up(x.data_ptr(), _DT[x.dtype], M, K, wg.data_ptr(), sg.data_ptr(),
+                                zg.data_ptr(), wu.data_ptr(), su.data_ptr(), zu.data_ptr(), N, bits, gs, split_k,
+                                rho, _ptr(ws), _ptr(part), out.data_ptr(), x.get_device(), _stream(x))
+    if rc:
+        _raise(rc)
     return out
 
 
@@ -224,9 +235,9 @@ def fused_qkv(x, wq, sq, zq, bq, wk, sk, zk, bk, wv, sv, zv, bv, rope_cos, rope_
         rc = rope_cos.to(device=x.device, dtype=torch.float32).contiguous()
         rs = rope_sin.to(device=x.device, dtype=torch.float32).contiguous()
     nq, nk, nv = wq.size(0), wk.size(0), wv.size(0)
-    b = [_bias(bb, x, n) for bb, n in ((bq, nq), (bk, nk), (bv, nv))]
+    b = (_bias(bq, x, nq), _bias(bk, x, nk), _bias(bv, x, nv))
     ws = _workspace(workspace, x)
-    outs = [torch.empty((B, n), dtype=x.dtype, device=x.device) for n in (nq, nk, nv)]
+    outs = [x.new_empty((B, n)) for n in (nq, nk, nv)]
     if B == 0:
         return outs
     part = _partial(x, B, nq + nk + nv, K, gs, split_k)

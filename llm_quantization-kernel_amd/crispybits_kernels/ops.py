@@ -185,11 +185,13 @@ def candidate_split_k(batch: int, n: int, bn: int, sms: int, rho: int, max_split
     return pk if max_split is None else min(max_split, pk)
 
 
-def _resolve(split_k: Optional[int], rho: int, batch: int, v_rows: int, k: int, device) -> int:
-    """split_k=None means: apply the underfill rule at call time for this batch size."""
-    nchunks = ceil(k / 32)
+def _resolve(split_k: Optional[int], rho: int, batch: int, v_rows: int, k: int, where) -> int:
+    """split_k=None means: apply the underfill rule at call time for this batch size.
+    ``where`` is the activation tensor or its device (looked at only for the rule)."""
+    nchunks = -(-k // 32)
     if split_k is not None:
         return max(1, min(int(split_k), nchunks))
+    device = where.device if isinstance(where, torch.Tensor) else where
     idx = device.index if device.index is not None else (torch.cuda.current_device() if device.type == "cuda" else 0)
     tiles = ceil(batch / BATCH_TILE)
     return max(1, min(candidate_split_k(tiles, v_rows, tile_n(), _sm_count_for(idx), rho), nchunks))
@@ -207,18 +209,19 @@ def packed_linear(x: torch.Tensor, w: PackedLinearWeight, split_k: Optional[int]
 
 def _packed_linear_raw(x, w, split_k=None, rho=1, act=None, decode_threshold=DECODE_THRESHOLD,
                        workspace=None, use_tensor_cores=True):
-    original = x.shape[:-1]
-    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    flat = x.dim() == 2
+    original = None if flat else x.shape[:-1]
+    x2 = (x if flat else x.reshape(-1, x.shape[-1])).contiguous()
     bias = _bias_tensor(w, x2)
     a = ACT[act]
     if x2.shape[0] <= decode_threshold:
-        pk = _resolve(split_k, rho, x2.shape[0], w.out_features, w.in_features, x2.device)
+        pk = _resolve(split_k, rho, x2.shape[0], w.out_features, w.in_features, x2)
         y = _C.packed_gemv(x2, w.packed, w.scales, w.zeros, bias, w.bits, w.in_features, w.group_size,
                            pk, rho, a, _ws(workspace, x2))
     else:
         y = _C.packed_gemm(x2, w.packed, w.scales, w.zeros, bias, w.bits, w.in_features, w.group_size,
                            a, use_tensor_cores)
-    return y.reshape(*original, w.out_features)
+    return y if flat else y.reshape(*original, w.out_features)
 
 
 def fused_gate_up(x: torch.Tensor, gate: PackedLinearWeight, up: PackedLinearWeight,
@@ -229,19 +232,20 @@ def fused_gate_up(x: torch.Tensor, gate: PackedLinearWeight, up: PackedLinearWei
     _check_ext()
     if gate.bits != up.bits:
         raise ValueError("fused Gate/Up requires the same precision for Gate and Up within a block")
-    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    flat = x.dim() == 2
+    x2 = (x if flat else x.reshape(-1, x.shape[-1])).contiguous()
     if x2.shape[0] <= decode_threshold:
         pk = _resolve(split_k, rho, x2.shape[0], virtual_rows("gate_up", gate.out_features),
-                      gate.in_features, x2.device)
+                      gate.in_features, x2)
         y = _C.fused_gate_up(x2, gate.packed, gate.scales, gate.zeros, up.packed, up.scales, up.zeros,
                              gate.bits, gate.in_features, gate.group_size, pk, rho, _ws(workspace, x2))
     else:
-        g = _C.packed_gemm(x2, gate.packed, gate.scales, gate.zeros, _empty(x2), gate.bits, gate.in_features,
+        g = _C.packed_gemm(x2, gate.packed, gate.scales, gate.zeros, None, gate.bits, gate.in_features,
                            gate.group_size, ACT["silu"], True)
-        u = _C.packed_gemm(x2, up.packed, up.scales, up.zeros, _empty(x2), up.bits, up.in_features,
+        u = _C.packed_gemm(x2, up.packed, up.scales, up.zeros, None, up.bits, up.in_features,
                            up.group_size, 0, True)
         y = g * u
-    return y.reshape(*x.shape[:-1], gate.out_features)
+    return y if flat else y.reshape(*x.shape[:-1], gate.out_features)
 
 
 def apply_rope_reference(t: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, head_dim: int) -> torch.Tensor:
@@ -267,8 +271,9 @@ def fused_qkv(x: torch.Tensor, q: PackedLinearWeight, k: PackedLinearWeight, v: 
     if q.rope_perm_head_dim != k.rope_perm_head_dim or v.rope_perm_head_dim:
         raise ValueError("Q and K must be permuted with the same head_dim; V must not be permuted")
     perm = q.rope_perm_head_dim
+    flat = x.dim() == 2
     pre = x.shape[:-1]
-    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    x2 = (x if flat else x.reshape(-1, x.shape[-1])).contiguous()
     M = x2.shape[0]
     if rope is not None:
         cos, sin, head_dim = rope
@@ -280,7 +285,7 @@ def fused_qkv(x: torch.Tensor, q: PackedLinearWeight, k: PackedLinearWeight, v: 
         sin2 = sin.expand(*pre, head_dim).reshape(M, head_dim)
     if M <= decode_threshold:
         v_rows = virtual_rows("qkv", q.out_features, k.out_features, v.out_features)
-        pk = _resolve(split_k, rho, M, v_rows, q.in_features, x2.device)
+        pk = _resolve(split_k, rho, M, v_rows, q.in_features, x2)
         if rope is None:
             rc, rs, hd = None, None, 0
         else:
@@ -296,6 +301,8 @@ def fused_qkv(x: torch.Tensor, q: PackedLinearWeight, k: PackedLinearWeight, v: 
         if rope is not None:
             oq = apply_rope_reference(oq, cos2, sin2, head_dim)
             ok = apply_rope_reference(ok, cos2, sin2, head_dim)
+    if flat:
+        return oq, ok, ov
     return oq.reshape(*pre, q.out_features), ok.reshape(*pre, k.out_features), ov.reshape(*pre, v.out_features)
 
 
