@@ -152,7 +152,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one MI355X; --gpus {args.gpus} is not supported "
-              "(the decode path would shard by output rows, see DESIGN.md)", file=sys.stderr)
+              "(one GPU's share is the same kernel at a smaller N: column-parallel linears shard output rows, "
+              "row-parallel ones K with an all-reduce of the fp32 partials)", file=sys.stderr)
         sys.exit(2)
 
     import torch

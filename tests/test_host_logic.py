@@ -260,3 +260,14 @@ def test_paper_checkpoint_dir_installs(emu, tmp_path):
     assert (la - lb).abs().max() / la.abs().max() < 2e-2
     with pytest.raises(ValueError):
         install_bitmap(copy.deepcopy(base), tmp_path, [4, 2, 4], device="cpu", dtype=dtype)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; any other --gpus exits non-zero with a message, before
+    touching a device."""
+    import subprocess
+    import sys
+    root = __import__("os").path.dirname(__import__("os").path.dirname(__import__("os").path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "bench.py", "--gpus", "2", "--steps", "1"], cwd=root,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "--gpus 2 is not supported" in r.stderr
