@@ -172,6 +172,17 @@ def fused_qkv(x, wq, sq, zq, bq, wk, sk, zk, bk, wv, sv, zv, bv, rope_cos, rope_
     return outs
 
 
+def rope64(y: np.ndarray, cos: np.ndarray, sin: np.ndarray, head_dim: int) -> np.ndarray:
+    """HF rotate-half RoPE in float64 on un-permuted outputs y [M, H*head_dim] with cos/sin
+    [M, head_dim], one row per x row (apply_rope_reference, Kernel/crispybits_kernels/
+    ops.py:224-231; the fused epilogue's rotation, packed_gemv.cu:69-79)."""
+    M, W = y.shape
+    t = y.reshape(M, W // head_dim, head_dim)
+    h = head_dim // 2
+    rot = np.concatenate([-t[..., h:], t[..., :h]], axis=-1)
+    return (t * cos[:, None, :] + rot * sin[:, None, :]).reshape(M, W)
+
+
 def round_to(a: np.ndarray, dtype: torch.dtype) -> np.ndarray:
     """Round a float64 array once to ``dtype`` and back (RN-even)."""
     return torch.from_numpy(a).to(dtype).to(torch.float64).numpy()

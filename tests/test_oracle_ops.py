@@ -130,3 +130,20 @@ def test_gemm_weight_rounded_once(dtype):
             g = k // 32
             exact = (float(q[n, k]) - float(z[n, g])) * float(s[n, g])
             assert W[n, k] == torch.tensor(exact, dtype=torch.float32).to(dtype).double().item()
+
+
+def test_rope64_is_a_complex_rotation():
+    """rotate-half RoPE on the pair (d, d + h) is the complex product
+    (y_d + i y_{d+h}) * e^{i theta_d} with HF's tables cos/sin = cat(f, f)."""
+    rng = np.random.default_rng(5)
+    M, heads, hd = 3, 4, 64
+    h = hd // 2
+    y = rng.standard_normal((M, heads * hd))
+    theta = rng.uniform(-7, 7, (M, h))
+    cos, sin = np.cos(np.concatenate([theta, theta], -1)), np.sin(np.concatenate([theta, theta], -1))
+    out = E.rope64(y, cos, sin, hd).reshape(M, heads, hd)
+    t = y.reshape(M, heads, hd)
+    z = (t[..., :h] + 1j * t[..., h:]) * np.exp(1j * theta)[:, None, :]
+    assert np.allclose(out[..., :h], z.real, atol=1e-12) and np.allclose(out[..., h:], z.imag, atol=1e-12)
+    # angle zero is the identity; norms of each pair are kept
+    assert np.array_equal(E.rope64(y, np.ones((M, hd)), np.zeros((M, hd)), hd), y)
