@@ -72,6 +72,21 @@ int cbk_packed_gemv(const void* x, int dtype, int64_t M, int64_t K,
                     int64_t N, int bits, int group_size, int split_k, int rho, int act,
                     int32_t* workspace, float* partial, void* out, int device, void* stream);
 
+/* Allocation-free variant of cbk_packed_gemv.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The split-K partial sums live in a file-scope
+ * device array of CBK_NOALLOC_PARTIAL_FLOATS fp32 values per GPU (8 MiB, held until the
+ * process ends) instead of a caller buffer; calls whose cbk_gemv_partial_floats(...)
+ * exceeds that return CBK_EINVAL.  The call allocates nothing (no hipMalloc, no library
+ * allocation); every partial it reads it has written in the same call, so nothing needs
+ * clearing between calls.  Calls that overlap on one GPU (concurrent streams, threads)
+ * share the array and race. */
+#define CBK_NOALLOC_PARTIAL_FLOATS (1 << 21)
+int cbk_packed_gemv_noalloc(const void* x, int dtype, int64_t M, int64_t K,
+                            const int32_t* packed, const void* scales, const void* zeros, const void* bias,
+                            int64_t N, int bits, int group_size, int split_k, int rho, int act,
+                            void* out, int device, void* stream);
+
 /* out[M,N] = silu(x . G-hat^T) * (x . U-hat^T) with gate and up read in one pass
  * (replaces fused_gate_up_cuda, packed_gemv.cu:317-337; bindings.cpp:10-13). */
 int cbk_fused_gate_up(const void* x, int dtype, int64_t M, int64_t K,

@@ -38,6 +38,7 @@ _SIGS = {
     "cbk_max_rho": (_I, [_I, _I, _I, ctypes.POINTER(_I)]),
     "cbk_gemv_partial_floats": (_L, [_I, _L, _L, _L, _I, _I]),
     "cbk_packed_gemv": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
+    "cbk_packed_gemv_noalloc": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _I, _P]),
     "cbk_fused_gate_up": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
     "cbk_fused_qkv": (_I, [_P, _I, _L, _L,
                            _P, _P, _P, _P, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _L,

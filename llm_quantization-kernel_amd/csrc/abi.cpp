@@ -102,6 +102,28 @@ int cu_count(int device) {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Split-K partial sums of the allocation-free decode entry point (cbk_packed_gemv_noalloc):
+// a file-scope device array, one copy per GPU, held until the process ends.  Host code
+// never passes `scratch` itself (on the host it names a stand-in, not device memory): it
+// looks up each device's address once, with that device current, and passes that.
+constexpr int64_t NOALLOC_PARTIAL_FLOATS = CBK_NOALLOC_PARTIAL_FLOATS;
+static __device__ __align__(256) float scratch[NOALLOC_PARTIAL_FLOATS];
+float* g_scratch[MAX_DEVICES];
+hipError_t g_scratch_err[MAX_DEVICES];
+std::once_flag g_scratch_once[MAX_DEVICES];
+
+// This device's copy of `scratch`; the caller has made `device` current.
+hipError_t scratch_for(int device, float** out) {
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::call_once(g_scratch_once[device], [device] {
+        void* p = nullptr;
+        g_scratch_err[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch[device] = g_scratch_err[device] == hipSuccess ? static_cast<float*>(p) : nullptr;
+    });
+    *out = g_scratch[device];
+    return g_scratch_err[device];
+}
+
 constexpr int MFMA_TILE = 16;          // virtual rows per MFMA decode job
 constexpr int LDS_BUDGET = 160 * 1024; // dynamic LDS per decode workgroup (gfx950: 160 KB per CU)
 constexpr int WAVES_PER_CU = 8;        // decode occupancy target
@@ -667,6 +689,36 @@ int cbk_packed_gemv(const void* x, int dtype, int64_t M, int64_t K, const int32_
     A.V = (int)N;
     A.act = act;
     return run_decode(A, dtype, CBK_MODE_GEMV, false, split_k, rho, partial, device, stream);
+}
+
+int cbk_packed_gemv_noalloc(const void* x, int dtype, int64_t M, int64_t K, const int32_t* packed,
+                            const void* scales, const void* zeros, const void* bias, int64_t N, int bits,
+                            int group_size, int split_k, int rho, int act, void* out, int device, void* stream) {
+    int rc = check_x(x, dtype, M, K);
+    if (rc) return rc;
+    if ((rc = check_weight(packed, scales, zeros, N, bits, group_size, "packed_gemv_noalloc"))) return rc;
+    if (split_k < 1) return fail(CBK_EINVAL, "split_k must be >= 1");
+    if (act < 0 || act > 2) return fail(CBK_EINVAL, "act must be 0 (none), 1 (relu) or 2 (silu)");
+    if (!out) return fail(CBK_EINVAL, "packed_gemv_noalloc: out must be non-null");
+    const int64_t need = cbk_gemv_partial_floats(dtype, M, N, K, group_size, split_k);
+    if (need > NOALLOC_PARTIAL_FLOATS)
+        return fail(CBK_EINVAL,
+                    "packed_gemv_noalloc: split-K partial sums need %lld floats, above the %lld-float device "
+                    "scratch (use cbk_packed_gemv with a caller buffer, or a smaller split_k or batch)",
+                    (long long)need, (long long)NOALLOC_PARTIAL_FLOATS);
+    if (M == 0) return CBK_OK;
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    float* part = nullptr;
+    const hipError_t e = scratch_for(device, &part);
+    if (e != hipSuccess) return hip_fail(e, "packed_gemv_noalloc: scratch address");
+    GemvArgs A = base_args(x, M, K, group_size);
+    A.p[0] = make_proj(packed, scales, zeros, bias, out, N, bits, K);
+    A.p[1] = A.p[0];
+    A.p[2] = A.p[0];
+    A.V = (int)N;
+    A.act = act;
+    return run_decode(A, dtype, CBK_MODE_GEMV, false, split_k, rho, need > 0 ? part : nullptr, device, stream);
 }
 
 int cbk_fused_gate_up(const void* x, int dtype, int64_t M, int64_t K, const int32_t* wg, const void* sg,
