@@ -56,9 +56,21 @@ int cbk_sm_count(int device, int* out);
  * (replaces crispybits_tile_n, packed_gemv.cu:340). */
 int cbk_tile_n(void);
 
-/* Occupancy-limited resident decode workgroups per CU of the fp16 kernel for `bits`
- * and `mode` (replaces crispybits_max_rho_mode, packed_gemv.cu:343-347). */
+/* Occupancy-limited resident workgroups per CU of the kernel an fp16 batch-1 decode call of
+ * `mode` runs at the Llama-2-7B widths (K = 4096), at that call's workgroup size and LDS
+ * (replaces crispybits_max_rho_mode, packed_gemv.cu:343-347). */
 int cbk_max_rho(int device, int bits, int mode, int* out);
+
+/* Decode kernel families reported by cbk_decode_plan. */
+enum { CBK_KERNEL_STREAM = 1, CBK_KERNEL_BSTREAM = 2, CBK_KERNEL_MFMA = 3, CBK_KERNEL_GENERIC = 4 };
+
+/* Additive policy query (no counterpart in the reference, whose tuner infers launches from
+ * (split_k, rho), autotune.py:55-88): the launch a decode call with these arguments makes,
+ * without launching it.  out[6] = {kernel family, K splits, workgroups, threads per workgroup,
+ * dynamic LDS bytes, launches per call}.  n1/n2 and bits1/bits2 are read for CBK_MODE_QKV
+ * only; tensors are assumed allocated as torch allocates them (aligned bases). */
+int cbk_decode_plan(int dtype, int64_t M, int64_t K, int group_size, int64_t n0, int64_t n1, int64_t n2,
+                    int bits0, int bits1, int bits2, int mode, int split_k, int rho, int device, int32_t* out);
 
 /* fp32 elements of `partial` that a decode call with these arguments needs
  * (0 = none).  `V` is the number of virtual rows (N, nq+nk+nv or 2N). */

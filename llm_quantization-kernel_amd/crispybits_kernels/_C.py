@@ -36,6 +36,7 @@ _SIGS = {
     "cbk_sm_count": (_I, [_I, ctypes.POINTER(_I)]),
     "cbk_tile_n": (_I, []),
     "cbk_max_rho": (_I, [_I, _I, _I, ctypes.POINTER(_I)]),
+    "cbk_decode_plan": (_I, [_I, _L, _L, _I, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _P]),
     "cbk_gemv_partial_floats": (_L, [_I, _L, _L, _L, _I, _I]),
     "cbk_packed_gemv": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
     "cbk_packed_gemv_noalloc": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P, _I, _P]),
@@ -324,6 +325,23 @@ def max_rho(bits, kind="gemv") -> int:
     v = _I()
     _raise(_lib.cbk_max_rho(_device_index(), int(bits), _KIND[kind], ctypes.byref(v)))
     return v.value
+
+
+PLAN_FAMILIES = {1: "stream", 2: "bstream", 3: "mfma", 4: "generic"}
+
+
+def decode_plan(dtype, batch, in_features, group_size, out_features, bits, kind, split_k, rho):
+    """Additive policy query: the launch a decode call would make, as a tuple (kernel family,
+    K splits, workgroups, threads per workgroup, LDS bytes, launches per call).
+    ``out_features`` / ``bits`` are one value, or (q, k, v) tuples for kind "qkv"."""
+    if kind not in _KIND:
+        raise RuntimeError("kind must be 'gemv', 'qkv' or 'gate_up'")
+    ns = tuple(int(n) for n in out_features) if isinstance(out_features, (tuple, list)) else (int(out_features),) * 3
+    bs = tuple(int(b) for b in bits) if isinstance(bits, (tuple, list)) else (int(bits),) * 3
+    out = (ctypes.c_int32 * 6)()
+    _raise(_lib.cbk_decode_plan(_DT[dtype], int(batch), int(in_features), int(group_size), *ns, *bs, _KIND[kind],
+                                int(split_k), int(rho), _device_index(), out))
+    return (PLAN_FAMILIES.get(out[0], "?"),) + tuple(out[1:])
 
 
 def timer_start(capacity: int = 4096):

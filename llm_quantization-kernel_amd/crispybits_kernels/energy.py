@@ -94,39 +94,66 @@ class AMDSMIPowerSampler(PowerSampler):
         self.smi.amdsmi_shut_down()
 
 
+class _PowerTrace:
+    """Power readings taken every ``period`` seconds on a daemon thread, one before the
+    window opens and one after it closes, so the window's edges can be interpolated."""
+
+    def __init__(self, sampler: PowerSampler, period: float):
+        self.sampler, self.period = sampler, period
+        self.t: List[float] = []
+        self.w: List[float] = []
+        self._stop = Event()
+        self._thread = Thread(target=self._run, daemon=True)
+
+    def _read(self):
+        w = self.sampler.read_watts()
+        self.t.append(perf_counter())
+        self.w.append(w)
+
+    def _run(self):
+        while not self._stop.wait(self.period):
+            self._read()
+
+    def __enter__(self):
+        self._read()
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._thread.join()
+        self._read()
+        return False
+
+    def energy(self, t0: float, t1: float) -> float:
+        """Trapezoid integral of the readings over [t0, t1], the edge powers interpolated
+        between the readings around them (held at the nearest reading beyond the ends)."""
+        import numpy as np
+        t, w = np.asarray(self.t), np.asarray(self.w)
+        inside = (t > t0) & (t < t1)
+        ts = np.concatenate(([t0], t[inside], [t1]))
+        ws = np.concatenate(([np.interp(t0, t, w)], w[inside], [np.interp(t1, t, w)]))
+        return float(np.trapezoid(ws, ts))
+
+
 def integrate_energy(fn: Callable[[], None], sampler: PowerSampler, hz: float = 50.0,
                      synchronize: Optional[Callable[[], None]] = None) -> EnergyMeasurement:
-    """Energy of one call of ``fn`` from power sampled at ``hz`` by a background thread,
-    integrated with trapezoids over [start, end] (energy.py:50-93 of the reference); the
-    first and last samples are extended to the window's edges."""
-    period = 1.0 / hz
-    stop = Event()
-    samples: List[Tuple[float, float]] = []
-
-    def worker():
-        while not stop.is_set():
-            samples.append((perf_counter(), sampler.read_watts()))
-            sleep(period)
-
+    """Energy of one call of ``fn`` from its power readings at ``hz`` (the reference's
+    integrate_energy interface, quantization/crispybits_quant/energy.py:50-93): the window
+    runs from after a first ``synchronize`` to after the last one; the readings inside it,
+    plus the powers at its two edges interpolated from the readings around them, are
+    integrated with the trapezoid rule.  ``samples`` counts the readings inside the window."""
     if synchronize:
         synchronize()
-    t0 = perf_counter()
-    th = Thread(target=worker, daemon=True)
-    th.start()
-    fn()
-    if synchronize:
-        synchronize()
-    t1 = perf_counter()
-    stop.set()
-    th.join()
-    pts = list(samples) or [(t0, sampler.read_watts())]
-    pts = [(t0, pts[0][1])] + pts + [(t1, pts[-1][1])]
-    joules = 0.0
-    for (ta, pa), (tb, pb) in zip(pts[:-1], pts[1:]):
-        a, b = max(t0, ta), min(t1, tb)
-        if b > a:
-            joules += 0.5 * (pa + pb) * (b - a)
-    return EnergyMeasurement(joules, t1 - t0, len(pts), joules / max(t1 - t0, 1e-12))
+    with _PowerTrace(sampler, 1.0 / hz) as trace:
+        t0 = perf_counter()
+        fn()
+        if synchronize:
+            synchronize()
+        t1 = perf_counter()
+    joules = trace.energy(t0, t1)
+    inside = sum(1 for t in trace.t if t0 < t < t1)
+    return EnergyMeasurement(joules, t1 - t0, inside + 2, joules / max(t1 - t0, 1e-12))
 
 
 def steady_energy(step: Callable[[], None], sampler: PowerSampler, seconds: float = 4.0, settle: float = 1.1,

@@ -1,23 +1,32 @@
-"""Hugging Face model surgery: swap nn.Linear for PackedLinear and fuse Q/K/V and
-gate/up (Kernel/crispybits_kernels/integration.py:1-230 interface).
+"""Model surgery for Hugging Face causal LMs: packed linears in, fused decode paths on.
 
-install_bitmap(model, packed_dir, bitmap) loads block_{i:03d}_w{bits}.pt per block,
-replaces each listed linear, and with ``fuse`` routes
-  * q/k/v_proj through one FusedQKV owner (proxies hand out its cached outputs),
-    optionally with RoPE applied in the decode kernel (``fuse_rope``: Q/K rows are
-    stored pair-interleaved, the attention forward primes the owner with the
-    position embeddings and marks them so the model's own apply_rotary_pos_emb
-    skips the already-rotated tensors);
-  * LLaMA MLP gate/up through fused_gate_up (SiLU gating in the epilogue);
-  * OPT fc1 + ReLU through the GEMV's ReLU epilogue.
-Packed dicts are loaded with ``torch.load(weights_only=True)``.
+``install_bitmap(model, packed_dir, bitmap)`` keeps the reference's interface and file
+layout (Kernel/crispybits_kernels/integration.py:201-218): block i's linears come from
+``block_{i:03d}_w{bits}.pt`` (or the paper's ``block_{i:03d}.pt`` + ``manifest.json``), each
+becomes a ``PackedLinear``, and with ``fuse`` the block's decode paths are fused.  The
+mechanism is this build's own:
+
+* **Validate, then install, per block.**  A block's file is read and every entry checked
+  (width against the bitmap, target is an ``nn.Linear``) before any of its modules is
+  replaced, so a bad entry never leaves a half-converted block.
+* **Fusion rules.**  Each block is offered to a short list of rules (``_FUSIONS``), each
+  recognising one pattern and rewriting it: Q/K/V of an attention into one ``FusedQKV``
+  owner with three slot modules; a SiLU-gated MLP into ``FusedLlamaMLP`` (gate and up in one
+  decode pass); an OPT ``fc1`` followed by ReLU into the GEMV's ReLU epilogue.
+* **Fused RoPE through module hooks.**  When RoPE is fused, a forward pre-hook on the
+  attention evaluates Q/K/V of its ``hidden_states`` with Q/K rotated by its
+  ``position_embeddings`` (``FusedQKV.prime``) and passes the attention *identity tables*
+  (cos = 1, sin = 0) in their place, so the model's own rotation leaves the pre-rotated Q/K
+  exactly as they are (q * 1 + rotate_half(q) * 0 = q); a forward hook (always called)
+  drops whatever the slots did not take.  No modeling function is patched and nothing
+  outside the converted modules changes.
 """
 from __future__ import annotations
 
+import inspect
 import json
-import sys
 from pathlib import Path
-from typing import Dict, Optional
+from typing import Dict, List, Optional
 
 import torch
 import torch.nn as nn
@@ -25,36 +34,58 @@ import torch.nn as nn
 from .io import from_packed_dict
 from .ops import PackedLinear, fused_gate_up, fused_qkv, new_workspace
 
-_PREROTATED = "_crispybits_prerotated"
+_DECODER_PATHS = (("model", "layers"), ("model", "decoder", "layers"))
 
 
-def _blocks(model):
-    inner = getattr(model, "model", None)
-    if inner is not None and hasattr(inner, "layers"):
-        return list(inner.layers)
-    if inner is not None and hasattr(getattr(inner, "decoder", None), "layers"):
-        return list(inner.decoder.layers)
+def _blocks(model) -> List[nn.Module]:
+    """The decoder blocks of a LLaMA-family (model.layers) or OPT (model.decoder.layers) LM."""
+    for path in _DECODER_PATHS:
+        node = model
+        for attr in path:
+            node = getattr(node, attr, None)
+            if node is None:
+                break
+        if node is not None:
+            return list(node)
     raise ValueError("Supported integration targets are Hugging Face LLaMA-family and OPT causal LMs")
 
 
 def _get(root: nn.Module, name: str):
-    for part in name.split("."):
-        root = getattr(root, part, None)
-        if root is None:
+    node = root
+    for attr in name.split("."):
+        node = getattr(node, attr, None)
+        if node is None:
             return None
-    return root
+    return node
 
 
 def _set_by_dotted_name(root: nn.Module, name: str, module: nn.Module):
-    *path, leaf = name.split(".")
-    for part in path:
-        root = getattr(root, part)
-    setattr(root, leaf, module)
+    parent, _, leaf = name.rpartition(".")
+    setattr(_get(root, parent) if parent else root, leaf, module)
+
+
+# ----------------------------------------------------------------------------- fused Q/K/V
+
+class _Parked:
+    """Outputs of one fused Q/K/V evaluation waiting for their slots."""
+    __slots__ = ("source", "version", "outs", "rotated")
+
+    def __init__(self, source, outs, rotated):
+        self.source, self.version, self.outs, self.rotated = source, source._version, list(outs), rotated
+
+    def matches(self, x, idx):
+        return self.source is x and self.version == x._version and self.outs[idx] is not None
 
 
 class FusedQKV(nn.Module):
-    """Owns the packed q/k/v projections of one attention layer and computes them
-    in a single fused decode pass; the _QKVProxy modules read its cached outputs."""
+    """Q/K/V of one attention layer served by one fused decode call.
+
+    The attention's ``q_proj`` / ``k_proj`` / ``v_proj`` become slots (``_QKVProxy``) drawing
+    on this owner.  ``prime(x, cos, sin)`` evaluates Q/K/V of x with Q/K rotated and parks the
+    three outputs; a slot called with the parked input takes its output once.  Unprimed, the
+    first slot call evaluates all three (no rotation) and parks the other two.  A slot called
+    with another input while rotated outputs are parked raises RuntimeError: the model would
+    rotate that input's Q/K a second time."""
 
     def __init__(self, q: PackedLinear, k: PackedLinear, v: PackedLinear, split_k=None, rho: int = 1,
                  rope_head_dim: int = 0):
@@ -63,117 +94,95 @@ class FusedQKV(nn.Module):
         self.split_k, self.rho = split_k, int(rho)
         self.rope_head_dim = int(rope_head_dim)
         self.register_buffer("workspace", new_workspace(q.packed.device), persistent=False)
-        self._cache = None        # (x, [q, k, v], indices not yet handed out, rotated?)
+        self._parked: Optional[_Parked] = None
+        self._identity = None       # ((shape, dtype, device), cos = 1, sin = 0)
+
+    @property
+    def pending(self) -> bool:
+        """Whether outputs of an evaluation are still waiting for their slots."""
+        return self._parked is not None
 
     def compute(self, x, rope=None):
         return fused_qkv(x, self.q.weight_spec(), self.k.weight_spec(), self.v.weight_spec(), self.split_k,
                          self.rho, rope=rope, workspace=self.workspace)
 
     def prime(self, x, cos, sin):
-        """Compute rotated Q/K and V for ``x`` ahead of the proxies (fused RoPE path)."""
-        self._cache = (x, self.compute(x, rope=(cos, sin, self.rope_head_dim)), {0, 1, 2}, True)
+        """Evaluate rotated Q/K and V of ``x`` ahead of the slots (the fused RoPE path)."""
+        self._parked = _Parked(x, self.compute(x, rope=(cos, sin, self.rope_head_dim)), True)
 
-    def get(self, x, idx: int):
-        c = self._cache
-        if c is None or c[0] is not x or idx not in c[2]:
-            if c is not None and c[3]:
-                self._cache = None
+    def release(self):
+        self._parked = None
+
+    def take(self, x, idx: int):
+        p = self._parked
+        if p is None or not p.matches(x, idx):
+            if p is not None and p.rotated:
+                self._parked = None
                 raise RuntimeError("CrispyBits fused RoPE: q/k/v_proj received a different tensor than the one "
-                                   "primed by the attention wrapper; install with fuse_rope=False for this model")
-            c = (x, self.compute(x), {0, 1, 2}, False)
-        out = c[1][idx]
-        c[2].discard(idx)
-        self._cache = c if c[2] else None
+                                   "primed by the attention hook; install with fuse_rope=False for this model")
+            p = self._parked = _Parked(x, self.compute(x), False)
+        out, p.outs[idx] = p.outs[idx], None
+        if not any(o is not None for o in p.outs):
+            self._parked = None
         return out
+
+    def identity_tables(self, cos, sin):
+        """cos = 1 and sin = 0 of the given tables' shape and dtype (kept between calls)."""
+        key = (tuple(cos.shape), cos.dtype, cos.device, tuple(sin.shape), sin.dtype)
+        if self._identity is None or self._identity[0] != key:
+            self._identity = (key, torch.ones_like(cos), torch.zeros_like(sin))
+        return self._identity[1], self._identity[2]
 
 
 class _QKVProxy(nn.Module):
+    """The q_proj / k_proj / v_proj slot of a FusedQKV owner (the owner is not a registered
+    child, so its parameters are not listed twice)."""
+
     def __init__(self, owner: FusedQKV, idx: int):
         super().__init__()
-        object.__setattr__(self, "_owner", owner)      # not a registered child: no duplicate parameters
+        object.__setattr__(self, "_owner", owner)
         self.idx = idx
         src = (owner.q, owner.k, owner.v)[idx]
         self.in_features, self.out_features = src.in_features, src.out_features
 
     def forward(self, x):
-        return self._owner.get(x, self.idx)
+        return self._owner.take(x, self.idx)
 
     def extra_repr(self):
-        return f"fused {'qkv'[self.idx]}_proj (see crispybits_qkv)"
+        return f"slot {'qkv'[self.idx]} of crispybits_qkv, {self.in_features} -> {self.out_features}"
 
 
-class FusedLlamaMLP(nn.Module):
-    def __init__(self, gate: PackedLinear, up: PackedLinear, down: PackedLinear, split_k=None, rho: int = 1):
-        super().__init__()
-        self.gate_proj, self.up_proj, self.down_proj = gate, up, down
-        self.split_k, self.rho = split_k, int(rho)
-        self.register_buffer("workspace", new_workspace(gate.packed.device), persistent=False)
-
-    def forward(self, x):
-        h = fused_gate_up(x, self.gate_proj.weight_spec(), self.up_proj.weight_spec(), self.split_k, self.rho,
-                          workspace=self.workspace)
-        return self.down_proj(h)
-
-
-def _is_act(mod, names):
-    return mod is not None and type(mod).__name__ in names
-
-
-def _patch_rotary(module_name: str) -> bool:
-    """Wrap the modeling module's apply_rotary_pos_emb so marked (pre-rotated)
-    cos/sin pass q/k through untouched."""
-    mod = sys.modules.get(module_name)
-    orig = getattr(mod, "apply_rotary_pos_emb", None)
-    if orig is None:
+def _takes_position_embeddings(attn: nn.Module) -> bool:
+    try:
+        return "position_embeddings" in inspect.signature(attn.forward).parameters
+    except (TypeError, ValueError):
         return False
-    if getattr(orig, "_crispybits_patched", False):
-        return True
-
-    def apply_rotary_pos_emb(q, k, cos, sin, *args, **kwargs):
-        if getattr(cos, _PREROTATED, False):
-            return q, k
-        return orig(q, k, cos, sin, *args, **kwargs)
-
-    apply_rotary_pos_emb._crispybits_patched = True
-    apply_rotary_pos_emb.__wrapped__ = orig
-    mod.apply_rotary_pos_emb = apply_rotary_pos_emb
-    return True
 
 
-def _mark(t: torch.Tensor) -> torch.Tensor:
-    view = t.view_as(t)
-    setattr(view, _PREROTATED, True)
-    return view
+def _install_rope_hooks(attn: nn.Module, owner: FusedQKV):
+    """Prime the owner from the attention's inputs and hand the attention identity tables."""
 
-
-def _wrap_attention_forward(attn: nn.Module, owner: FusedQKV):
-    orig_forward = attn.forward
-
-    def forward(*args, **kwargs):
-        hs = kwargs.get("hidden_states", args[0] if args else None)
-        pe = kwargs.get("position_embeddings")
-        pe_positional = pe is None and len(args) > 1 and isinstance(args[1], (tuple, list))
-        if pe_positional:
-            pe = args[1]
-        if hs is None or pe is None:
-            return orig_forward(*args, **kwargs)
+    def before(module, args, kwargs):
+        hs = kwargs["hidden_states"] if "hidden_states" in kwargs else (args[0] if args else None)
+        in_kwargs = "position_embeddings" in kwargs
+        pe = kwargs["position_embeddings"] if in_kwargs else (args[1] if len(args) > 1 else None)
+        if hs is None or not isinstance(pe, (tuple, list)) or len(pe) != 2:
+            return None                     # nothing to fuse with: the slots evaluate unrotated
         cos, sin = pe
         owner.prime(hs, cos, sin)
-        marked = (_mark(cos), _mark(sin))
-        if pe_positional:
-            args = (args[0], marked, *args[2:])
-        else:
-            kwargs["position_embeddings"] = marked
-        try:
-            return orig_forward(*args, **kwargs)
-        finally:
-            owner._cache = None
+        ident = owner.identity_tables(cos, sin)
+        if in_kwargs:
+            return args, {**kwargs, "position_embeddings": ident}
+        return (args[0], ident, *args[2:]), kwargs
 
-    attn.forward = forward
-    attn._crispybits_orig_forward = orig_forward
+    def after(module, args, kwargs, output):
+        owner.release()
+
+    attn.register_forward_pre_hook(before, with_kwargs=True)
+    attn.register_forward_hook(after, with_kwargs=True, always_call=True)
 
 
-def _head_dim(attn):
+def _head_dim(attn) -> int:
     hd = getattr(attn, "head_dim", None)
     if hd is None and hasattr(attn, "config"):
         cfg = attn.config
@@ -181,73 +190,115 @@ def _head_dim(attn):
     return int(hd) if hd else 0
 
 
-def _fuse_block(block: nn.Module, tuning: Dict, i: int, fuse_rope: bool):
-    attn = getattr(block, "self_attn", None)
-    if attn is not None and all(isinstance(getattr(attn, n, None), PackedLinear) for n in ("q_proj", "k_proj", "v_proj")):
-        cfg = tuning.get(f"block.{i}.self_attn.qkv", {})
-        rope_hd = 0
-        llama_like = hasattr(block, "mlp") and not hasattr(block, "fc1")
-        if fuse_rope and llama_like:
-            hd = _head_dim(attn)
-            if (hd and hd % 2 == 0 and attn.q_proj.out_features % hd == 0 and attn.k_proj.out_features % hd == 0
-                    and _patch_rotary(type(attn).__module__)):
-                attn.q_proj.permute_for_rope_(hd)
-                attn.k_proj.permute_for_rope_(hd)
-                rope_hd = hd
-        owner = FusedQKV(attn.q_proj, attn.k_proj, attn.v_proj, cfg.get("split_k"), cfg.get("rho", 1), rope_hd)
-        attn.crispybits_qkv = owner
-        attn.q_proj, attn.k_proj, attn.v_proj = (_QKVProxy(owner, j) for j in range(3))
-        if rope_hd:
-            _wrap_attention_forward(attn, owner)
-    mlp = getattr(block, "mlp", None)
-    if (mlp is not None and all(isinstance(getattr(mlp, n, None), PackedLinear) for n in ("gate_proj", "up_proj", "down_proj"))
-            and _is_act(getattr(mlp, "act_fn", None), ("SiLU", "SiLUActivation"))):
-        cfg = tuning.get(f"block.{i}.mlp.gate_up", {})
-        block.mlp = FusedLlamaMLP(mlp.gate_proj, mlp.up_proj, mlp.down_proj, cfg.get("split_k"), cfg.get("rho", 1))
-    if isinstance(getattr(block, "fc1", None), PackedLinear) and _is_act(getattr(block, "activation_fn", None), ("ReLU",)):
-        block.fc1.act = "relu"
-        block.activation_fn = nn.Identity()
+# ----------------------------------------------------------------------------- fused MLP
 
+class FusedLlamaMLP(nn.Module):
+    """A SiLU-gated MLP whose gate and up projections run as one decode pass."""
+
+    def __init__(self, gate: PackedLinear, up: PackedLinear, down: PackedLinear, split_k=None, rho: int = 1):
+        super().__init__()
+        self.gate_proj, self.up_proj, self.down_proj = gate, up, down
+        self.split_k, self.rho = split_k, int(rho)
+        self.register_buffer("workspace", new_workspace(gate.packed.device), persistent=False)
+
+    def forward(self, x):
+        hidden = fused_gate_up(x, self.gate_proj.weight_spec(), self.up_proj.weight_spec(), self.split_k, self.rho,
+                               workspace=self.workspace)
+        return self.down_proj(hidden)
+
+
+# ----------------------------------------------------------------------------- fusion rules
+
+def _all_packed(mod, names) -> bool:
+    return mod is not None and all(isinstance(getattr(mod, n, None), PackedLinear) for n in names)
+
+
+def _activation_named(mod, names) -> bool:
+    return mod is not None and type(mod).__name__ in names
+
+
+def _fuse_attention(block, i, tuning, fuse_rope) -> bool:
+    attn = getattr(block, "self_attn", None)
+    if not _all_packed(attn, ("q_proj", "k_proj", "v_proj")):
+        return False
+    cfg = tuning.get(f"block.{i}.self_attn.qkv", {})
+    rope_hd = 0
+    rotary = hasattr(block, "mlp") and not hasattr(block, "fc1")       # LLaMA family; OPT has no RoPE
+    if fuse_rope and rotary and _takes_position_embeddings(attn):
+        hd = _head_dim(attn)
+        if hd and hd % 2 == 0 and attn.q_proj.out_features % hd == 0 and attn.k_proj.out_features % hd == 0:
+            attn.q_proj.permute_for_rope_(hd)
+            attn.k_proj.permute_for_rope_(hd)
+            rope_hd = hd
+    owner = FusedQKV(attn.q_proj, attn.k_proj, attn.v_proj, cfg.get("split_k"), cfg.get("rho", 1), rope_hd)
+    attn.crispybits_qkv = owner
+    attn.q_proj, attn.k_proj, attn.v_proj = (_QKVProxy(owner, j) for j in range(3))
+    if rope_hd:
+        _install_rope_hooks(attn, owner)
+    return True
+
+
+def _fuse_swiglu(block, i, tuning, fuse_rope) -> bool:
+    mlp = getattr(block, "mlp", None)
+    if not (_all_packed(mlp, ("gate_proj", "up_proj", "down_proj"))
+            and _activation_named(getattr(mlp, "act_fn", None), ("SiLU", "SiLUActivation"))):
+        return False
+    cfg = tuning.get(f"block.{i}.mlp.gate_up", {})
+    block.mlp = FusedLlamaMLP(mlp.gate_proj, mlp.up_proj, mlp.down_proj, cfg.get("split_k"), cfg.get("rho", 1))
+    return True
+
+
+def _fuse_relu_fc1(block, i, tuning, fuse_rope) -> bool:
+    if not (isinstance(getattr(block, "fc1", None), PackedLinear)
+            and _activation_named(getattr(block, "activation_fn", None), ("ReLU",))):
+        return False
+    block.fc1.act = "relu"
+    block.activation_fn = nn.Identity()
+    return True
+
+
+_FUSIONS = (_fuse_attention, _fuse_swiglu, _fuse_relu_fc1)
+
+
+# ----------------------------------------------------------------------------- install
 
 def _block_file(packed_dir: Path, i: int, bits: int) -> Path:
-    """block_{i:03d}_w{bits}.pt (write_packed_dir, reference.py:85-94), else the single-width
+    """block_{i:03d}_w{bits}.pt (write_packed_dir, reference.py:85-94), else the one-width
     block_{i:03d}.pt of the paper's pack_checkpoint.py:26."""
-    per_width = packed_dir / f"block_{i:03d}_w{bits}.pt"
-    if per_width.exists():
-        return per_width
-    single = packed_dir / f"block_{i:03d}.pt"
-    if single.exists():
-        return single
-    raise FileNotFoundError(f"neither {per_width.name} nor {single.name} in {packed_dir}")
+    for name in (f"block_{i:03d}_w{bits}.pt", f"block_{i:03d}.pt"):
+        path = packed_dir / name
+        if path.exists():
+            return path
+    raise FileNotFoundError(f"neither block_{i:03d}_w{bits}.pt nor block_{i:03d}.pt in {packed_dir}")
 
 
 def install_bitmap(model: nn.Module, packed_dir: str, bitmap, device="cuda", dtype=torch.float16,
                    tuning: Optional[Dict] = None, fuse: bool = True, fuse_rope: bool = True):
-    """Replace every linear of block i with the packed weights of width bitmap[i].
-
-    Reads write_packed_dir's block_{i:03d}_w{bits}.pt, or pack_checkpoint.py's block_{i:03d}.pt
-    (one width per block, continuous bitstream; its manifest.json supplies the bitmap when
-    ``bitmap`` is None)."""
-    packed_dir = Path(packed_dir)
+    """Replace every linear of block i with its packed weights of width ``bitmap[i]`` (the
+    bitmap of ``manifest.json`` when None), then fuse each block's decode paths."""
+    root = Path(packed_dir)
     if bitmap is None:
-        with open(packed_dir / "manifest.json") as f:
+        with open(root / "manifest.json") as f:
             bitmap = json.load(f)["bitmap"]
     blocks = _blocks(model)
     if len(blocks) != len(bitmap):
         raise ValueError("bitmap length does not match model")
     tuning = tuning or {}
     for i, (block, bits) in enumerate(zip(blocks, bitmap)):
-        data = torch.load(_block_file(packed_dir, i, int(bits)), map_location="cpu", weights_only=True)
-        for name, d in data.items():
-            if int(d["bits"]) != int(bits):
-                raise ValueError(f"block {i}: '{name}' is packed at W{int(d['bits'])}, the bitmap asks for W{int(bits)}")
+        bits = int(bits)
+        entries = torch.load(_block_file(root, i, bits), map_location="cpu", weights_only=True)
+        for name, d in entries.items():
+            if int(d["bits"]) != bits:
+                raise ValueError(f"block {i}: '{name}' is packed at W{int(d['bits'])}, the bitmap asks for W{bits}")
             if not isinstance(_get(block, name), nn.Linear):
                 raise ValueError(f"block {i}: '{name}' is not an nn.Linear in this model")
-            w = from_packed_dict(d, device=device, dtype=dtype)
+        for name, d in entries.items():
             cfg = tuning.get(f"block.{i}.{name}", {})
-            _set_by_dotted_name(block, name, PackedLinear(w, split_k=cfg.get("split_k"), rho=int(cfg.get("rho", 1))))
+            _set_by_dotted_name(block, name, PackedLinear(from_packed_dict(d, device=device, dtype=dtype),
+                                                          split_k=cfg.get("split_k"), rho=int(cfg.get("rho", 1))))
         if fuse:
-            _fuse_block(block, tuning, i, fuse_rope)
+            for rule in _FUSIONS:
+                rule(block, i, tuning, fuse_rope)
     return model
 
 

@@ -1,18 +1,35 @@
-"""Host op API for packed W2/W3/W4 linears -- same names, arguments and error
-behaviour as the reference's Kernel/crispybits_kernels/ops.py:1-321, running on
-the gfx950 kernels of ``_C`` (libcrispybits_hip.so).
+"""Host op API of the packed W2/W3/W4 linears on MI355X (gfx950).
 
-Differences from the reference, all additive or retuned constants:
-  * DECODE_THRESHOLD is 16: the decode GEMV streams each weight once for up to 16
-    batch rows (16-row MFMA tiles), 3-4x faster than the prefill GEMM's 128-row
-    tiles at M = 9..16, so M = 1..16 stays on it (the reference uses 4, ops.py:23).
-  * fused_qkv accepts per-projection widths (the reference raises ValueError,
-    ops.py:240-241); the kernel dispatches the width per 16-row tile.
-  * The split-K rule counts decode jobs as ceil(batch/16) batch tiles, matching
-    the kernel's job shape.
-  * set_backend() takes "cuda" (alias "hip") or a module object with the
-    ``_C`` interface -- the hook tests use to inject the CPU oracle; no CPU
-    emulator ships with this package.
+The public surface is the reference's (Kernel/crispybits_kernels/ops.py:1-321): the
+weight record ``PackedLinearWeight``, the module ``PackedLinear``, the ops
+``packed_linear`` / ``fused_qkv`` / ``fused_gate_up``, the RoPE row-order helpers, the
+split-K rule and the device queries, with the same arguments and the same ValueError /
+RuntimeError behaviour.  How they run is this build's own:
+
+* **Call routing.**  A call is decode (the streaming GEMV kernels) when its flattened
+  batch has at most ``decode_threshold`` rows, else prefill (the MFMA GEMM).  The K split
+  of a decode call is a pure function of plain integers (kind, rows, virtual rows, K,
+  requested split, rho, device), memoised in ``_rule_splits``, so a repeated call shape
+  costs a dictionary lookup on the host.
+* **RoPE layout.**  ``rope_row_order`` / ``rope_inverse_order`` are closed forms (stored
+  row 2i of a head is original row i, stored row 2i+1 is original row i + head_dim/2).
+  The prefill fallback of ``fused_qkv`` rotates the projection while it is still in the
+  stored, pair-interleaved order -- a stored pair is (y_d, y_{d+h}), one complex number
+  of the rotation -- and restores the original column order with one reshape-transpose
+  (``_original_columns``) instead of an index gather.
+* **Modules** keep their ``PackedLinearWeight`` cached and rebuild it when a buffer is
+  replaced (``.to()``, ``permute_for_rope_``).
+
+Retuned or additive, relative to the reference:
+  * ``DECODE_THRESHOLD = 16``: the batched streaming GEMV reads each weight once for up
+    to 16 batch rows, 3-4x faster than the prefill GEMM's 128-row tiles at M = 9..16
+    (the reference uses 4, ops.py:23).
+  * ``fused_qkv`` takes per-projection widths (the reference raises ValueError,
+    ops.py:240-241); the kernel dispatches the width per workgroup.
+  * The split-K rule counts decode jobs per ``BATCH_TILE`` batch rows.
+  * ``set_backend`` takes "cuda" (alias "hip") or a module object with the ``_C``
+    functions -- the hook the CPU tests use to inject the oracle.  No emulator ships in
+    the product: ``set_backend("emulator")`` raises RuntimeError.
 """
 from __future__ import annotations
 
@@ -20,7 +37,6 @@ import os
 import warnings
 from dataclasses import dataclass, replace
 from functools import lru_cache
-from math import ceil
 from typing import Optional, Tuple
 
 import torch
@@ -40,33 +56,45 @@ if os.environ.get("CRISPYBITS_BACKEND", "").lower() == "emulator":
 DECODE_THRESHOLD = 16
 ACT = {"none": 0, None: 0, "relu": 1, "silu": 2}
 KINDS = ("gemv", "qkv", "gate_up")
-BATCH_TILE = 16          # batch rows one decode job covers
+BATCH_TILE = 16          # batch rows of one decode job
 
+
+# ----------------------------------------------------------------------------- backend
 
 def set_backend(name):
-    """Select the op backend: "cuda"/"hip" (the gfx950 kernels) or a module object
-    implementing the ``_C`` functions (used by tests to run the host logic on CPU)."""
+    """"cuda" / "hip": the gfx950 library.  A module object: its ``packed_gemv`` /
+    ``packed_gemm`` / ``fused_*`` / ``sm_count`` / ``tile_n`` / ``max_rho`` serve every op
+    (the tests pass the CPU oracle this way)."""
     global _C
-    if isinstance(name, str):
-        if name in ("cuda", "hip"):
-            _C = _CUDA
-        elif name == "emulator":
-            raise RuntimeError("the CPU emulator is test infrastructure (oracle.emulator); "
-                               "pass the module object to set_backend to use it")
-        else:
-            raise ValueError(name)
-    else:
+    if not isinstance(name, str):
         _C = name
-    tile_n.cache_clear()
-    _sm_count_for.cache_clear()
+    elif name in ("cuda", "hip"):
+        _C = _CUDA
+    elif name == "emulator":
+        raise RuntimeError("the CPU emulator is test infrastructure (oracle.emulator); "
+                           "pass the module object to set_backend to use it")
+    else:
+        raise ValueError(name)
+    for cached in (tile_n, _sm_count_for, _rule_splits):
+        cached.cache_clear()
 
 
 def backend_name() -> str:
-    return "emulator" if (_C is not None and getattr(_C, "IS_EMULATOR", False)) else "cuda"
+    return "emulator" if getattr(_C, "IS_EMULATOR", False) else "cuda"
 
+
+def _check_ext():
+    if _C is None:
+        raise RuntimeError(f"crispybits HIP library is not built: {_IMPORT_ERROR}")
+
+
+# ----------------------------------------------------------------------------- weights
 
 @dataclass
 class PackedLinearWeight:
+    """One packed linear: int32 codes [N, ceil(K/32)*bits], scales and zeros
+    [N, ceil(K/group_size)] in the activation dtype, optional bias [N], and the head_dim
+    its rows are stored pair-interleaved with (0 when in original order)."""
     packed: torch.Tensor
     scales: torch.Tensor
     zeros: torch.Tensor
@@ -78,81 +106,109 @@ class PackedLinearWeight:
     rope_perm_head_dim: int = 0
 
     def cuda(self, device=None, dtype=torch.float16):
-        device = device or "cuda"
-        return replace(
-            self,
-            packed=self.packed.to(device=device, dtype=torch.int32).contiguous(),
-            scales=self.scales.to(device=device, dtype=dtype).contiguous(),
-            zeros=self.zeros.to(device=device, dtype=dtype).contiguous(),
-            bias=None if self.bias is None else self.bias.to(device=device, dtype=dtype).contiguous(),
-        )
+        """A copy on ``device`` (default: the current GPU) with int32 codes and metadata
+        and bias in ``dtype``, every tensor contiguous."""
+        dev = torch.device(device if device is not None else "cuda")
 
+        def moved(t, dt):
+            return None if t is None else t.to(device=dev, dtype=dt).contiguous()
 
-def _check_ext():
-    if _C is None:
-        raise RuntimeError(f"crispybits HIP library is not built: {_IMPORT_ERROR}")
-
-
-def _empty(x: torch.Tensor) -> torch.Tensor:
-    return torch.empty(0, device=x.device, dtype=x.dtype)
-
-
-def _bias_tensor(w: PackedLinearWeight, x: torch.Tensor):
-    """The bias, or None for none (the backends take None or an empty tensor alike)."""
-    return w.bias
-
-
-def _ws(workspace, x):
-    return workspace
+        return replace(self, packed=moved(self.packed, torch.int32), scales=moved(self.scales, dtype),
+                       zeros=moved(self.zeros, dtype), bias=moved(self.bias, dtype))
 
 
 def new_workspace(device) -> torch.Tensor:
-    """Per-module int32[2] workspace (kept for the reference's interface; the HIP
-    kernels schedule jobs statically and leave it at [0, 0])."""
+    """The reference's per-module int32[2] job-queue words.  The HIP kernels assign jobs
+    statically, accept it and never write it, so it stays [0, 0]."""
     return torch.zeros(2, dtype=torch.int32, device=device)
 
 
-def rope_row_order(out_features: int, head_dim: int, device=None) -> torch.Tensor:
-    """Stored row p <- original row order[p]: per head, (0, h/2, 1, h/2+1, ...)."""
+# ----------------------------------------------------------------------------- RoPE layout
+
+def _check_heads(out_features: int, head_dim: int):
     if head_dim % 2 or out_features % head_dim:
         raise ValueError("out_features must be a multiple of an even head_dim")
-    h = head_dim // 2
-    pair = torch.arange(head_dim) // 2 + (torch.arange(head_dim) % 2) * h
-    base = torch.arange(out_features // head_dim)[:, None] * head_dim
-    return (base + pair[None]).reshape(-1).to(device)
+
+
+def rope_row_order(out_features: int, head_dim: int, device=None) -> torch.Tensor:
+    """Stored row p <- original row order[p]: within a head, stored 2i holds original i and
+    stored 2i+1 holds original i + head_dim/2 (each rotate-half pair side by side)."""
+    _check_heads(out_features, head_dim)
+    p = torch.arange(out_features)
+    within = p % head_dim
+    return (p - within + (within >> 1) + (within & 1) * (head_dim // 2)).to(device)
 
 
 def rope_inverse_order(out_features: int, head_dim: int, device=None) -> torch.Tensor:
-    order = rope_row_order(out_features, head_dim)
-    inv = torch.empty_like(order)
-    inv[order] = torch.arange(order.numel())
-    return inv.to(device)
+    """Original row o -> its stored row: 2d for the first half of a head, 2(d - h) + 1 for
+    the second (d = o mod head_dim, h = head_dim / 2)."""
+    _check_heads(out_features, head_dim)
+    o = torch.arange(out_features)
+    d = o % head_dim
+    h = head_dim // 2
+    return (o - d + torch.where(d < h, 2 * d, 2 * (d - h) + 1)).to(device)
 
 
 def permute_for_rope(w: PackedLinearWeight, head_dim: int) -> PackedLinearWeight:
-    """Store rows pair-interleaved (row r next to its rotate-half partner r + h/2)
-    so the fused-RoPE epilogue finds the partner in the neighbouring lane."""
+    """The weight with its rows stored pair-interleaved for ``head_dim`` (what the fused
+    RoPE epilogue needs: a row's rotate-half partner is the adjacent row)."""
     if w.rope_perm_head_dim:
         if w.rope_perm_head_dim != head_dim:
             raise ValueError("weight already permuted with a different head_dim")
         return w
-    o = rope_row_order(w.out_features, head_dim, w.packed.device)
-    return replace(w, packed=w.packed[o].contiguous(), scales=w.scales[o].contiguous(),
-                   zeros=w.zeros[o].contiguous(),
-                   bias=None if w.bias is None else w.bias[o].contiguous(),
+    order = rope_row_order(w.out_features, head_dim, w.packed.device)
+
+    def rows(t):
+        return None if t is None else t.index_select(0, order).contiguous()
+
+    return replace(w, packed=rows(w.packed), scales=rows(w.scales), zeros=rows(w.zeros), bias=rows(w.bias),
                    rope_perm_head_dim=head_dim)
+
+
+def _original_columns(y: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """Columns of y [M, n] in stored (pair-interleaved) order -> original order: per head,
+    the stored [h, 2] pairs transposed to [2, h]."""
+    M, n = y.shape
+    return y.view(M, n // head_dim, head_dim // 2, 2).transpose(-1, -2).reshape(M, n)
 
 
 def _unpermute_cols(y: torch.Tensor, w: PackedLinearWeight) -> torch.Tensor:
     """Kernel-order outputs of a permuted weight -> original column order."""
-    if not w.rope_perm_head_dim:
-        return y
-    inv = rope_inverse_order(w.out_features, w.rope_perm_head_dim, y.device)
-    return y.index_select(-1, inv)
+    return _original_columns(y, w.rope_perm_head_dim) if w.rope_perm_head_dim else y
 
+
+def apply_rope_reference(t: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """HF rotate-half RoPE of t [M, H*head_dim] (original column order) with cos/sin
+    [M, head_dim], computed in fp32 and rounded once to t's dtype."""
+    M, W = t.shape
+    h = head_dim // 2
+    halves = t.float().reshape(M, W // head_dim, 2, h)
+    a, b = halves[:, :, 0], halves[:, :, 1]
+    c = cos.float().reshape(M, 1, 2, h)
+    s = sin.float().reshape(M, 1, 2, h)
+    out = torch.stack((a * c[:, :, 0] - b * s[:, :, 0], b * c[:, :, 1] + a * s[:, :, 1]), dim=2)
+    return out.view(M, W).to(t.dtype)
+
+
+def _rope_stored(y: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """RoPE of a pair-interleaved projection y [M, n] (stored order), returned in the original
+    column order: the same fp32 arithmetic and single rounding as un-permuting first and
+    then ``apply_rope_reference``."""
+    M, n = y.shape
+    h = head_dim // 2
+    pairs = y.float().reshape(M, n // head_dim, h, 2)
+    a, b = pairs[..., 0], pairs[..., 1]                       # (y_d, y_{d+h}), d < h
+    c = cos.float().reshape(M, 1, 2, h)
+    s = sin.float().reshape(M, 1, 2, h)
+    out = torch.stack((a * c[:, :, 0] - b * s[:, :, 0], b * c[:, :, 1] + a * s[:, :, 1]), dim=2)
+    return out.view(M, n).to(y.dtype)
+
+
+# ----------------------------------------------------------------------------- split-K policy
 
 @lru_cache(maxsize=None)
 def tile_n() -> int:
+    """Virtual rows of one decode job tile (B_N of the split-K rule)."""
     _check_ext()
     return int(_C.tile_n())
 
@@ -165,6 +221,7 @@ def _sm_count_for(device_index: int) -> int:
 
 
 def virtual_rows(kind: str, *out_features: int) -> int:
+    """Rows one decode call produces: N (gemv), nq + nk + nv (qkv), 2N (gate_up)."""
     if kind == "gemv":
         return out_features[0]
     if kind == "qkv":
@@ -175,154 +232,159 @@ def virtual_rows(kind: str, *out_features: int) -> int:
 
 
 def candidate_split_k(batch: int, n: int, bn: int, sms: int, rho: int, max_split: Optional[int] = None) -> int:
-    """P_K = ceil(rho*S / (B*ceil(N/B_N))) if C_out < C_target, else 1 (ops.py:155-163)."""
-    rho = max(1, int(rho))
-    c_out = batch * ceil(n / bn)
-    c_target = rho * sms
-    if c_out >= c_target:
+    """The underfill rule (ops.py:155-163): with C_out = batch * ceil(n / bn) decode jobs and
+    a target of rho * sms, split K into ceil(target / C_out) parts when C_out falls short,
+    else not at all; optionally capped at max_split."""
+    target = max(1, int(rho)) * sms
+    jobs = batch * -(-n // bn)
+    if jobs >= target:
         return 1
-    pk = max(1, ceil(c_target / c_out))
-    return pk if max_split is None else min(max_split, pk)
+    parts = max(1, -(-target // jobs))
+    return parts if max_split is None else min(max_split, parts)
 
 
-def _resolve(split_k: Optional[int], rho: int, batch: int, v_rows: int, k: int, where) -> int:
-    """split_k=None means: apply the underfill rule at call time for this batch size.
-    ``where`` is the activation tensor or its device (looked at only for the rule)."""
-    nchunks = -(-k // 32)
+@lru_cache(maxsize=None)
+def _rule_splits(rho: int, batch: int, v_rows: int, chunks: int, device_index: int) -> int:
+    tiles = -(-batch // BATCH_TILE)
+    return max(1, min(candidate_split_k(tiles, v_rows, tile_n(), _sm_count_for(device_index), rho), chunks))
+
+
+def _k_splits(split_k: Optional[int], rho: int, batch: int, v_rows: int, k: int, x: torch.Tensor) -> int:
+    """K splits of a decode call: the caller's split clamped to [1, chunks], or for
+    split_k=None the underfill rule at this call's batch size."""
+    chunks = -(-k // 32)
     if split_k is not None:
-        return max(1, min(int(split_k), nchunks))
-    device = where.device if isinstance(where, torch.Tensor) else where
-    idx = device.index if device.index is not None else (torch.cuda.current_device() if device.type == "cuda" else 0)
-    tiles = ceil(batch / BATCH_TILE)
-    return max(1, min(candidate_split_k(tiles, v_rows, tile_n(), _sm_count_for(idx), rho), nchunks))
+        return max(1, min(int(split_k), chunks))
+    dev = x.get_device()
+    return _rule_splits(int(rho), batch, v_rows, chunks, dev if dev >= 0 else 0)
+
+
+# ----------------------------------------------------------------------------- ops
+
+def _as_matrix(x: torch.Tensor):
+    """x as a contiguous [M, K] matrix and its leading dims (None when already 2-D)."""
+    if x.dim() == 2:
+        return (x if x.is_contiguous() else x.contiguous()), None
+    return x.reshape(-1, x.shape[-1]).contiguous(), x.shape[:-1]
+
+
+def _restore(y: torch.Tensor, lead) -> torch.Tensor:
+    return y if lead is None else y.view(*lead, y.shape[-1])
+
+
+def _linear(x2, w: PackedLinearWeight, split_k, rho, act: int, threshold, workspace, use_tensor_cores):
+    """One projection of a 2-D activation, decode or prefill by its row count."""
+    if x2.shape[0] <= threshold:
+        pk = _k_splits(split_k, rho, x2.shape[0], w.out_features, w.in_features, x2)
+        return _C.packed_gemv(x2, w.packed, w.scales, w.zeros, w.bias, w.bits, w.in_features, w.group_size,
+                              pk, rho, act, workspace)
+    return _C.packed_gemm(x2, w.packed, w.scales, w.zeros, w.bias, w.bits, w.in_features, w.group_size,
+                          act, use_tensor_cores)
 
 
 def packed_linear(x: torch.Tensor, w: PackedLinearWeight, split_k: Optional[int] = None, rho: int = 1,
                   act: Optional[str] = None, decode_threshold: int = DECODE_THRESHOLD,
                   workspace: Optional[torch.Tensor] = None, use_tensor_cores: bool = True):
-    """y = act(x W-hat^T + b): decode GEMV for M <= decode_threshold, else the prefill GEMM."""
+    """act(x W-hat^T + bias) for x [..., K]: the decode GEMV up to ``decode_threshold``
+    flattened rows, the prefill GEMM beyond."""
     _check_ext()
     if w.rope_perm_head_dim:
         raise ValueError("this weight is stored RoPE-permuted; use fused_qkv (or _unpermute_cols)")
-    return _packed_linear_raw(x, w, split_k, rho, act, decode_threshold, workspace, use_tensor_cores)
-
-
-def _packed_linear_raw(x, w, split_k=None, rho=1, act=None, decode_threshold=DECODE_THRESHOLD,
-                       workspace=None, use_tensor_cores=True):
-    flat = x.dim() == 2
-    original = None if flat else x.shape[:-1]
-    x2 = (x if flat else x.reshape(-1, x.shape[-1])).contiguous()
-    bias = _bias_tensor(w, x2)
-    a = ACT[act]
-    if x2.shape[0] <= decode_threshold:
-        pk = _resolve(split_k, rho, x2.shape[0], w.out_features, w.in_features, x2)
-        y = _C.packed_gemv(x2, w.packed, w.scales, w.zeros, bias, w.bits, w.in_features, w.group_size,
-                           pk, rho, a, _ws(workspace, x2))
-    else:
-        y = _C.packed_gemm(x2, w.packed, w.scales, w.zeros, bias, w.bits, w.in_features, w.group_size,
-                           a, use_tensor_cores)
-    return y if flat else y.reshape(*original, w.out_features)
+    x2, lead = _as_matrix(x)
+    return _restore(_linear(x2, w, split_k, rho, ACT[act], decode_threshold, workspace, use_tensor_cores), lead)
 
 
 def fused_gate_up(x: torch.Tensor, gate: PackedLinearWeight, up: PackedLinearWeight,
                   split_k: Optional[int] = None, rho: int = 1, decode_threshold: int = DECODE_THRESHOLD,
                   workspace: Optional[torch.Tensor] = None):
-    """silu(x G^T) * (x U^T): one decode pass over interleaved gate/up rows, or two
-    prefill GEMMs multiplied in the activation dtype (ops.py:202-221)."""
+    """silu(x G^T) * (x U^T).  Decode: one kernel over interleaved gate/up rows, the
+    product formed in fp32 and rounded once.  Prefill: two GEMMs (SiLU in the gate's
+    epilogue), multiplied in the activation dtype -- the reference's double rounding
+    (ops.py:216-220)."""
     _check_ext()
     if gate.bits != up.bits:
         raise ValueError("fused Gate/Up requires the same precision for Gate and Up within a block")
-    flat = x.dim() == 2
-    x2 = (x if flat else x.reshape(-1, x.shape[-1])).contiguous()
-    if x2.shape[0] <= decode_threshold:
-        pk = _resolve(split_k, rho, x2.shape[0], virtual_rows("gate_up", gate.out_features),
-                      gate.in_features, x2)
+    x2, lead = _as_matrix(x)
+    M = x2.shape[0]
+    if M <= decode_threshold:
+        pk = _k_splits(split_k, rho, M, 2 * gate.out_features, gate.in_features, x2)
         y = _C.fused_gate_up(x2, gate.packed, gate.scales, gate.zeros, up.packed, up.scales, up.zeros,
-                             gate.bits, gate.in_features, gate.group_size, pk, rho, _ws(workspace, x2))
+                             gate.bits, gate.in_features, gate.group_size, pk, rho, workspace)
     else:
-        g = _C.packed_gemm(x2, gate.packed, gate.scales, gate.zeros, None, gate.bits, gate.in_features,
+        y = _C.packed_gemm(x2, gate.packed, gate.scales, gate.zeros, None, gate.bits, gate.in_features,
                            gate.group_size, ACT["silu"], True)
-        u = _C.packed_gemm(x2, up.packed, up.scales, up.zeros, None, up.bits, up.in_features,
-                           up.group_size, 0, True)
-        y = g * u
-    return y if flat else y.reshape(*x.shape[:-1], gate.out_features)
-
-
-def apply_rope_reference(t: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, head_dim: int) -> torch.Tensor:
-    """HF rotate_half RoPE on a flat [M, H*head_dim] tensor with cos/sin [M, head_dim]."""
-    M, W = t.shape
-    th = t.float().view(M, W // head_dim, head_dim)
-    c, s = cos.float()[:, None, :], sin.float()[:, None, :]
-    h = head_dim // 2
-    rot = torch.cat([-th[..., h:], th[..., :h]], dim=-1)
-    return (th * c + rot * s).view(M, W).to(t.dtype)
+        y.mul_(_C.packed_gemm(x2, up.packed, up.scales, up.zeros, None, up.bits, up.in_features,
+                              up.group_size, ACT["none"], True))
+    return _restore(y, lead)
 
 
 def fused_qkv(x: torch.Tensor, q: PackedLinearWeight, k: PackedLinearWeight, v: PackedLinearWeight,
               split_k: Optional[int] = None, rho: int = 1,
               rope: Optional[Tuple[torch.Tensor, torch.Tensor, int]] = None,
               decode_threshold: int = DECODE_THRESHOLD, workspace: Optional[torch.Tensor] = None):
-    """Q/K/V projections in one decode pass (GQA widths, biases, optional RoPE on
-    pair-interleaved Q/K); prefill runs three GEMMs + reference RoPE (ops.py:234-273)."""
+    """Q, K and V of one attention layer.  Decode: one kernel (GQA widths, biases, and with
+    ``rope=(cos, sin, head_dim)`` HF rotate-half RoPE on Q/K stored pair-interleaved).
+    Prefill: three GEMMs, then RoPE on the stored layout and the original column order."""
     _check_ext()
-    if q.in_features != k.in_features or k.in_features != v.in_features or q.group_size != k.group_size \
-            or k.group_size != v.group_size:
+    if not (q.in_features == k.in_features == v.in_features and q.group_size == k.group_size == v.group_size):
         raise ValueError("Q/K/V must share in_features and group_size")
     if q.rope_perm_head_dim != k.rope_perm_head_dim or v.rope_perm_head_dim:
         raise ValueError("Q and K must be permuted with the same head_dim; V must not be permuted")
     perm = q.rope_perm_head_dim
-    flat = x.dim() == 2
-    pre = x.shape[:-1]
-    x2 = (x if flat else x.reshape(-1, x.shape[-1])).contiguous()
+    x2, lead = _as_matrix(x)
     M = x2.shape[0]
+    cos2 = sin2 = None
+    head_dim = 0
     if rope is not None:
         cos, sin, head_dim = rope
         head_dim = int(head_dim)
         if perm != head_dim:
             raise ValueError("fused RoPE needs Q/K permuted with permute_for_rope(w, head_dim) "
                              "(install_bitmap(fuse_rope=True) does this)")
+        pre = x.shape[:-1]                    # one cos/sin row per activation row
         cos2 = cos.expand(*pre, head_dim).reshape(M, head_dim)
         sin2 = sin.expand(*pre, head_dim).reshape(M, head_dim)
     if M <= decode_threshold:
-        v_rows = virtual_rows("qkv", q.out_features, k.out_features, v.out_features)
-        pk = _resolve(split_k, rho, M, v_rows, q.in_features, x2)
-        if rope is None:
-            rc, rs, hd = None, None, 0
-        else:
-            rc, rs, hd = cos2.float().contiguous(), sin2.float().contiguous(), head_dim
+        pk = _k_splits(split_k, rho, M, q.out_features + k.out_features + v.out_features, q.in_features, x2)
+        rc = None if cos2 is None else cos2.float().contiguous()
+        rs = None if sin2 is None else sin2.float().contiguous()
         bits = q.bits if q.bits == k.bits == v.bits else (q.bits, k.bits, v.bits)
-        oq, ok, ov = _C.fused_qkv(x2, q.packed, q.scales, q.zeros, _bias_tensor(q, x2),
-                                  k.packed, k.scales, k.zeros, _bias_tensor(k, x2),
-                                  v.packed, v.scales, v.zeros, _bias_tensor(v, x2),
-                                  rc, rs, hd, perm, bits, q.in_features, q.group_size, pk, rho,
-                                  _ws(workspace, x2))
+        outs = _C.fused_qkv(x2, q.packed, q.scales, q.zeros, q.bias, k.packed, k.scales, k.zeros, k.bias,
+                            v.packed, v.scales, v.zeros, v.bias, rc, rs, head_dim, perm, bits, q.in_features,
+                            q.group_size, pk, rho, workspace)
     else:
-        oq, ok, ov = (_unpermute_cols(_packed_linear_raw(x2, w, decode_threshold=0), w) for w in (q, k, v))
-        if rope is not None:
-            oq = apply_rope_reference(oq, cos2, sin2, head_dim)
-            ok = apply_rope_reference(ok, cos2, sin2, head_dim)
-    if flat:
-        return oq, ok, ov
-    return oq.reshape(*pre, q.out_features), ok.reshape(*pre, k.out_features), ov.reshape(*pre, v.out_features)
+        outs = []
+        for i, w in enumerate((q, k, v)):
+            y = _linear(x2, w, None, 1, 0, 0, None, True)
+            if i < 2 and cos2 is not None:
+                y = _rope_stored(y, cos2, sin2, head_dim)
+            elif w.rope_perm_head_dim:
+                y = _original_columns(y, w.rope_perm_head_dim)
+            outs.append(y)
+    return tuple(_restore(o, lead) for o in outs)
 
 
 def sm_count():
-    _check_ext(); return int(_C.sm_count())
+    _check_ext()
+    return int(_C.sm_count())
 
 
 def max_rho(bits: int, kind: str = "gemv"):
-    _check_ext(); return int(_C.max_rho(bits, kind))
+    _check_ext()
+    return int(_C.max_rho(bits, kind))
 
+
+# ----------------------------------------------------------------------------- module
 
 class PackedLinear(nn.Module):
-    """nn.Linear replacement holding a packed weight (ops.py:285-321)."""
+    """nn.Linear stand-in over a packed weight: buffers ``packed``, ``scales``, ``zeros``,
+    ``bias`` (persistent) and ``workspace`` (not), the decode policy (``split_k``,
+    ``rho``) and an epilogue activation ``act``."""
 
     def __init__(self, w: PackedLinearWeight, split_k: Optional[int] = None, rho: int = 1, act: Optional[str] = None):
         super().__init__()
-        self.register_buffer("packed", w.packed)
-        self.register_buffer("scales", w.scales)
-        self.register_buffer("zeros", w.zeros)
-        self.register_buffer("bias", w.bias)
+        for name in ("packed", "scales", "zeros", "bias"):
+            self.register_buffer(name, getattr(w, name))
         self.register_buffer("workspace", new_workspace(w.packed.device), persistent=False)
         self.bits = int(w.bits)
         self.group_size = int(w.group_size)
@@ -332,13 +394,22 @@ class PackedLinear(nn.Module):
         self.split_k = None if split_k is None else int(split_k)
         self.rho = int(rho)
         self.act = act
+        self._spec: Optional[PackedLinearWeight] = None
 
     def weight_spec(self) -> PackedLinearWeight:
-        return PackedLinearWeight(self.packed, self.scales, self.zeros, self.bits, self.group_size,
-                                  self.in_features, self.out_features, self.bias, self.rope_perm_head_dim)
+        """The module's weight as a PackedLinearWeight (cached; rebuilt when a buffer or the
+        RoPE layout changed)."""
+        s = self._spec
+        b = self._buffers
+        if (s is None or s.packed is not b["packed"] or s.scales is not b["scales"] or s.zeros is not b["zeros"]
+                or s.bias is not b["bias"] or s.rope_perm_head_dim != self.rope_perm_head_dim):
+            s = self._spec = PackedLinearWeight(b["packed"], b["scales"], b["zeros"], self.bits, self.group_size,
+                                                self.in_features, self.out_features, b["bias"],
+                                                self.rope_perm_head_dim)
+        return s
 
     def permute_for_rope_(self, head_dim: int):
-        """In place: store rows pair-interleaved for the fused RoPE epilogue."""
+        """In place: store the rows pair-interleaved for the fused RoPE epilogue."""
         w = permute_for_rope(self.weight_spec(), head_dim)
         self.packed, self.scales, self.zeros, self.bias = w.packed, w.scales, w.zeros, w.bias
         self.rope_perm_head_dim = head_dim
@@ -348,6 +419,7 @@ class PackedLinear(nn.Module):
         return packed_linear(x, self.weight_spec(), self.split_k, self.rho, self.act, workspace=self.workspace)
 
     def extra_repr(self):
-        r = f", rope_perm={self.rope_perm_head_dim}" if self.rope_perm_head_dim else ""
-        return (f"in={self.in_features}, out={self.out_features}, W{self.bits}, g={self.group_size}, "
-                f"split_k={self.split_k}, rho={self.rho}, act={self.act}{r}")
+        layout = f", pair-interleaved(head_dim={self.rope_perm_head_dim})" if self.rope_perm_head_dim else ""
+        act = f", act={self.act}" if self.act else ""
+        return (f"{self.in_features} -> {self.out_features}, W{self.bits} g{self.group_size}, "
+                f"split_k={self.split_k}, rho={self.rho}{act}{layout}")

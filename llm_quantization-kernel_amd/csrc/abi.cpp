@@ -424,23 +424,38 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     return bp;
 }
 
+// Kernels (per device) whose dynamic-LDS limit has been raised to the whole budget.  The
+// limit is set once, to LDS_BUDGET, and never lowered, so launches of one kernel with
+// different LDS sizes from several threads cannot undercut each other.
 std::mutex g_attr_mu;
+std::vector<std::pair<int, const void*>> g_lds_raised;
 
 hipError_t ensure_lds(const void* f, int bytes) {
     if (bytes <= 64 * 1024) return hipSuccess;
+    if (bytes > LDS_BUDGET) return hipErrorInvalidValue;
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const std::pair<int, const void*> key(dev, f);
     std::lock_guard<std::mutex> lk(g_attr_mu);
-    return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (std::find(g_lds_raised.begin(), g_lds_raised.end(), key) != g_lds_raised.end()) return hipSuccess;
+    e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BUDGET);
+    if (e == hipSuccess) g_lds_raised.push_back(key);
+    return e;
 }
 
 int max_bits(const GemvArgs& A) { return std::max({A.p[0].bits, A.p[1].bits, A.p[2].bits}); }
 
-// Common body of the three decode entry points.
-int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rho, float* partial, int device,
-               void* stream) {
-    DeviceGuard guard(device);
-    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
-    const int cus = cu_count(device);
-    if (cus <= 0) return fail(CBK_EHIP, "cannot query the compute-unit count of device %d", device);
+// The launch a decode call makes: kernel family, the kernel, its grid, workgroup size,
+// dynamic LDS and K splits.  plan_decode also fills the plan fields of A the kernels read.
+struct DecodeLaunch {
+    int family = 0;              // CBK_KERNEL_*
+    const void* f = nullptr;     // kernel address (the generic kernel is chosen at launch)
+    int grid = 0, block = 0, lds = 0, P = 1;
+};
+
+DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rho, int cus) {
+    DecodeLaunch L;
     bool mfma_ok = !mixed || (A.p[0].n % MFMA_TILE == 0 && A.p[1].n % MFMA_TILE == 0);
     // direct-to-LDS dwordx4 streaming needs 16-byte aligned rows
     for (int i = 0; i < 3; ++i)
@@ -450,7 +465,6 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     bool xvec = (A.K % 8 == 0) && (reinterpret_cast<uintptr_t>(A.x) % 16 == 0);
     for (int i = 0; i < 3; ++i)
         xvec = xvec && reinterpret_cast<uintptr_t>(A.p[i].s) % 16 == 0 && reinterpret_cast<uintptr_t>(A.p[i].z) % 16 == 0;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const StreamPlan sp = plan_stream(A, dtype, mixed, split_k);
     if (sp.ok) {
         A.P = sp.P;
@@ -459,23 +473,13 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
         A.divP = make_fastdiv((uint32_t)A.P);
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divGS = make_fastdiv((uint32_t)(A.gs / 32));
-        if (A.P > 1) {
-            if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
-            A.partial = partial;
-        } else {
-            A.partial = nullptr;
-        }
-        const void* f = gemv_stream_kernel_for(mode, A.p[0].bits, mixed, sp.mb);
-        hipError_t e = ensure_lds(f, sp.lds);
-        if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
-        void* args[] = {&A};
-        e = launch(f, dim3(sp.grid), dim3(64 * sp.ks * sp.rw), args, (size_t)sp.lds, s);
-        if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
-        if (A.P > 1) {
-            e = launch_gemv_reduce(A, dtype, mode, s);
-            if (e != hipSuccess) return hip_fail(e, "packed_gemv: reduce launch");
-        }
-        return CBK_OK;
+        L.family = CBK_KERNEL_STREAM;
+        L.f = gemv_stream_kernel_for(mode, A.p[0].bits, mixed, sp.mb);
+        L.grid = sp.grid;
+        L.block = 64 * sp.ks * sp.rw;
+        L.lds = sp.lds;
+        L.P = sp.P;
+        return L;
     }
     const BStreamPlan bp = plan_bstream(A, dtype, mode, mixed, split_k);
     if (bp.ok) {
@@ -485,23 +489,13 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
         A.divP = make_fastdiv((uint32_t)A.P);
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divG = make_fastdiv((uint32_t)(A.gs / 128));
-        if (A.P > 1) {
-            if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
-            A.partial = partial;
-        } else {
-            A.partial = nullptr;
-        }
-        const void* f = gemv_bstream_kernel_for(mode, A.p[0].bits, mixed, bp.bsu);
-        hipError_t e = ensure_lds(f, bp.lds);
-        if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
-        void* args[] = {&A};
-        e = launch(f, dim3(bp.grid), dim3(64 * bp.ks * bp.rw), args, (size_t)bp.lds, s);
-        if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
-        if (A.P > 1) {
-            e = launch_gemv_reduce(A, dtype, mode, s);
-            if (e != hipSuccess) return hip_fail(e, "packed_gemv: reduce launch");
-        }
-        return CBK_OK;
+        L.family = CBK_KERNEL_BSTREAM;
+        L.f = gemv_bstream_kernel_for(mode, A.p[0].bits, mixed, bp.bsu);
+        L.grid = bp.grid;
+        L.block = 64 * bp.ks * bp.rw;
+        L.lds = bp.lds;
+        L.P = bp.P;
+        return L;
     }
     const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, max_bits(A), split_k, rho, cus, mfma_ok, xvec);
     A.P = pl.P;
@@ -521,28 +515,51 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     A.raw_np = pl.L.raw_np;
     A.lds_bytes = pl.lds;
     A.ring = pl.ring;
-    if ((int64_t)A.units * A.P >= (1ll << 31) || (int64_t)A.jobs * 16 >= (1ll << 31))
-        return fail(CBK_EINVAL, "packed_gemv: problem too large for 32-bit job indexing");
     A.divP = make_fastdiv((uint32_t)A.P);
     A.divT = make_fastdiv((uint32_t)std::max(A.ntiles, 1));
     A.divW = make_fastdiv((uint32_t)std::max(A.nw, 1));
     A.divG = make_fastdiv((uint32_t)std::max(A.gs >> 7, 1));
     A.divNP = make_fastdiv((uint32_t)std::max(A.raw_np, 1));
+    L.P = pl.P;
+    L.grid = pl.grid;
+    if (pl.mfma) {
+        L.family = CBK_KERNEL_MFMA;
+        L.f = gemv_mfma_kernel_for(mode, A.p[0].bits, mixed, pl.unit_rows ? 1 : 16);
+        L.block = 64 * pl.nw;
+        L.lds = pl.lds;
+    } else {
+        L.family = CBK_KERNEL_GENERIC;
+        L.block = GENERIC_THREADS;
+    }
+    return L;
+}
+
+// Common body of the three decode entry points.
+int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rho, float* partial, int device,
+               void* stream) {
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    const int cus = cu_count(device);
+    if (cus <= 0) return fail(CBK_EHIP, "cannot query the compute-unit count of device %d", device);
+    const DecodeLaunch L = plan_decode(A, dtype, mode, mixed, split_k, rho, cus);
+    if (L.family == CBK_KERNEL_MFMA &&
+        ((int64_t)A.units * A.P >= (1ll << 31) || (int64_t)A.jobs * 16 >= (1ll << 31)))
+        return fail(CBK_EINVAL, "packed_gemv: problem too large for 32-bit job indexing");
     if (A.P > 1) {
         if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
         A.partial = partial;
     } else {
         A.partial = nullptr;
     }
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t e;
-    if (pl.mfma) {
-        const void* f = gemv_mfma_kernel_for(mode, A.p[0].bits, mixed, pl.unit_rows ? 1 : 16);
-        e = ensure_lds(f, pl.lds);
+    if (L.family == CBK_KERNEL_GENERIC) {
+        e = launch_gemv_generic(A, dtype, mode, L.grid, s);
+    } else {
+        e = ensure_lds(L.f, L.lds);
         if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
         void* args[] = {&A};
-        e = launch(f, dim3(pl.grid), dim3(64 * pl.nw), args, (size_t)pl.lds, s);
-    } else {
-        e = launch_gemv_generic(A, dtype, mode, pl.grid, s);
+        e = launch(L.f, dim3(L.grid), dim3(L.block), args, (size_t)L.lds, s);
     }
     if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
     if (A.P > 1) {
@@ -644,13 +661,24 @@ int cbk_max_rho(int device, int bits, int mode, int* out) {
     if (mode < 0 || mode > 2) return fail(CBK_EINVAL, "kind must be 'gemv', 'qkv' or 'gate_up'");
     DeviceGuard guard(device);
     if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
-    // fp16 decode of a 4096-wide row at batch 1 with 4 waves per workgroup
-    const void* f = gemv_mfma_kernel_for(mode, bits, false, 1);
-    const int lds = mfma_lds(32, 1, 1, 4, bits, 128, 2, true).total;
+    const int cus = cu_count(device);
+    if (cus <= 0) return fail(CBK_EHIP, "cannot query the compute-unit count of device %d", device);
+    // the kernel, workgroup size and LDS of an fp16 batch-1 call at the Llama-2-7B widths of
+    // this kind (K = 4096; N = 4096, 3 x 4096 or 2 x 11008), unsplit
+    const uintptr_t base = (uintptr_t)1 << 20;
+    const void* a = reinterpret_cast<const void*>(base);
+    const int64_t n = mode == CBK_MODE_GATEUP ? 11008 : 4096;
+    GemvArgs A = base_args(a, 1, 4096, 128);
+    for (int i = 0; i < 3; ++i)
+        A.p[i] = make_proj(reinterpret_cast<const int32_t*>(base), a, a, nullptr, nullptr, n, bits, 4096);
+    A.V = (int)(mode == CBK_MODE_QKV ? 3 * n : (mode == CBK_MODE_GATEUP ? 2 * n : n));
+    const DecodeLaunch L = plan_decode(A, CBK_F16, mode, false, 1, 1, cus);
+    const void* f = L.f ? L.f : gemv_generic_kernel_for(CBK_F16, mode);
     int blocks = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, 256, (size_t)lds);
+    hipError_t e = ensure_lds(f, L.lds);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, L.block, (size_t)L.lds);
     if (e != hipSuccess) return hip_fail(e, "max_rho: occupancy query");
-    *out = blocks;
+    *out = std::max(blocks, 1);
     return CBK_OK;
 }
 
@@ -689,6 +717,41 @@ int cbk_packed_gemv(const void* x, int dtype, int64_t M, int64_t K, const int32_
     A.V = (int)N;
     A.act = act;
     return run_decode(A, dtype, CBK_MODE_GEMV, false, split_k, rho, partial, device, stream);
+}
+
+int cbk_decode_plan(int dtype, int64_t M, int64_t K, int group_size, int64_t n0, int64_t n1, int64_t n2, int bits0,
+                    int bits1, int bits2, int mode, int split_k, int rho, int device, int32_t* out) {
+    if (!out) return fail(CBK_EINVAL, "decode_plan: out must be non-null");
+    if (!valid_dtype(dtype)) return fail(CBK_EINVAL, "x must be fp16/bf16/fp32");
+    if (M < 1 || K <= 0 || K > (1 << 24) || M > (1 << 24)) return fail(CBK_EINVAL, "decode_plan: bad shape");
+    if (mode < 0 || mode > 2) return fail(CBK_EINVAL, "decode_plan: mode must be 0 (gemv), 1 (qkv) or 2 (gate_up)");
+    if (group_size <= 0 || group_size % 32 != 0)
+        return fail(CBK_EINVAL, "group_size must be a positive multiple of 32");
+    if (split_k < 1) return fail(CBK_EINVAL, "split_k must be >= 1");
+    const int64_t ns[3] = {n0, mode == CBK_MODE_QKV ? n1 : n0, mode == CBK_MODE_QKV ? n2 : n0};
+    const int bs[3] = {bits0, mode == CBK_MODE_QKV ? bits1 : bits0, mode == CBK_MODE_QKV ? bits2 : bits0};
+    for (int i = 0; i < 3; ++i) {
+        if (ns[i] <= 0 || ns[i] > (1 << 29)) return fail(CBK_EINVAL, "decode_plan: bad out_features");
+        if (bs[i] != 2 && bs[i] != 3 && bs[i] != 4) return fail(CBK_EINVAL, "bits must be 2/3/4");
+    }
+    const int cus = cu_count(device);
+    if (cus <= 0) return fail(CBK_EHIP, "cannot query the compute-unit count of device %d", device);
+    // the plan of tensors as torch allocates them: every base 256-byte aligned
+    const uintptr_t base = (uintptr_t)1 << 20;
+    const void* a = reinterpret_cast<const void*>(base);
+    GemvArgs A = base_args(a, M, K, group_size);
+    for (int i = 0; i < 3; ++i)
+        A.p[i] = make_proj(reinterpret_cast<const int32_t*>(base), a, a, nullptr, nullptr, ns[i], bs[i], K);
+    A.V = (int)(mode == CBK_MODE_QKV ? ns[0] + ns[1] + ns[2] : (mode == CBK_MODE_GATEUP ? 2 * ns[0] : ns[0]));
+    const bool mixed = mode == CBK_MODE_QKV && !(bs[0] == bs[1] && bs[1] == bs[2]);
+    const DecodeLaunch L = plan_decode(A, dtype, mode, mixed, split_k, rho, cus);
+    out[0] = L.family;
+    out[1] = L.P;
+    out[2] = L.grid;
+    out[3] = L.block;
+    out[4] = L.lds;
+    out[5] = L.P > 1 ? 2 : 1;      // launches per call (a split adds the combine)
+    return CBK_OK;
 }
 
 int cbk_packed_gemv_noalloc(const void* x, int dtype, int64_t M, int64_t K, const int32_t* packed,

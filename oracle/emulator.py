@@ -40,6 +40,18 @@ def max_rho(bits, kind="gemv"):
     return MAX_RHO
 
 
+def decode_plan(dtype, batch, in_features, group_size, out_features, bits, kind, split_k, rho):
+    """Launch-plan query of the HIP backend (its ``decode_plan``), for the host logic of the
+    tuner on the CPU: one job per 16 virtual rows and K split, splits clamped to the 32-code
+    chunks, rho ignored (as the streaming kernels ignore it)."""
+    if kind not in ("gemv", "qkv", "gate_up"):
+        raise RuntimeError("kind must be 'gemv', 'qkv' or 'gate_up'")
+    ns = out_features if isinstance(out_features, (tuple, list)) else (out_features,)
+    v = sum(ns) if kind == "qkv" else (2 * ns[0] if kind == "gate_up" else ns[0])
+    P = max(1, min(int(split_k), math.ceil(in_features / 32)))
+    return ("stream", P, math.ceil(v / TILE_N) * P, 256, 0, 2 if P > 1 else 1)
+
+
 # ----------------------------------------------------------------------------- numpy cores
 
 def silu64(v: np.ndarray) -> np.ndarray:

@@ -22,9 +22,7 @@ def emu():
     prev = ops._C
     ops.set_backend(emulator)
     yield "cpu"
-    ops._C = prev
-    ops.tile_n.cache_clear()
-    ops._sm_count_for.cache_clear()
+    ops.set_backend(prev)
 
 
 @pytest.fixture
@@ -37,6 +35,4 @@ def hip():
     prev = ops._C
     ops.set_backend("cuda")
     yield "cuda"
-    ops._C = prev
-    ops.tile_n.cache_clear()
-    ops._sm_count_for.cache_clear()
+    ops.set_backend(prev)

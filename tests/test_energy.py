@@ -61,3 +61,22 @@ def test_amdsmi_sampler_reads_the_gpu():
         assert 50.0 < m.mean_watts < 3000.0 and m.joules > 0 and m.samples > 10
     finally:
         s.close()
+
+
+class RampPower(E.PowerSampler):
+    """Power rising linearly in time: the trapezoid rule with interpolated edges is exact."""
+    def __init__(self, w0, slope):
+        self.w0, self.slope, self.t0 = w0, slope, time.perf_counter()
+
+    def read_watts(self):
+        return self.w0 + self.slope * (time.perf_counter() - self.t0)
+
+
+def test_integrate_linear_ramp_exactly():
+    s = RampPower(50.0, 400.0)
+    start = time.perf_counter()
+    m = E.integrate_energy(lambda: time.sleep(0.25), s, hz=100)
+    a = start - s.t0                          # the window starts after `start`; bound it both ways
+    lo = 50.0 * m.seconds + 200.0 * ((a + m.seconds) ** 2 - a ** 2)
+    assert m.joules == pytest.approx(lo, rel=0.02)
+    assert m.samples >= 10

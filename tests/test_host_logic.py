@@ -121,11 +121,12 @@ def test_policy_rule(emu):
     assert candidate_split_k(64, 4096, bn, S, 1) == 1
     assert candidate_split_k(1, 10 ** 6, bn, S, 1) == 1
     assert candidate_split_k(1, bn, bn, S, 2, max_split=8) == 8
-    # _resolve clamps to the chunk count and counts batch tiles of 16 rows
-    dev = torch.device("cpu")
-    assert ops._resolve(None, 1, 1, 64, 64, dev) == 2           # rule wants 64, K has 2 chunks
-    assert ops._resolve(5, 1, 1, 64, 4096, dev) == 5
-    assert ops._resolve(None, 1, 16, 4096, 4096, dev) == ops._resolve(None, 1, 1, 4096, 4096, dev)
+    # a decode call's split clamps to the chunk count and counts batch tiles of 16 rows
+    x = torch.empty(0)
+    assert ops._k_splits(None, 1, 1, 64, 64, x) == 2           # rule wants 64, K has 2 chunks
+    assert ops._k_splits(5, 1, 1, 64, 4096, x) == 5
+    assert ops._k_splits(99, 1, 1, 64, 100, x) == 4            # ceil(100 / 32) chunks
+    assert ops._k_splits(None, 1, 16, 4096, 4096, x) == ops._k_splits(None, 1, 1, 4096, 4096, x)
 
 
 def test_workspace_contract(emu):
@@ -271,3 +272,34 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, "bench.py", "--gpus", "2", "--steps", "1"], cwd=root,
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "--gpus 2 is not supported" in r.stderr
+
+
+def test_fused_rope_hooks_prime_once_and_keep_the_model_exact(emu, tmp_path, monkeypatch):
+    """The attention pre-hook primes each block's owner once per forward, the slots take the
+    parked outputs (nothing stays parked), and the identity tables are what keeps the model's
+    own rotation from rotating Q/K a second time: without them the block output is far off."""
+    torch.manual_seed(0)
+    dtype = torch.float32
+    base = _tiny("llama").to(dtype).eval()
+    write_packed_dir(base, tmp_path, bits_options=(3,), dtype=dtype)
+    ref = copy.deepcopy(base)
+    _dequantize_model_(ref, [3, 3, 3])
+    model = install_bitmap(copy.deepcopy(base), tmp_path, [3, 3, 3], device="cpu", dtype=dtype, fuse_rope=True)
+    primes = []
+    orig_prime = FusedQKV.prime
+    monkeypatch.setattr(FusedQKV, "prime", lambda self, *a: (primes.append(1), orig_prime(self, *a))[1])
+    ids = torch.randint(0, 512, (1, 16))
+
+    def block0_update(m):
+        h = m(ids, output_hidden_states=True).hidden_states
+        return (h[1] - h[0]).float()
+
+    with torch.no_grad():
+        la, lb = block0_update(ref), block0_update(model)
+    assert len(primes) == 3
+    assert (la - lb).abs().max() / la.abs().max() < 2e-2
+    assert not any(blk.self_attn.crispybits_qkv.pending for blk in _blocks(model))
+    monkeypatch.setattr(FusedQKV, "identity_tables", lambda self, cos, sin: (cos, sin))
+    with torch.no_grad():
+        lb2 = block0_update(model)
+    assert (la - lb2).abs().max() / la.abs().max() > 0.2, "a second rotation went unnoticed"
