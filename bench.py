@@ -91,51 +91,92 @@ def timed_kernels(C, fn, n_launch):
     return total, durs
 
 
+def graph_launch_us(torch, fn, n_launch, replays=20):
+    """Mean µs per launch of fn() (which makes n_launch launches), captured once as a HIP graph
+    and replayed `replays` times between events recorded on the replay stream."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    g.replay()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    t1.record(stream)
+    t1.synchronize()
+    ms = t0.elapsed_time(t1)
+    del g
+    return ms * 1e3 / (replays * n_launch)
+
+
 def best_config(torch, C, ops, x, ws, candidates):
-    """Pick (split_k, rho) with the smallest summed kernel time over the layer copies."""
+    """Pick (split_k, rho) with the shortest graph-replayed time over the layer copies."""
     best = None
     for sk, rho in candidates:
-        def run():
-            for w in ws:
-                ops.packed_linear(x, w, sk, rho)
-        run()
-        total, _ = timed_kernels(C, run, len(ws) * 2)
-        if best is None or total < best[0]:
-            best = (total, sk, rho)
+        us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w, sk, rho) for w in ws], len(ws), replays=4)
+        if best is None or us < best[0]:
+            best = (us, sk, rho)
     return best[1], best[2]
 
 
-def cpu_baseline(torch, weights, xs):
-    """Oracle (numpy dequant + matmul, reference.py:30-34 + test_correctness.py:23-31) on the host."""
-    import numpy as np
-    from oracle import reference as R
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
-    host = [(w.packed.cpu().numpy(), w.scales.float().cpu().numpy(), w.zeros.float().cpu().numpy(), w.bits,
-             w.in_features, x.float().cpu().numpy()) for w, x in zip(weights, xs)]
-
-    def one_pass():
-        for packed, s, z, bits, K, x in host:
-            Wd = R.dequantize(R.unpack_codes(packed, bits, K), s, z, GS)
-            _ = x @ Wd.T
-
-    for _ in range(2):
-        one_pass()
+def _median_ms(fn, warm=2, runs=5):
+    for _ in range(warm):
+        fn()
     times = []
-    for _ in range(3):
+    for _ in range(runs):
         t0 = time.perf_counter()
-        one_pass()
+        fn()
         times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    return statistics.median(times) * 1e3
+
+
+def cpu_baseline(torch, weights, xs, gemm_weight, gemm_x):
+    """The reference's CPU path on the host cores (BASELINE.md section 3 protocol): the oracle's
+    restatement of reference.py unpack_codes -> dequantize (reference.py:30-34,58-67) followed by
+    x.float() @ W.T in torch (test_correctness.py:23-31), on the same seeded inputs as the GPU.
+    Two numbers per config: dequant + matmul per call, and the matmul alone on a pre-dequantized
+    fp32 W.  torch runs on every core this process may use; 2 warm-up runs, median of 5."""
+    from oracle import reference as R
+    affinity = len(os.sched_getaffinity(0))
+    torch.set_num_threads(affinity)
+
+    def host(w):
+        return (w.packed.cpu().numpy(), w.scales.float().cpu().numpy(), w.zeros.float().cpu().numpy(), w.bits,
+                w.in_features)
+
+    def dequant(h):
+        packed, s, z, bits, K = h
+        return torch.from_numpy(R.dequantize(R.unpack_codes(packed, bits, K), s, z, GS))
+
+    # config 2 (the timed workload): one layer-set of the step, the three W3 GEMVs at M = 1
+    gemv = [(host(w), x.float().cpu()) for w, x in zip(weights, xs)]
+    dense = [dequant(h) for h, _ in gemv]
+    full_ms = _median_ms(lambda: [x @ dequant(h).T for h, x in gemv])
+    mm_ms = _median_ms(lambda: [x @ W.T for (_, x), W in zip(gemv, dense)])
     nbytes = sum(gemv_bytes(1, w.in_features, w.out_features, w.bits) for w in weights)
-    return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
-            "ms_per_layer_set": round(t * 1e3, 2),
-            "sample": "one layer-set of the timed step (the 3 W3 GEMVs at M=1) through oracle.reference "
-                      "unpack+dequantize (numpy, 1 thread) + fp32 matmul (BLAS threads = cores); "
-                      "2 warm-up passes, median of 3"}
+    # config 4 row: the M = 1024 prefill GEMM, W4 4096 x 4096
+    gh, gx = host(gemm_weight), gemm_x.float().cpu()
+    gW = dequant(gh)
+    g_full = _median_ms(lambda: gx @ dequant(gh).T)
+    g_mm = _median_ms(lambda: gx @ gW.T)
+    M, K = gemm_x.shape
+    flops = 2.0 * M * gemm_weight.out_features * K
+    return {"value": round(nbytes / (full_ms * 1e-3) / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "cpu_count": os.cpu_count(), "affinity": affinity, "torch_threads": torch.get_num_threads(),
+            "gemv_w3_m1_layer_set": {"dequant_matmul_ms": round(full_ms, 2), "matmul_only_ms": round(mm_ms, 3),
+                                     "GBps": round(nbytes / (full_ms * 1e-3) / 1e9, 4)},
+            "gemm_w4_m1024_4096x4096": {"dequant_matmul_ms": round(g_full, 2), "matmul_only_ms": round(g_mm, 2),
+                                        "TFLOPs": round(flops / (g_full * 1e-3) / 1e12, 4),
+                                        "TFLOPs_matmul_only": round(flops / (g_mm * 1e-3) / 1e12, 4)},
+            "sample": "config 2: one layer-set of the timed step (W3 GEMVs 4096x4096, 4096->11008, 11008->4096 at "
+                      "M=1); config 4: the W4 M=1024 4096x4096 GEMM.  oracle.reference unpack_codes + dequantize "
+                      "(numpy) then torch fp32 matmul on all affinity cores; 2 warm-up runs, median of 5; value = "
+                      "config 2 algorithmic bytes / dequant+matmul time"}
 
 
 def main():
@@ -145,7 +186,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="timed step + roofline only (no sweeps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--sweeps", default="gemv,fused,gemm,stack,producer",
+    ap.add_argument("--sweeps", default="gemv,fused,gemm,stack,model,producer",
                     help="comma-separated extra sweeps after the timed step (ignored with --quick)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the fixed launch sequence of the counter passes and exit")
@@ -208,25 +249,25 @@ def main():
     log(f"timed: {args.steps} steps, {ms_per_step:.4f} ms/step, {value:.1f} GB/s")
 
     # ---------------------------------------------------------------- roofline of the dominant kernel
-    # per shape: the 32 calls of that shape, timed per dispatch; a call's time is the sum
-    # of its dispatches (a split-K call also launches the combine)
+    # per shape: the 32 launches of that shape (one per layer copy) captured in a graph and
+    # replayed between two events recorded on the stream the kernels run on; a launch's
+    # duration is the replays' elapsed time over the launches, so it includes the gaps
+    # between back-to-back kernels and can only understate the kernel's own rate
     total_ms, per_shape = 0.0, []
     for s, (K, N) in enumerate(SHAPES):
-        def run_shape():
-            for lw in layers:
-                ops.packed_linear(xs[s], lw[s], cfg[s][0], cfg[s][1])
-        t, _ = timed_kernels(C, run_shape, 2 * LAYERS)
-        total_ms += t
-        us = t * 1e3 / LAYERS
+        us = graph_launch_us(torch, lambda s=s: [ops.packed_linear(xs[s], lw[s], cfg[s][0], cfg[s][1])
+                                                 for lw in layers], LAYERS)
+        total_ms += us * LAYERS * 1e-3
         per_shape.append({"K": K, "N": N, "bits": bits, "M": 1, "us": round(us, 3),
                           "GBps": round(gemv_bytes(1, K, N, bits) / (us * 1e-6) / 1e9, 1),
                           "split_k": cfg[s][0], "rho": cfg[s][1]})
     achieved = step_bytes / (total_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                "kernel": "gemv_stream_kernel<GEMV, 3> (W3 decode GEMV, M=1)",
+                "kernel": "gemv_stream_kernel<GEMV, 3, 1> (W3 decode GEMV, M=1)",
                 "bytes_per_launch_avg": round(step_bytes / (3 * LAYERS)),
-                "avg_launch_us": round(total_ms * 1e3 / (3 * LAYERS), 3), "per_shape": per_shape}
+                "avg_launch_us": round(total_ms * 1e3 / (3 * LAYERS), 3), "per_shape": per_shape,
+                "timing": "HIP events on the launch stream around graph replays of 32 launches per shape"}
     log(f"roofline: {achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of HBM peak; {per_shape}")
 
     out = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -248,11 +289,19 @@ def main():
             out["gemm"] = gemm_sweep(torch, C, ops, dev)
         if "stack" in todo:
             out["llama2_7b_stack"] = stack_sweep(torch, C, ops, dev)
+        if "model" in todo:
+            try:
+                out["llama2_7b_model"] = model_sweep(torch, dev)
+            except Exception as e:              # reported in the line; the other legs stand
+                log(f"llama2-7b model sweep failed: {e!r}")
+                out["llama2_7b_model"] = {"error": repr(e)[:500]}
+                torch.cuda.empty_cache()
         if "producer" in todo:
             out["producer"] = producer_sweep(torch, C, dev)
     if not args.no_cpu:
         log("cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(torch, base, xs)
+        gw = make_weight(torch, 4096, 4096, 4, 0, dev)
+        out["cpu_baseline"] = cpu_baseline(torch, base, xs, gw, randx(torch, 1024, 4096, 1, dev))
     print(json.dumps(out), flush=True)
 
 
@@ -290,54 +339,71 @@ def pmc_workload(torch, ops, dev):
     log("pmc workload done")
 
 
+ROTATE_BYTES = 1 << 30          # every GEMV sweep point streams at least this many distinct weight bytes
+
+
+def copies_for(nbytes, least=8):
+    """Weight copies whose total reaches ROTATE_BYTES, so no repeat is served by the 256 MB
+    MALL or the 4 MB per-XCD L2."""
+    return max(least, math.ceil(ROTATE_BYTES / nbytes))
+
+
+def weight_bytes(w):
+    return w.packed.numel() * 4 + w.scales.numel() * w.scales.element_size() * 2
+
+
 def gemv_sweep(torch, C, ops, dev):
-    """W2/W3/W4 x M in {1,4,8} x shapes: mean kernel us over 32 weight copies."""
+    """W2/W3/W4 x M in {1,4,8} x shapes: µs per call (graph-replayed, a split call counts its
+    combine launch) over >= 1 GiB of distinct weight copies per shape."""
     rows = []
     for bits in (4, 3, 2):
-        base = [make_weight(torch, N, K, bits, 0, dev) for K, N in SHAPES]
-        copies = [[clone_weight(w) for w in base] for _ in range(LAYERS)]
-        for M in (1, 4, 8):
-            for s, (K, N) in enumerate(SHAPES):
+        for s, (K, N) in enumerate(SHAPES):
+            base = make_weight(torch, N, K, bits, 0, dev)
+            ws = [base] + [clone_weight(base) for _ in range(copies_for(weight_bytes(base)) - 1)]
+            for M in (1, 4, 8):
                 x = randx(torch, M, K, 1, dev)
-                ws = [c[s] for c in copies]
-                sk, rho = best_config(torch, C, ops, x, ws, [(1, 0), (1, 1), (2, 0), (None, 1)])
-                run = lambda: [ops.packed_linear(x, w, sk, rho) for w in ws]
-                run()
-                total, durs = timed_kernels(C, run, 2 * len(ws))
-                us = total * 1e3 / len(ws)          # per call: a split-K call also launches the combine
+                best = None
+                for sk, rho in [(1, 1), (2, 1), (None, 1)]:
+                    us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w, sk, rho) for w in ws], len(ws),
+                                         replays=4)
+                    if best is None or us < best[0]:
+                        best = (us, sk, rho)
+                us, sk, rho = best
                 gbs = gemv_bytes(M, K, N, bits) / (us * 1e-6) / 1e9
                 rows.append({"bits": bits, "M": M, "K": K, "N": N, "us": round(us, 3), "GBps": round(gbs, 1),
-                             "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "split_k": sk, "rho": rho})
-                log(f"gemv W{bits} M={M} K={K} N={N}: {us:.2f} us {gbs:.0f} GB/s")
-        del copies
-        torch.cuda.empty_cache()
+                             "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "split_k": sk, "rho": rho,
+                             "copies": len(ws)})
+                log(f"gemv W{bits} M={M} K={K} N={N}: {us:.2f} us {gbs:.0f} GB/s ({len(ws)} copies)")
+            del ws, base
+            torch.cuda.empty_cache()
     return rows
 
 
 def fused_sweep(torch, C, ops, dev):
+    """Config 3 at M = 1: fused QKV (widths by seed) and fused gate-up (W3, 2 x 11008), µs per call
+    graph-replayed over >= 1 GiB of weight copies."""
     import numpy as np
     res = {}
     qkv_bits = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 3)]
-    sets = [[make_weight(torch, 4096, 4096, b, s + 1, dev) for s, b in enumerate(qkv_bits)]]
-    sets += [[clone_weight(w) for w in sets[0]] for _ in range(15)]
+    first = [make_weight(torch, 4096, 4096, b, s + 1, dev) for s, b in enumerate(qkv_bits)]
+    n = copies_for(sum(weight_bytes(w) for w in first))
+    sets = [first] + [[clone_weight(w) for w in first] for _ in range(n - 1)]
     x = randx(torch, 1, 4096, 1, dev)
-    run = lambda: [ops.fused_qkv(x, *ws) for ws in sets]
-    run()
-    total, durs = timed_kernels(C, run, 2 * len(sets))
-    us = total * 1e3 / len(sets)
+    us = graph_launch_us(torch, lambda: [ops.fused_qkv(x, *ws) for ws in sets], len(sets), replays=4)
     nbytes = sum(gemv_bytes(1, 4096, 4096, b) for b in qkv_bits) - 2 * 4096 * 2
     res["qkv"] = {"bits": qkv_bits, "K": 4096, "N": [4096] * 3, "us": round(us, 3),
-                  "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+                  "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "copies": len(sets)}
+    del sets, first
     g0 = make_weight(torch, 11008, 4096, 3, 4, dev)
     u0 = make_weight(torch, 11008, 4096, 3, 5, dev)
-    pairs = [(g0, u0)] + [(clone_weight(g0), clone_weight(u0)) for _ in range(11)]
-    run = lambda: [ops.fused_gate_up(x, g, u) for g, u in pairs]
-    run()
-    total, durs = timed_kernels(C, run, 2 * len(pairs))
-    us = total * 1e3 / len(pairs)
+    n = copies_for(weight_bytes(g0) + weight_bytes(u0))
+    pairs = [(g0, u0)] + [(clone_weight(g0), clone_weight(u0)) for _ in range(n - 1)]
+    us = graph_launch_us(torch, lambda: [ops.fused_gate_up(x, g, u) for g, u in pairs], len(pairs), replays=4)
     nbytes = 2 * gemv_bytes(1, 4096, 11008, 3) - 4096 * 2 - 11008 * 2
     res["gate_up"] = {"bits": 3, "K": 4096, "N": [11008, 11008], "us": round(us, 3),
-                      "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+                      "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "copies": len(pairs)}
+    del pairs
+    torch.cuda.empty_cache()
     log(f"fused: {res}")
     return res
 
@@ -366,27 +432,28 @@ def producer_sweep(torch, C, dev):
 
 
 def gemm_sweep(torch, C, ops, dev):
+    """Config 4: the prefill GEMM at M in {1024, 2048}, µs per call graph-replayed over 4 weight
+    copies (the weights are read once per 128-row tile either way; the activations dominate)."""
     rows = []
     for M in (1024, 2048):
         for K, N in SHAPES:
             x = randx(torch, M, K, 1, dev)
             for bits in (4, 3, 2):
                 ws = [make_weight(torch, N, K, bits, 0, dev)]
-                ws += [clone_weight(ws[0]) for _ in range(2)]
-                run = lambda: [ops.packed_linear(x, w) for w in ws * 2]
-                run()
-                total, durs = timed_kernels(C, run, len(ws) * 4)
-                us = total * 1e3 / (2 * len(ws))
+                ws += [clone_weight(ws[0]) for _ in range(3)]
+                us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w) for w in ws], len(ws), replays=5)
                 tfs = 2.0 * M * N * K / (us * 1e-6) / 1e12
                 rows.append({"M": M, "K": K, "N": N, "bits": bits, "us": round(us, 2), "TFLOPs": round(tfs, 1),
                              "pct_peak": round(100 * tfs / MFMA_F16_PEAK_TFS, 1)})
                 log(f"gemm M={M} K={K} N={N} W{bits}: {us:.1f} us {tfs:.1f} TFLOP/s")
+                del ws
     return rows
 
 
 STACK_H, STACK_I, STACK_BLOCKS = 4096, 11008, 32
 STACK_LINEARS = [("q", STACK_H, STACK_H), ("k", STACK_H, STACK_H), ("v", STACK_H, STACK_H), ("o", STACK_H, STACK_H),
                  ("gate", STACK_I, STACK_H), ("up", STACK_I, STACK_H), ("down", STACK_H, STACK_I)]   # (name, N, K)
+PREFILL_M = 2048
 
 
 def stack_energy(torch, gr, gr16, seconds=4.0):
@@ -490,6 +557,39 @@ def stack_sweep(torch, C, ops, dev, steps=20):
     fp16_t = wall(gr16.replay, steps)
     energy = stack_energy(torch, gr, gr16)
     del gr, gr16
+
+    # prefill leg: the same 32 blocks at M = 2048 (every linear on the prefill GEMM; fused QKV
+    # as three GEMMs, fused gate-up as two GEMMs and their product), one graph per step
+    Xh = randx(torch, PREFILL_M, STACK_H, 3, dev)
+    Xi = randx(torch, PREFILL_M, STACK_I, 4, dev)
+
+    def prefill():
+        for b in blocks:
+            ops.fused_qkv(Xh, b["q"], b["k"], b["v"])
+            ops.packed_linear(Xh, b["o"])
+            ops.fused_gate_up(Xh, b["gate"], b["up"])
+            ops.packed_linear(Xi, b["down"])
+
+    def prefill_fp16():
+        for d in dense:
+            for nm in ("q", "k", "v", "o"):
+                F.linear(Xh, d[nm])
+            F.silu(F.linear(Xh, d["gate"])) * F.linear(Xh, d["up"])
+            F.linear(Xi, d["down"])
+
+    flops = 2.0 * PREFILL_M * sum(N * K for _, N, K in STACK_LINEARS) * len(blocks)
+    gp = graphed(prefill)
+    pre_t = wall(gp.replay, 3)
+    del gp
+    gp16 = graphed(prefill_fp16)
+    pre16_t = wall(gp16.replay, 3)
+    del gp16, Xh, Xi
+    prefill_res = {"M": PREFILL_M, "TFLOP_per_step": round(flops / 1e12, 3),
+                   "graph_ms_per_step": round(pre_t * 1e3, 3), "TFLOPs": round(flops / pre_t / 1e12, 1),
+                   "pct_peak": round(100 * flops / pre_t / 1e12 / MFMA_F16_PEAK_TFS, 1),
+                   "fp16_dense_graph_ms_per_step": round(pre16_t * 1e3, 3),
+                   "speedup_vs_fp16": round(pre16_t / pre_t, 3)}
+    log(f"llama2-7b stack prefill: {prefill_res}")
     dense_gb = sum(t.numel() * 2 for d in dense for t in d.values()) / 1e9
     res = {"workload": "Llama-2-7B linear stack, decode M=1, 32 blocks x (fused QKV, o, fused gate-up, down)",
            "bitmap": bitmap, "mean_bits": round(float(np.mean(bitmap)), 3), "packed_GB": round(packed_gb, 3),
@@ -497,9 +597,108 @@ def stack_sweep(torch, C, ops, dev, steps=20):
            "graph_us_per_step": round(graph_t * 1e6, 1), "kernel_us_per_step": round(kern_ms * 1e3, 1),
            "GBps_graph": round(step_bytes / graph_t / 1e9, 1),
            "fp16_dense_GB": round(dense_gb, 3), "fp16_graph_us_per_step": round(fp16_t * 1e6, 1),
-           "speedup_vs_fp16": round(fp16_t / graph_t, 2), "energy": energy}
+           "speedup_vs_fp16": round(fp16_t / graph_t, 2), "energy": energy, "prefill": prefill_res}
     log(f"llama2-7b stack: {res}")
     del blocks, dense
+    torch.cuda.empty_cache()
+    return res
+
+
+def model_sweep(torch, dev, steps=20, prompt_len=32):
+    """Config 5 through the integration glue: an HF LlamaForCausalLM with Llama-2-7B dimensions
+    (32 blocks, hidden 4096, intermediate 11008, 32 heads, random init), written with the config-5
+    bitmap (write_packed_dir(bitmap=...), GPU producer) and installed with
+    install_bitmap(fuse=True, fuse_rope=True) (integration.py:201-218 interface).  One decode
+    step over a static KV cache is captured as a HIP graph and replayed; the same model with every
+    block linear replaced by its dequantized fp16 weight is captured the same way.  Reports µs per
+    step of both and the relative difference of their logits."""
+    import copy
+    import shutil
+    import tempfile
+    import numpy as np
+    import transformers
+    from crispybits_kernels import _C
+    from crispybits_kernels.integration import _blocks, install_bitmap
+    from crispybits_kernels.reference import dequantize, pack_linear_dict, write_packed_dir
+    bitmap = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], STACK_BLOCKS)]
+    cfg = transformers.LlamaConfig(hidden_size=STACK_H, intermediate_size=STACK_I, num_hidden_layers=STACK_BLOCKS,
+                                   num_attention_heads=32, num_key_value_heads=32, vocab_size=32000,
+                                   max_position_embeddings=512)
+    torch.manual_seed(0)
+    t0 = time.perf_counter()
+    with torch.device(dev):
+        base = transformers.LlamaForCausalLM(cfg).half().eval()
+    tmp = tempfile.mkdtemp(prefix="cbk_model_", dir="/tmp")
+    try:
+        write_packed_dir(base, tmp, group_size=GS, dtype=torch.float16, bitmap=bitmap)
+        ref = copy.deepcopy(base)
+        with torch.no_grad():
+            for block, bits in zip(_blocks(ref), bitmap):
+                for _, m in block.named_modules():
+                    if isinstance(m, torch.nn.Linear):
+                        d = pack_linear_dict(m.weight.detach(), bits, GS, None, torch.float16)
+                        q = _C.unpack_codes(d["packed"].to(dev), bits, m.in_features)
+                        m.weight.copy_(dequantize(q, d["scales"].to(dev).float(), d["zeros"].to(dev).float(),
+                                                  GS).half())
+        t1 = time.perf_counter()
+        model = install_bitmap(base, tmp, bitmap, device=dev, dtype=torch.float16, fuse=True, fuse_rope=True)
+        install_s = time.perf_counter() - t1
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    prompt = torch.randint(0, 32000, (1, prompt_len), generator=torch.Generator().manual_seed(1)).to(dev)
+
+    def captured(m):
+        """Decode steps of m as one captured graph.  HF's StaticLayer writes each update at its
+        own device counter and advances it in place (cache_position is not read for the
+        write), so the step advances its position buffer the same way: the warm-up and every
+        replay decode the next slot, as a generation loop does.  The cache holds the prompt,
+        the warm-up and every replay, and each replay is checked to stay inside it."""
+        slots = prompt_len + steps + 8
+        cache = transformers.StaticCache(config=cfg, max_cache_len=slots)
+        with torch.no_grad():
+            m(prompt, past_key_values=cache, cache_position=torch.arange(prompt_len, device=dev), use_cache=True)
+        tok = prompt[:, -1:].clone()
+        pos = torch.tensor([prompt_len], device=dev)
+
+        def step():
+            logits = m(tok, past_key_values=cache, cache_position=pos, use_cache=True).logits[:, -1]
+            pos.add_(1)
+            return logits
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.no_grad(), torch.cuda.stream(side):
+            step()                                        # slot prompt_len
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.no_grad(), torch.cuda.graph(g):
+            logits = step()
+        written = prompt_len + 1
+        if written + 1 + steps > slots:
+            raise RuntimeError("decode replays would run past the static cache")
+        g.replay()                                        # slot prompt_len + 1
+        torch.cuda.synchronize()
+        first = logits.float().clone()
+        t = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        elapsed = (time.perf_counter() - t) / steps
+        del g
+        return elapsed, first
+
+    packed_t, packed_logits = captured(model)
+    fp16_t, fp16_logits = captured(ref)
+    diff = ((packed_logits - fp16_logits).abs().max() / fp16_logits.abs().max()).item()
+    res = {"workload": "HF LlamaForCausalLM, Llama-2-7B dimensions (32 blocks, random init), config-5 bitmap, "
+                       "install_bitmap(fuse=True, fuse_rope=True); one decode step (M=1) over a static KV cache "
+                       f"after a {prompt_len}-token prompt, as a HIP graph",
+           "bitmap": bitmap, "packed_graph_us_per_step": round(packed_t * 1e6, 1),
+           "fp16_dequantized_graph_us_per_step": round(fp16_t * 1e6, 1),
+           "speedup_vs_fp16": round(fp16_t / packed_t, 3), "logits_rel_diff_vs_dequantized_fp16": round(diff, 5),
+           "build_s": round(t1 - t0, 1), "install_s": round(install_s, 1)}
+    log(f"llama2-7b model: {res}")
+    del model, ref, base
     torch.cuda.empty_cache()
     return res
 

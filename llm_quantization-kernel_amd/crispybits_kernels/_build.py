@@ -49,20 +49,69 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP/C++ source and link the shared library; returns its path."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
-    jobs = min(len(SOURCES), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
-    with ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
-    tmp = LIB_PATH + ".tmp"
-    cmd = [_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
+EXT_SOURCE = "torch_ext.cpp"
+
+
+def _ext_path() -> str:
+    import sysconfig
+    return os.path.join(PKG_DIR, "_ext" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _torch_flags():
+    """Include paths, defines and libraries of the installed torch (ROCm build) for a host-only
+    C++ extension; no torch.utils.cpp_extension (it would hipify), no device code."""
+    import sysconfig
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    inc = [os.path.join(tdir, "include"), os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+           sysconfig.get_paths()["include"], "/opt/rocm/include", os.path.join(os.path.dirname(ROOT), "include")]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    defs = ["-DTORCH_EXTENSION_NAME=_ext", "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            "-DUSE_ROCM=1", "-D__HIP_PLATFORM_AMD__=1"]
+    libdir = os.path.join(tdir, "lib")
+    libs = [f"-L{libdir}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+            f"-Wl,-rpath,{libdir}"]
+    return [f"-I{p}" for p in inc] + defs, libs
+
+
+def _compile_ext(verbose: bool) -> str:
+    obj = os.path.join(OBJ_DIR, "torch_ext.o")
+    cflags, _ = _torch_flags()
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-w", *cflags, "-c",
+           os.path.join(CSRC, EXT_SOURCE), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+        raise RuntimeError(f"compile failed for {EXT_SOURCE}:\n{r.stdout}\n{r.stderr}")
+    return obj
+
+
+def _run(cmd, verbose, what):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{r.stdout}\n{r.stderr}")
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP/C++ source, link the C-ABI library and the torch op module over it;
+    returns the library's path."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    jobs = min(len(SOURCES) + 1, max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with ThreadPoolExecutor(jobs) as ex:
+        ext_obj = ex.submit(_compile_ext, verbose)
+        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
+        ext_obj = ext_obj.result()
+    tmp = LIB_PATH + ".tmp"
+    _run([_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp], verbose, "link")
     os.replace(tmp, LIB_PATH)
+    _, libs = _torch_flags()
+    ext = _ext_path()
+    _run([os.environ.get("CXX", "g++"), "-shared", "-fPIC", ext_obj, "-o", ext + ".tmp", f"-L{PKG_DIR}",
+          "-lcrispybits_hip", "-Wl,-rpath,$ORIGIN", *libs], verbose, "extension link")
+    os.replace(ext + ".tmp", ext)
     return LIB_PATH
 
 

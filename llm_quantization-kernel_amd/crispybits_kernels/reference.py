@@ -190,14 +190,17 @@ def dequantized_weight(d: Dict) -> torch.Tensor:
 
 
 def write_packed_dir(model: torch.nn.Module, out_dir: str, bits_options: Iterable[int] = (2, 3, 4),
-                     group_size: int = 128, dtype=torch.float16) -> None:
-    """block_{i:03d}_w{b}.pt per block and width: {linear name: packed dict}."""
+                     group_size: int = 128, dtype=torch.float16, bitmap: Optional[Iterable[int]] = None) -> None:
+    """block_{i:03d}_w{b}.pt per block and width: {linear name: packed dict}.  With ``bitmap``
+    (additive) block i is written at width bitmap[i] only, the files install_bitmap reads for
+    that bitmap."""
     from .integration import _blocks
     out = Path(out_dir)
     out.mkdir(parents=True, exist_ok=True)
+    widths = None if bitmap is None else [int(b) for b in bitmap]
     for i, block in enumerate(_blocks(model)):
         linears = {n: m for n, m in block.named_modules() if isinstance(m, torch.nn.Linear)}
-        for b in bits_options:
+        for b in (bits_options if widths is None else (widths[i],)):
             data = {n: pack_linear_dict(m.weight.detach(), b, group_size, m.bias, dtype) for n, m in linears.items()}
             torch.save(data, out / f"block_{i:03d}_w{b}.pt")
 

@@ -25,17 +25,34 @@ def test_header_declares_expected_entry_points():
 
 def test_library_exports_every_declared_symbol():
     from crispybits_kernels import _C
+    import cabi
     lib = ctypes.CDLL(_C.LIB_PATH)
     for name in _declared():
         assert hasattr(lib, name), name
-    assert set(_declared()) == set(_C.EXPORTS)
+    assert set(_declared()) == set(cabi.SIGS)          # every entry point is callable from the tests
     assert _C.ABI_VERSION == 1
     assert _C.tile_n() == 16
 
 
-def _lib():
+def test_op_module_binds_the_reference_functions():
+    """The compiled op module exports the reference's seven _C functions (bindings.cpp:32-40)
+    plus the additive ones, and its checks raise RuntimeError without touching a device."""
+    import torch
     from crispybits_kernels import _C
-    return _C._lib
+    for name in ("packed_gemv", "packed_gemm", "fused_gate_up", "fused_qkv", "sm_count", "tile_n", "max_rho",
+                 "unpack_codes", "quantize_pack", "decode_plan", "timer_start", "timer_stop"):
+        assert callable(getattr(_C, name)), name
+    x = torch.zeros(1, 256)
+    w = torch.zeros(4, 32, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="x must be CUDA"):
+        _C.packed_gemv(x, w, torch.zeros(4, 2), torch.zeros(4, 2), None, 4, 256, 128, 1, 1, 0, None)
+    with pytest.raises(RuntimeError, match="kind must be"):
+        _C.max_rho(3, "nope")
+
+
+def _lib():
+    import cabi
+    return cabi.lib
 
 
 def _err():

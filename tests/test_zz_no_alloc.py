@@ -2,12 +2,11 @@
 its output equals cbk_packed_gemv's (same kernels, split-K partials in the library's
 device scratch instead of a caller buffer) bit for bit, on two calls in a row, the
 second with a smaller input; sizes above the scratch are rejected on the host."""
-import ctypes
-
 import numpy as np
 import pytest
 import torch
 
+import cabi
 from crispybits_kernels import _C
 from crispybits_kernels.io import from_packed_dict
 from crispybits_kernels.reference import pack_linear_dict
@@ -26,11 +25,11 @@ def _weight(n, k, bits, seed):
 def _noalloc(x, w, split_k, rho=1, act=0):
     out = torch.empty((x.size(0), w.out_features), dtype=x.dtype, device=x.device)
     dev = x.get_device()
-    rc = _C._lib.cbk_packed_gemv_noalloc(x.data_ptr(), 0, x.size(0), x.size(1), w.packed.data_ptr(),
+    rc = cabi.lib.cbk_packed_gemv_noalloc(x.data_ptr(), 0, x.size(0), x.size(1), w.packed.data_ptr(),
                                          w.scales.data_ptr(), w.zeros.data_ptr(), None, w.out_features, w.bits,
                                          w.group_size, split_k, rho, act, out.data_ptr(), dev,
                                          torch.cuda.current_stream(dev).cuda_stream)
-    assert rc == 0, _C._lib.cbk_last_error().decode()
+    assert rc == 0, cabi.lib.cbk_last_error().decode()
     return out
 
 
@@ -55,9 +54,9 @@ def test_noalloc_rejects_oversized_partials():
     # 16 batch rows x 4096 rows x 64 splits of fp32 partials exceed the scratch; the check
     # runs on the host before any device work (fake, never dereferenced addresses)
     a = 1 << 20
-    rc = _C._lib.cbk_packed_gemv_noalloc(a, 0, 16, 4096, a, a, a, None, 4096, 4, 128, 64, 1, 0, a, 0, None)
+    rc = cabi.lib.cbk_packed_gemv_noalloc(a, 0, 16, 4096, a, a, a, None, 4096, 4, 128, 64, 1, 0, a, 0, None)
     assert rc == 1
-    assert "device scratch" in _C._lib.cbk_last_error().decode()
+    assert "device scratch" in cabi.lib.cbk_last_error().decode()
     limit = 1 << 21
-    need = _C._lib.cbk_gemv_partial_floats(0, 16, 4096, 4096, 128, 64)
+    need = cabi.lib.cbk_gemv_partial_floats(0, 16, 4096, 4096, 128, 64)
     assert need > limit
