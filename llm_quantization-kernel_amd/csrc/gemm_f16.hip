@@ -4,40 +4,39 @@
 // activations, with the reference's weight rounding W-hat = RN_fp16((q - z) * s)
 // (packed_gemm.cu:56,60).
 //
-// Tile: 128 x 128 outputs per workgroup of six waves.  All global traffic is
-// direct-to-LDS loads issued by two loader waves; the four compute waves read LDS
-// only, so their waits are LDS counts the compiler tracks exactly.
-//   activation loader (wave 4): the activation tile, 128 rows x 64 codes per stage,
-//     into a ring of NSTAGE stages (16 instructions of 1 KB per stage, XOR-swizzled
-//     16-byte pieces: piece p of row r at slot r * 8 + (p ^ ((r >> 1) & 7))),
-//     NSTAGE - 1 stages ahead; one workgroup barrier publishes each stage.
-//   weight loader (wave 5): the packed tile in blocks of WBLK stages (256 codes =
-//     8 chunks of each of the 128 rows), double-buffered one block ahead.  A row's
-//     block is fetched as the 16-byte-aligned pieces that cover it (its start has
-//     phase (row address & 15) within the first), with an odd piece count per row
-//     as the LDS pitch, so the compute lanes' reads of 32 rows are free of bank
-//     conflicts.  Scales and zeros likewise: per row and tensor a 32-byte aligned
-//     span holding the 8 groups of a window (gs / 32 blocks), double-buffered.
-//     Aligned pieces never straddle a page, so a piece holding any valid byte is
-//     readable; pieces wholly past a tensor's end re-read its last piece.
-//   compute (waves 0-3, a 2 x 2 grid of 64 x 64 wave tiles): each wave reads its
-//     activation operands and its columns' packed chunks from LDS and dequantizes
-//     the chunks straight into the B operands of v_mfma_f32_32x32x16_f16; the
-//     dequantized tile never touches LDS.
+// Tile: 128 x 128 outputs per workgroup of eight waves, two per SIMD.  Wave w owns
+// the 128 x 32 slab at columns 32 (w & 3) -- every tile row, so each column is
+// dequantized once -- for k half w >> 2 of every stage: the two waves sharing a
+// SIMD split each stage's k-steps, so while one waits on LDS or memory the other
+// issues, and their partial sums meet in LDS at the end.
+//
+// Every wave computes and every wave loads.  Global traffic is direct-to-LDS
+// buffer loads (one instruction per KB, no VGPR data).  A stage is 128 codes of K.
+// Load group t holds the wave's eighth of activation stage t + 2 (128 rows x 128
+// codes, XOR-swizzled 16-byte pieces, into a ring of three stage slots) and, at
+// even t, of weight block t / 2 + 1 (256 codes of the tile's 128 packed rows,
+// double-buffered) and of a scale / zero window (8 groups per row).  Group t's
+// instructions go out in eight slots, two per k-step, between barrier t and the
+// wait before barrier t + 1, so no wave stalls long on a full memory queue while
+// the MFMAs starve.  Before barrier t + 1 a wave waits until at most group t is in
+// flight, so group t - 1 -- everything stage t + 1 needs -- has landed for every
+// wave once the barrier passes.  Every group of a parity holds the same number of
+// loads, so the waits are constants.
+//
+// MFMA operand lane map (v_mfma_f32_32x32x16_f16): lane (r32 = lane & 31, hk =
+// lane >> 5) holds column r32's B operand and the A operands of rows 32 a + r32
+// (a < 4).  Step ks of a stage gives lane half hk the codes 64 hk + 8 ks .. +7
+// (octet ks & 3 of chunk 4 s + 2 hk + (ks >> 2)), the same k order for both
+// operands; the wave of k half kh runs steps 4 kh .. 4 kh + 3, so each lane needs
+// one chunk (chunk 2 hk + kh of the stage) and one (scale, zero) per stage.
 //
 // Weight rounding: the codes of a pair are OR-ed into 0x6400 (1024 + q, exact),
-// then (h - (1024 + z)) * s in packed fp16 when every zero point of the tile is an
-// integer below 1024 in magnitude (the reference quantizer's; the weight loader
-// scans the tile's zeros once): the difference is an exact integer and the product
-// rounds once, exactly RN_fp16((q - z) * s).  Other zero points take the fp32
-// product.  Codes at k >= K dequantize to zero, so the clamped activation reads and
-// the tail of the last weight block contribute nothing.
-//
-// MFMA operand lane map (32x32x16): lane (r = lane & 31, h = lane >> 5) holds
-// row / column r and 8 k-values of the step.  The k order within a stage is free
-// as long as both operands use it: step ks of a stage gives lane half h the codes
-// 32 h + 8 ks .. +7 (octet ks of chunk 2 s + h), so each compute lane needs one
-// packed chunk and one (scale, zero) pair per column per stage.
+// then (h - (1024 + z)) * s in packed fp16 when every zero point of the wave's
+// columns is an integer below 1024 in magnitude (the reference quantizer's; each
+// wave scans its columns' zeros once): the difference is an exact integer and the
+// product rounds once, exactly RN_fp16((q - z) * s).  Other zero points take the
+// fp32 product.  Codes at k >= K meet zero activations, so the tail of the last
+// weight block contributes nothing.
 #include "cbk_decode.hpp"
 #include "cbk_device.hpp"
 #include "cbk_kernels.hpp"
@@ -51,32 +50,40 @@ typedef float f16x __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) char lds_t;            // LDS bytes: 32-bit addresses
 
 constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int NSTAGE = 3;                    // activation stages in LDS
-constexpr int THREADS = 448;                 // 4 compute waves + 2 activation loaders + 1 weight loader
+constexpr int WAVES = 8;                     // two per SIMD: four column slabs x two k halves
+constexpr int THREADS = 64 * WAVES;
+constexpr int NSTAGE = 3;                    // activation stage slots in LDS
 constexpr int TILE = BM * BK * 2;            // bytes of an activation stage (32 KB)
 constexpr int APR = BK * 2 / 16;             // 16-byte pieces per activation row of a stage
-constexpr int A_INSTR = TILE / 1024 / 2;     // instructions per activation loader per stage
+constexpr int A_Q = TILE / 1024 / WAVES;     // activation instructions per wave per stage (4)
 constexpr int WBLK = 2;                      // stages per weight block (256 codes)
 constexpr int SZG = 8;                       // groups per scale / zero window
-constexpr int SZ_INSTR = 2 * BN * 2 / 64;    // window: [tensor][row] x two 16-byte pieces
-constexpr int SZ_BUF = 2 * BN * 32;
+constexpr int SZ_Q = 2 * BN * 2 / 64 / WAVES;   // window instructions per wave (1)
+constexpr int SZ_BUF = 2 * BN * 32;          // [tensor][row] x 32 bytes
+constexpr int SLOTS = 8;                     // issue slots of a load group (two per k-step)
+constexpr int KSTEPS = 4;                    // k-steps of a stage per wave (its k half)
 
 // Weight block geometry: a row's block is 32 * BITS bytes at phase 0 (W4), 0 / 8
-// (W2) or 0 / 4 / 8 / 12 (W3) within its first aligned piece.
+// (W2) or 0 / 4 / 8 / 12 (W3) within its first aligned piece, PPR pieces (odd, so
+// 32 rows read at one offset hit distinct banks).  The block's pieces are spread
+// over the waves in whole instructions; the last ones re-read the last row
+// into the padding.
 template <int BITS> struct WGeo {
-    static constexpr int PPR = BITS == 4 ? 9 : (BITS == 3 ? 7 : 5);   // pieces per row, odd
+    static constexpr int PPR = BITS == 4 ? 9 : (BITS == 3 ? 7 : 5);
     static constexpr int PITCH = 16 * PPR;
-    static constexpr int BUF = BN * PITCH;
-    static constexpr int INSTR = BN * PPR / 64;
+    static constexpr int W_Q = (BN * PPR + 64 * WAVES - 1) / (64 * WAVES);
+    static constexpr int BUF = W_Q * WAVES * 1024;
+    static_assert(A_Q + W_Q + SZ_Q <= SLOTS, "slot budget");
 };
 
 constexpr int A_OFF = 0;
 constexpr int W_OFF = NSTAGE * TILE;
 template <int BITS> constexpr int SZ_OFF = W_OFF + 2 * WGeo<BITS>::BUF;
-template <int BITS> constexpr int FLAG_OFF = SZ_OFF<BITS> + 2 * SZ_BUF;   // tile zeros allow the fp16 form
-template <int BITS> constexpr int LDS_BYTES = FLAG_OFF<BITS> + 16;
+template <int BITS> constexpr int LDS_BYTES = SZ_OFF<BITS> + 2 * SZ_BUF;
+static_assert(LDS_BYTES<4> <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ int swz(int r) { return r & (APR - 1); }
 
@@ -94,115 +101,137 @@ __device__ __forceinline__ void barrier_lds() {
     __builtin_amdgcn_s_barrier();
 }
 
-__device__ __forceinline__ void dma16(const void* g, char* lds) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
-}
-
-// ------------------------------------------------------------------ activation loader
-// Loader wave h moves instructions t = 8 h .. 8 h + 7 of each stage; lane l of
-// instruction t moves slot q = 64 t + l: row q >> 3, logical piece (q & 7) ^ swz(row).
-// The loads go through a buffer descriptor over the activations: the lane's offset
-// (row clamped to M, piece) is fixed, the stage's column offset is a scalar, so a
-// stage costs no VALU.  Pieces past K read on into the next row (or, past the
-// tensor, zero), which meets zero weights -- except in the last stage, where pieces
-// at k >= K read as zero (K % 8 == 0, so a piece is wholly inside or outside), so
-// whatever the weight tile holds there contributes nothing.
-struct ALoader {
-    __amdgpu_buffer_rsrc_t rsrc;
-    int voff[A_INSTR];
-    int rowoff[A_INSTR];          // byte offset of the lane's row
-    int pk[A_INSTR];              // k of the lane's piece within a stage
-    int t0;                       // first instruction of this loader
-};
-
-__device__ __forceinline__ void a_setup(const GemmArgs& A, int m0, int half, int lane, ALoader& d) {
-    d.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * 2, 0x00020000);
-    d.t0 = A_INSTR * half;
-#pragma unroll
-    for (int i = 0; i < A_INSTR; ++i) {
-        const int q = 64 * (d.t0 + i) + lane;
-        const int r = q / APR, p = (q & (APR - 1)) ^ swz(r);
-        d.rowoff[i] = min(m0 + r, A.M - 1) * A.K * 2;
-        d.pk[i] = 8 * p;
-        d.voff[i] = d.rowoff[i] + 16 * p;
-    }
+// One 16-byte-per-lane direct-to-LDS buffer load into byte `dst` of the LDS.  A
+// plain function: the builtin then appears in no template body, which the host
+// pass would reject.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, lds_t* lds, uint32_t dst, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(lds + dst), 16, voff, soff, 0, 0);
 }
 
 // A byte offset past every buffer descriptor's range: such loads return zero.
 constexpr int OOR = 0x7FFFFFF0;
 
-// Stage s into slot s % NSTAGE; a stage past the last is issued as the last one,
-// so every iteration issues A_INSTR loads and the waits are constants.
-__device__ __forceinline__ void issue_a(const GemmArgs& A, const ALoader& d, int s, int nst, char* lds) {
-    char* dst = lds + A_OFF + (s % NSTAGE) * TILE + d.t0 * 1024;
-    s = min(s, nst - 1);
-    if (s == nst - 1 && A.K % BK != 0) {
-#pragma unroll
-        for (int i = 0; i < A_INSTR; ++i) {
-            const int k = BK * s + d.pk[i];
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rsrc, (lds_void*)(dst + i * 1024), 16,
-                                                     k < A.K ? d.rowoff[i] + 2 * k : OOR, 0, 0, 0);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < A_INSTR; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rsrc, (lds_void*)(dst + i * 1024), 16, d.voff[i], BK * 2 * s,
-                                                     0, 0);
-    }
-}
-
-// ------------------------------------------------------------------ weight loader
-// Block j of the tile into buffer j & 1: lane l of instruction t moves piece
-// q = 64 t + l, row q / PPR, piece q % PPR of the row's aligned span.  Scale /
-// zero window w: instruction t < 4 the scales, else the zeros; lane l moves piece
-// q & 1 of tile row (q >> 1) & 127's span, the 16 halves from floor8(col * G) + 8 w
-// (floor8(col * G + 8 w), as 8 w is a multiple of 8).  Buffer descriptors over the
-// packed words, scales and zeros: the lane's offsets are fixed and the block /
-// window offset is a scalar; reads past a tensor return zero (they are never used).
+// ------------------------------------------------------------------ the wave's loads
+// Activations: wave v moves instructions A_Q v .. A_Q v + A_Q - 1 of a stage (its
+// rows 16 v .. 16 v + 15); lane l of instruction t moves slot q = 64 t + l: row
+// q >> 4, logical piece (q & 15) ^ swz(row), through a descriptor over the
+// activations (row clamped to M).  In a partial last stage, pieces at k >= K read
+// as zero (K % 8 == 0, so a piece is wholly inside or outside).
+// Weights: wave v moves instructions W_Q v + t of a block; lane l moves piece
+// q = 64 (W_Q v + t) + l, row q / PPR (clamped to the tile), piece q % PPR of the
+// row's aligned span.  Windows: wave v moves instruction v of eight (the first four
+// the scales, the rest the zeros); lane l moves piece q & 1 of tile row
+// (q >> 1) & 127's span, the 16 halves from floor8(col * G) + 8 w.  The lane's
+// offsets are fixed; the stage / block / window offset is a scalar.
 template <int BITS>
-struct WLoader {
-    __amdgpu_buffer_rsrc_t wr, sr, zr;
-    int woff[WGeo<BITS>::INSTR];
-    int szoff[SZ_INSTR];
+struct Loads {
+    __amdgpu_buffer_rsrc_t ar, wr, szr;
+    int avoff[A_Q];
+    int atoff[A_Q];
+    int woff[WGeo<BITS>::W_Q];
+    int szoff[SZ_Q];
+    uint32_t a_lds, w_lds, sz_lds;   // LDS byte of the wave's first instruction in a slot / buffer
 };
 
 template <int BITS>
-__device__ __forceinline__ void w_setup(const GemmArgs& A, int n0, int lane, WLoader<BITS>& d) {
+__device__ __forceinline__ void loads_setup(const GemmArgs& A, int m0, int n0, int nst, int wave, int lane,
+                                            Loads<BITS>& L) {
     using G = WGeo<BITS>;
-    d.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(A.w), (short)0, A.N * A.wpr * 4, 0x00020000);
-    d.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.s), (short)0, A.N * A.G * 2, 0x00020000);
-    d.zr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.z), (short)0, A.N * A.G * 2, 0x00020000);
+    L.ar = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * 2, 0x00020000);
+    L.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(A.w), (short)0, A.N * A.wpr * 4, 0x00020000);
+    L.szr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(SZ_Q * wave >= 4 ? A.z : A.s), (short)0,
+                                              A.N * A.G * 2, 0x00020000);
 #pragma unroll
-    for (int t = 0; t < G::INSTR; ++t) {
-        const int q = 64 * t + lane;
-        const int r = q / G::PPR, p = q - r * G::PPR;
-        d.woff[t] = ((min(n0 + r, A.N - 1) * A.wpr * 4) & ~15) + 16 * p;
+    for (int i = 0; i < A_Q; ++i) {
+        const int q = 64 * (A_Q * wave + i) + lane;
+        const int r = q / APR, p = (q & (APR - 1)) ^ swz(r);
+        const int rowoff = min(m0 + r, A.M - 1) * A.K * 2;
+        const int k = BK * (nst - 1) + 8 * p;
+        L.avoff[i] = rowoff + 16 * p;
+        L.atoff[i] = k < A.K ? rowoff + 2 * k : OOR;
     }
 #pragma unroll
-    for (int t = 0; t < SZ_INSTR; ++t) {
-        const int q = 64 * t + lane;
+    for (int t = 0; t < G::W_Q; ++t) {
+        const int q = 64 * (G::W_Q * wave + t) + lane;
+        const int r = min(q / G::PPR, BN - 1), p = q - (q / G::PPR) * G::PPR;
+        L.woff[t] = ((min(n0 + r, A.N - 1) * A.wpr * 4) & ~15) + 16 * p;
+    }
+#pragma unroll
+    for (int t = 0; t < SZ_Q; ++t) {
+        const int q = 64 * (SZ_Q * wave + t) + lane;
         const int r = (q >> 1) & (BN - 1), p = q & 1;
-        d.szoff[t] = ((min(n0 + r, A.N - 1) * A.G) & ~7) * 2 + 16 * p;
+        L.szoff[t] = ((min(n0 + r, A.N - 1) * A.G) & ~7) * 2 + 16 * p;
+    }
+    L.a_lds = A_OFF + A_Q * wave * 1024;
+    L.w_lds = W_OFF + G::W_Q * wave * 1024;
+    L.sz_lds = SZ_OFF<BITS> + SZ_Q * wave * 1024;
+}
+
+// Load schedule (scalars).  Group t holds activation stage t + 2 (slot (t + 2) % 3,
+// the stage clamped to the last) and, at even t, weight block j = t / 2 + 1
+// (buffer j & 1, clamped to the last) and window win + (j % rp != 0) into its
+// buffer: the window of block j when j starts one, else the next window ahead of
+// time (its buffer held a window that ended at least one block before j - 1, and
+// its live load comes later), so every even group moves the same bytes.  All
+// buffers written by group t were last read in stages <= t - 1, which every wave
+// has finished (LDS reads completed) when it meets barrier t.
+struct Sched {
+    int nst, nblk, rp;            // stages, weight blocks, blocks per window
+    int aslot;                    // (t + 2) % 3 of the next group
+    int blk_in_win, win;          // j % rp, j / rp of the next even group's block
+};
+
+struct Group {
+    uint32_t a_dst, w_dst, sz_dst;   // LDS bytes of the wave's first instructions
+    int a_soff, w_soff, sz_soff;     // scalar global byte offsets
+    bool a_tail;                     // activations: the partial last stage
+};
+
+template <int BITS, bool TAIL, bool EVEN>
+__device__ __forceinline__ void group_at(const Loads<BITS>& L, Sched& sc, int t, Group& g) {
+    const int sa = min(t + 2, sc.nst - 1);
+    g.a_tail = TAIL && sa == sc.nst - 1;
+    g.a_dst = L.a_lds + sc.aslot * TILE;
+    g.a_soff = g.a_tail ? 0 : BK * 2 * sa;
+    sc.aslot = sc.aslot == NSTAGE - 1 ? 0 : sc.aslot + 1;
+    if constexpr (EVEN) {
+        const int j = t / 2 + 1;
+        g.w_dst = L.w_lds + (j & 1) * WGeo<BITS>::BUF;
+        g.w_soff = min(j, sc.nblk - 1) * (32 * BITS);
+        const int w = sc.blk_in_win == 0 ? sc.win : sc.win + 1;
+        g.sz_dst = L.sz_lds + (w & 1) * SZ_BUF;
+        g.sz_soff = 2 * SZG * w;
+        const bool wrap = sc.blk_in_win + 1 == sc.rp;
+        sc.blk_in_win = wrap ? 0 : sc.blk_in_win + 1;
+        sc.win += wrap ? 1 : 0;
     }
 }
 
-template <int BITS>
-__device__ __forceinline__ void issue_w(const WLoader<BITS>& d, int j, char* lds) {
-    using G = WGeo<BITS>;
-    char* dst = lds + W_OFF + (j & 1) * G::BUF;
-#pragma unroll
-    for (int t = 0; t < G::INSTR; ++t)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.wr, (lds_void*)(dst + t * 1024), 16, d.woff[t], j * (32 * BITS), 0,
-                                                 0);
+// Slot k (a constant after unrolling) of a group: activation instruction k
+// (k < A_Q), then, in an even group, weight instruction k - A_Q, then the window.
+template <int BITS, bool TAIL, bool EVEN>
+__device__ __forceinline__ void issue_slot(const Loads<BITS>& L, const Group& g, int k, lds_t* lds) {
+    constexpr int WQ = WGeo<BITS>::W_Q;
+    if (k < A_Q) {
+        dma16(L.ar, lds, g.a_dst + k * 1024, TAIL && g.a_tail ? L.atoff[k] : L.avoff[k], g.a_soff);
+    } else if constexpr (EVEN) {
+        const int e = k - A_Q;
+        if (e < WQ) dma16(L.wr, lds, g.w_dst + e * 1024, L.woff[e], g.w_soff);
+        else if (e < WQ + SZ_Q) dma16(L.szr, lds, g.sz_dst + (e - WQ) * 1024, L.szoff[e - WQ], g.sz_soff);
+    }
 }
 
-template <int BITS>
-__device__ __forceinline__ void issue_sz(const WLoader<BITS>& d, int w, char* lds) {
-    char* dst = lds + SZ_OFF<BITS> + (w & 1) * SZ_BUF;
+template <int BITS, bool TAIL, bool EVEN>
+__device__ __forceinline__ void issue_group(const Loads<BITS>& L, const Group& g, lds_t* lds) {
 #pragma unroll
-    for (int t = 0; t < SZ_INSTR; ++t)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(t < SZ_INSTR / 2 ? d.sr : d.zr, (lds_void*)(dst + t * 1024), 16,
-                                                 d.szoff[t], 2 * SZG * w, 0, 0);
+    for (int k = 0; k < SLOTS; ++k) issue_slot<BITS, TAIL, EVEN>(L, g, k, lds);
+}
+
+// Wait until at most group t (all of it issued) is in flight: group t - 1 landed.
+template <int BITS, bool EVEN>
+__device__ __forceinline__ void wait_group() {
+    if constexpr (EVEN) vmcnt<A_Q + WGeo<BITS>::W_Q + SZ_Q>();
+    else vmcnt<A_Q>();
 }
 
 __device__ __forceinline__ _Float16 half_of(uint32_t v) {
@@ -215,15 +244,37 @@ __device__ __forceinline__ bool zero_is_small_int(uint32_t zbits) {
     return zf == __builtin_rintf(zf) && __builtin_fabsf(zf) < 1024.f;
 }
 
-// Whether every zero point of tile columns [n0, min(n0 + BN, N)) -- a contiguous
-// range of the zeros tensor, whose start is 16-byte aligned -- allows the
-// packed-fp16 form.
-__device__ __forceinline__ bool scan_zeros(const GemmArgs& A, int n0, int lane) {
+// Whether every zero point of columns [c0, min(c0 + 32, N)) -- a contiguous range of
+// the zeros tensor, whose start is 16-byte aligned -- allows the packed-fp16 form.
+// scan_issue loads the lane's first SCAN_U pieces before the prologue's loads go
+// out, so their latency hides behind them; scan_finish checks them and the rest.
+constexpr int SCAN_U = 8;
+struct ZScan {
+    u4 v[SCAN_U];
+};
+
+__device__ __forceinline__ void scan_issue(const GemmArgs& A, int c0, int lane, ZScan& zs) {
     const uint16_t* z = reinterpret_cast<const uint16_t*>(A.z);
-    const long beg = (long)n0 * A.G, end = (long)min(n0 + BN, A.N) * A.G;   // beg % 8 == 0
+    const long beg = (long)c0 * A.G, end = (long)min(c0 + 32, A.N) * A.G;   // beg % 8 == 0
+#pragma unroll
+    for (int u = 0; u < SCAN_U; ++u) {
+        const long i = beg + 8 * lane + 512 * u;
+        zs.v[u] = i + 8 <= end ? *reinterpret_cast<const u4*>(z + i) : u4{0, 0, 0, 0};
+    }
+}
+
+__device__ __forceinline__ bool scan_finish(const GemmArgs& A, int c0, int lane, const ZScan& zs) {
+    const uint16_t* z = reinterpret_cast<const uint16_t*>(A.z);
+    const long beg = (long)c0 * A.G, end = (long)min(c0 + 32, A.N) * A.G;
     bool ok = true;
+#pragma unroll
+    for (int u = 0; u < SCAN_U; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            ok &= zero_is_small_int(zs.v[u][j] & 0xFFFFu) & zero_is_small_int(zs.v[u][j] >> 16);
     for (long i = beg + 8 * lane; i < end; i += 8 * 64) {
         if (i + 8 <= end) {
+            if (i < beg + 512 * SCAN_U) continue;      // preloaded
             const u4 v = *reinterpret_cast<const u4*>(z + i);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -236,18 +287,11 @@ __device__ __forceinline__ bool scan_zeros(const GemmArgs& A, int n0, int lane) 
 }
 
 // ------------------------------------------------------------------ compute
-// A compute wave owns a 128 x 32 slab of the tile: every row, columns
-// 32 wn .. 32 wn + 31 (wn = wave), so each column is dequantized by exactly one
-// wave.  Lane (r32 = lane & 31, hk = lane >> 5) holds column r32's B operand and
-// the A operands of rows 32 a + r32 (a < 4).  Step ks of a stage gives lane half hk
-// the codes 32 hk + 8 ks .. +7 (octet ks of chunk 2 s + hk), so a lane needs one
-// packed chunk and one (scale, zero) pair per stage.
-
-// The lane's two packed chunks of a stage and their scales and zeros as raw fp16 bits.
+// The lane's packed chunk of a stage and its scale and zero as raw fp16 bits.
 template <int BITS>
 struct WStage {
-    uint32_t w[2][BITS];
-    uint32_t s[2], z[2];
+    uint32_t w[BITS];
+    uint32_t s, z;
 };
 
 // Octet o (codes 8o .. 8o+7) of a chunk as 4 packed pairs (1024 + q, exact;
@@ -298,19 +342,17 @@ template <> struct Octet<3> {
     }
 };
 
-// B operand of step ks: the lane's codes 64 hk + 8 ks .. +7 of its column (octet
-// ks & 3 of its chunk ks >> 2).  FAST: every zero point of the tile is an integer
-// below 1024 in magnitude.
+// B operand of the wave's step kq: octet kq of the lane's chunk.  FAST: every zero
+// point of the wave's columns is an integer below 1024 in magnitude.
 template <int BITS, bool FAST>
-__device__ __forceinline__ u4 dequant_octet(const WStage<BITS>& r, int ks, uint32_t g) {
-    const int c = ks >> 2;
-    const float zf = (float)half_of(r.z[c]);
+__device__ __forceinline__ u4 dequant_octet(const WStage<BITS>& r, int kq, uint32_t g) {
+    const float zf = (float)half_of(r.z);
     const _Float16 cz = (_Float16)(1024.f + zf);      // exact when FAST: an integer below 2048
-    const _Float16 sh = half_of(r.s[c]);
+    const _Float16 sh = half_of(r.s);
     const h2 c2 = {cz, cz}, s2 = {sh, sh};
     const float sf = (float)sh;
     uint32_t h[4];
-    Octet<BITS>::run(r.w[c], ks & 3, g, h);
+    Octet<BITS>::run(r.w, kq, g, h);
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -327,51 +369,61 @@ __device__ __forceinline__ u4 dequant_octet(const WStage<BITS>& r, int ks, uint3
     return u4{o[0], o[1], o[2], o[3]};
 }
 
-// A operands of step ks of stage s: af[a] = row 32 a + r32, codes 64 hk + 8 ks .. +7.
-__device__ __forceinline__ void read_a(const char* lds, int s, int ks, int aoff, int hk, int sw, u4 (&af)[4]) {
-    const u4* at = reinterpret_cast<const u4*>(lds + A_OFF + (s % NSTAGE) * TILE);
-    const int p = (8 * hk + ks) ^ sw;
-#pragma unroll
-    for (int a = 0; a < 4; ++a) af[a] = at[aoff + a * 32 * APR + p];     // 32 rows apart
-}
-
-// Per-lane constants of a compute wave's column (tile row wn * 32 + r32).
+// Per-lane constants of a wave's column and its LDS reads.
 struct ColInfo {
-    int woff;         // LDS byte of the row in a weight buffer (row * PITCH + phase)
-    int soff;         // LDS byte of the row's scale span in a window buffer
+    int wlane;        // LDS byte of the lane's chunk in weight buffer 0, stage 0 of a block
+    int szlane;       // LDS byte of the column's span in window buffer 0 plus (col * G) & 7 halves
+    int soff;         // LDS byte of the row's span in a window buffer (general group sizes)
+    int cix;          // the lane's chunk within a stage: 2 hk + kh
     long cg;          // col * G
+    int aaddr[KSTEPS];   // LDS byte of the lane's A operand of step kq within a stage (row block 0)
 };
 
-// The lane's chunks (4 s + 2 hk + c, c < 2: chunks 4 (s % WBLK) + 2 hk + c of block
-// s / WBLK) and their (scale, zero) of stage s, as the weight loader filled its
-// buffer and window.
-template <int BITS>
-__device__ __forceinline__ void read_w(const GemmArgs& A, const char* lds, int s, const ColInfo& ci, int hk,
-                                       WStage<BITS>& r) {
-    const int j = s / WBLK;
-    const char* p = lds + W_OFF + (j & 1) * WGeo<BITS>::BUF + (4 * (s % WBLK) + 2 * hk) * (4 * BITS) + ci.woff;
-    if constexpr (BITS == 4) {
-        const u4 v0 = *reinterpret_cast<const u4*>(p), v1 = *reinterpret_cast<const u4*>(p + 16);
-        r.w[0][0] = v0.x; r.w[0][1] = v0.y; r.w[0][2] = v0.z; r.w[0][3] = v0.w;
-        r.w[1][0] = v1.x; r.w[1][1] = v1.y; r.w[1][2] = v1.z; r.w[1][3] = v1.w;
-    } else if constexpr (BITS == 2) {
-        const u4 v = *reinterpret_cast<const u4*>(p);
-        r.w[0][0] = v.x; r.w[0][1] = v.y; r.w[1][0] = v.z; r.w[1][1] = v.w;
-    } else {
-        const u2 v0 = *reinterpret_cast<const u2*>(p), v1 = *reinterpret_cast<const u2*>(p + 8);
-        const u2 v2 = *reinterpret_cast<const u2*>(p + 16);
-        r.w[0][0] = v0.x; r.w[0][1] = v0.y; r.w[0][2] = v1.x;
-        r.w[1][0] = v1.y; r.w[1][1] = v2.x; r.w[1][2] = v2.y;
-    }
-    const int w = (int)(fdiv((uint32_t)(j * 256), A.divG) >> 3);           // j / (gs / 32)
-    const char* sb = lds + SZ_OFF<BITS> + (w & 1) * SZ_BUF;
-    const long span = (ci.cg + SZG * w) & ~7L;
+// A operands of the wave's step kq of the stage in slot `slot`: af[a] = row 32 a +
+// r32 (row blocks are 32 rows = 8 KB apart: immediate offsets).
+__device__ __forceinline__ void read_a(const lds_t* lds, int slot, int kq, const ColInfo& ci, u4 (&af)[4]) {
+    typedef __attribute__((address_space(3))) const u4 l4;
+    const lds_t* at = lds + slot * TILE + ci.aaddr[kq];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const int gi = (int)fdiv((uint32_t)((4 * s + 2 * hk + c) * 32), A.divG);
-        const uint16_t* q = reinterpret_cast<const uint16_t*>(sb + ci.soff) + (int)(ci.cg + gi - span);
-        r.s[c] = q[0];
-        r.z[c] = q[BN * 16];      // the zeros follow the scales' 128 rows x 32 bytes
+    for (int a = 0; a < 4; ++a) af[a] = *reinterpret_cast<l4*>(at + a * 32 * APR * 16);
+}
+
+// The lane's chunk of stage s (chunk 4 (s % WBLK) + 2 hk + kh of block s / WBLK)
+// and its (scale, zero).  GS128: the group size is 128, so the chunk's group is
+// stage s's, at a lane-independent offset in window s >> 3.
+template <int BITS, bool GS128>
+__device__ __forceinline__ void read_w(const GemmArgs& A, const lds_t* lds, int s, const ColInfo& ci,
+                                       WStage<BITS>& r) {
+    typedef __attribute__((address_space(3))) const u4 l4;
+    typedef __attribute__((address_space(3))) const u2 l2;
+    typedef __attribute__((address_space(3))) const uint16_t l16;
+    const int j = s / WBLK;
+    const lds_t* p = lds + (j & 1) * WGeo<BITS>::BUF + (s % WBLK) * (16 * BITS) + ci.wlane;
+    if constexpr (BITS == 4) {
+        const u4 v = *reinterpret_cast<l4*>(p);
+        r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+    } else if constexpr (BITS == 3) {
+        // a 12-byte chunk is only word aligned
+        typedef __attribute__((address_space(3))) const uint32_t l1;
+        r.w[0] = *reinterpret_cast<l1*>(p);
+        r.w[1] = *reinterpret_cast<l1*>(p + 4);
+        r.w[2] = *reinterpret_cast<l1*>(p + 8);
+    } else {
+        const u2 v = *reinterpret_cast<l2*>(p);
+        r.w[0] = v.x; r.w[1] = v.y;
+    }
+    if constexpr (GS128) {
+        l16* q = reinterpret_cast<l16*>(lds + ((s >> 3) & 1) * SZ_BUF + 2 * (s & 7) + ci.szlane);
+        r.s = q[0];
+        r.z = q[BN * 16];      // the zeros follow the scales' 128 rows x 32 bytes
+    } else {
+        const int w = (int)(fdiv((uint32_t)(j * 256), A.divG) >> 3);       // j / (gs / 32)
+        const lds_t* sb = lds + SZ_OFF<BITS> + (w & 1) * SZ_BUF;
+        const long span = (ci.cg + SZG * w) & ~7L;
+        const int gi = (int)fdiv((uint32_t)((4 * s + ci.cix) * 32), A.divG);
+        l16* q = reinterpret_cast<l16*>(sb + ci.soff) + (int)(ci.cg + gi - span);
+        r.s = q[0];
+        r.z = q[BN * 16];
     }
 }
 
@@ -383,125 +435,132 @@ __device__ __forceinline__ void mma_step(const u4 (&af)[4], const u4& bw, f16x (
                                                         *reinterpret_cast<const h8*>(&bw), acc[a], 0, 0, 0);
 }
 
-// One stage, as a software pipeline over its 8 k-steps: the A operands of step ks
-// are read two steps ahead (a[ks & 3] of four rotating sets) and its B operand
-// dequantized one step ahead, so each step's 4 MFMAs find their operands in
-// registers while the dequant VALU of the next step and the LDS reads of the step
-// after it go out between them.  On entry a[0], a[1] hold steps 0 and 1, bw step
-// 0, wc the chunks of stage s.  NEXT: the wave meets barrier s + 1 after step 5 --
-// every read of stage s's activation slot has been issued by then, and
-// barrier_lds waits for them, so the loaders may refill it -- then reads steps 0
-// and 1 of stage s + 1 and its chunks (wn), and dequantizes its step 0, leaving
-// the entry state of stage s + 1.
-template <int BITS, bool FAST, bool NEXT>
-__device__ __forceinline__ void run_stage(const GemmArgs& A, const char* lds, int s, const ColInfo& ci, int hk,
-                                          int sw, int aoff, uint32_t g, u4 (&a)[4][4], u4& bw,
-                                          const WStage<BITS>& wc, WStage<BITS>& wn, f16x (&acc)[4]) {
+// Everything a stage needs besides its operands.
+template <int BITS>
+struct Ctx {
+    const GemmArgs& A;
+    lds_t* lds;
+    const ColInfo& ci;
+    uint32_t g;
+    const Loads<BITS>& L;
+    Sched& sc;
+    int cslot;                    // slot of the stage being computed
+};
+
+// The wave's four k-steps of stage s as a software pipeline: the A operands of
+// step kq are read two steps ahead (a[kq & 3] of four rotating sets) and its B
+// operand dequantized one step ahead.  On entry a[0], a[1] hold steps 0 and 1, bw
+// step 0, wc the chunk of stage s, gc the resolved group s.  NEXT: steps 0 and 1
+// issue slots 4 .. 7 of group s; after step 1 (every read of stage s's activation
+// slot issued; barrier_lds completes them) the wave waits for its group s - 1,
+// meets barrier s + 1 and resolves group s + 1 into gn; steps 2 and 3 issue its
+// slots 0 .. 3 (activation stage s + 3 into the slot of stage s), read steps 0 and
+// 1 of stage s + 1 and its chunk (wn), and dequantize its step 0, leaving the entry
+// state of stage s + 1.  The last stage (!NEXT) issues nothing.  ODD: s is odd.
+template <int BITS, bool TAIL, bool GS128, bool FAST, bool NEXT, bool ODD>
+__device__ __forceinline__ void run_stage(Ctx<BITS>& c, int s, u4 (&a)[4][4], u4& bw, const WStage<BITS>& wc,
+                                          WStage<BITS>& wn, const Group& gc, Group& gn, f16x (&acc)[4]) {
+    const int nslot = c.cslot == NSTAGE - 1 ? 0 : c.cslot + 1;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-        if (ks + 2 < 8) read_a(lds, s, ks + 2, aoff, hk, sw, a[(ks + 2) & 3]);
-        else if (NEXT) read_a(lds, s + 1, ks - 6, aoff, hk, sw, a[(ks + 2) & 3]);
-        if (NEXT && ks == 6) read_w<BITS>(A, lds, s + 1, ci, hk, wn);
+    for (int kq = 0; kq < KSTEPS; ++kq) {
+        if (kq + 2 < KSTEPS) read_a(c.lds, c.cslot, kq + 2, c.ci, a[(kq + 2) & 3]);
+        else if (NEXT) read_a(c.lds, nslot, kq - 2, c.ci, a[(kq + 2) & 3]);
+        if (NEXT && kq == 2) read_w<BITS, GS128>(c.A, c.lds, s + 1, c.ci, wn);
         u4 bwn = bw;
-        if (ks + 1 < 8) bwn = dequant_octet<BITS, FAST>(wc, ks + 1, g);
-        else if (NEXT) bwn = dequant_octet<BITS, FAST>(wn, 0, g);
-        mma_step(a[ks & 3], bw, acc);
+        if (kq + 1 < KSTEPS) bwn = dequant_octet<BITS, FAST>(wc, kq + 1, c.g);
+        else if (NEXT) bwn = dequant_octet<BITS, FAST>(wn, 0, c.g);
+        mma_step(a[kq & 3], bw, acc);
         bw = bwn;
-        if (NEXT && ks == 5) barrier_lds();       // stage s + 1 published
+        if (NEXT && kq <= 1) {
+            issue_slot<BITS, TAIL, !ODD>(c.L, gc, 4 + 2 * kq, c.lds);
+            issue_slot<BITS, TAIL, !ODD>(c.L, gc, 5 + 2 * kq, c.lds);
+        }
+        if (NEXT && kq == 1) {
+            wait_group<BITS, !ODD>();             // group s (parity of s) may stay in flight
+            barrier_lds();                        // stage s + 1 published
+            group_at<BITS, TAIL, ODD>(c.L, c.sc, s + 1, gn);
+        }
+        if (NEXT && kq >= 2) {
+            issue_slot<BITS, TAIL, ODD>(c.L, gn, 2 * (kq - 2), c.lds);
+            issue_slot<BITS, TAIL, ODD>(c.L, gn, 2 * (kq - 2) + 1, c.lds);
+        }
     }
+    c.cslot = nslot;
 }
 
-// The compute waves' stages, unrolled by two so the chunk registers of stage s and
-// stage s + 1 alternate without copies; the last stage is peeled.
-template <int BITS, bool FAST>
-__device__ __forceinline__ void compute_loop(const GemmArgs& A, const char* lds, int nst, const ColInfo& ci, int hk,
-                                             int sw, int aoff, uint32_t g, f16x (&acc)[4]) {
+// The stages, unrolled by two so the chunk and group registers of stage s and
+// stage s + 1 alternate without copies and the load-group parity is static; the
+// last stage is peeled.
+template <int BITS, bool TAIL, bool GS128, bool FAST>
+__device__ __forceinline__ void compute_loop(Ctx<BITS>& c, int nst, Group& g0, f16x (&acc)[4]) {
     u4 a[4][4], bw;
     WStage<BITS> w0, w1;
-    barrier_lds();                                // stage 0 published
-    read_a(lds, 0, 0, aoff, hk, sw, a[0]);
-    read_a(lds, 0, 1, aoff, hk, sw, a[1]);
-    read_w<BITS>(A, lds, 0, ci, hk, w0);
-    bw = dequant_octet<BITS, FAST>(w0, 0, g);
+    Group g1;
+    read_a(c.lds, 0, 0, c.ci, a[0]);
+    read_a(c.lds, 0, 1, c.ci, a[1]);
+    read_w<BITS, GS128>(c.A, c.lds, 0, c.ci, w0);
+    bw = dequant_octet<BITS, FAST>(w0, 0, c.g);
     int s = 0;
     for (; s + 2 < nst; s += 2) {
-        run_stage<BITS, FAST, true>(A, lds, s, ci, hk, sw, aoff, g, a, bw, w0, w1, acc);
-        run_stage<BITS, FAST, true>(A, lds, s + 1, ci, hk, sw, aoff, g, a, bw, w1, w0, acc);
+        run_stage<BITS, TAIL, GS128, FAST, true, false>(c, s, a, bw, w0, w1, g0, g1, acc);
+        run_stage<BITS, TAIL, GS128, FAST, true, true>(c, s + 1, a, bw, w1, w0, g1, g0, acc);
     }
     if (s + 1 < nst) {
-        run_stage<BITS, FAST, true>(A, lds, s, ci, hk, sw, aoff, g, a, bw, w0, w1, acc);
-        run_stage<BITS, FAST, false>(A, lds, s + 1, ci, hk, sw, aoff, g, a, bw, w1, w0, acc);
+        run_stage<BITS, TAIL, GS128, FAST, true, false>(c, s, a, bw, w0, w1, g0, g1, acc);
+        run_stage<BITS, TAIL, GS128, FAST, false, true>(c, s + 1, a, bw, w1, w0, g1, g0, acc);
     } else {
-        run_stage<BITS, FAST, false>(A, lds, s, ci, hk, sw, aoff, g, a, bw, w0, w1, acc);
+        run_stage<BITS, TAIL, GS128, FAST, false, false>(c, s, a, bw, w0, w1, g0, g1, acc);
     }
 }
 
-template <int BITS>
-__global__ void __launch_bounds__(THREADS) gemm_f16_kernel(const GemmArgs A) {
-    extern __shared__ __attribute__((aligned(16))) char lds[];
+template <int BITS, bool TAIL, bool GS128>
+__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_f16_kernel(const GemmArgs A) {
+    extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+    lds_t* lds = (lds_t*)lds_raw;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int slab = wave & 3, kh = wave >> 2;    // column slab, k half of every stage
     const int mtiles = (A.M + BM - 1) / BM;
     const int m0 = (blockIdx.x % mtiles) * BM, n0 = (blockIdx.x / mtiles) * BN;
     const int nst = (A.K + BK - 1) / BK;
 
-    if (wave == 4 || wave == 5) {
-        // activation loaders: stages s+1 .. s+NSTAGE-2 stay in flight while stage s is
-        // published
-        ALoader da;
-        a_setup(A, m0, wave - 4, lane, da);
-        for (int j = 0; j < NSTAGE - 1; ++j) issue_a(A, da, j, nst, lds);
-        barrier_lds();                            // weight block 0 and the zero-point flag
-        for (int s = 0; s < nst; ++s) {
-            vmcnt<A_INSTR * (NSTAGE - 2)>();      // this loader's half of stage s landed
-            barrier_lds();                        // publish stage s; every wave is past stage s-1
-            issue_a(A, da, s + NSTAGE - 1, nst, lds);   // into the slot of stage s-1
-        }
-        vmcnt<0>();                               // the surplus stages land before the wave ends
-        return;
-    }
-    if (wave == 6) {
-        // weight loader: block j + 1 (and the scale window it starts) is issued at
-        // the first barrier of block j and has landed before the first barrier of
-        // block j + 1
-        const int nblk = (nst + WBLK - 1) / WBLK, rp = A.gs >> 5;
-        WLoader<BITS> dw;
-        w_setup<BITS>(A, n0, lane, dw);
-        issue_w<BITS>(dw, 0, lds);
-        issue_sz<BITS>(dw, 0, lds);
-        const bool fast = scan_zeros(A, n0, lane);
-        if (lane == 0) *reinterpret_cast<int*>(lds + FLAG_OFF<BITS>) = fast;
-        vmcnt<0>();
-        barrier_lds();                            // weight block 0 and the zero-point flag
-        for (int s = 0; s < nst; ++s) {
-            if (s % WBLK == 0) vmcnt<0>();        // block s / WBLK landed: published by barrier s
-            barrier_lds();                        // every wave is past stage s-1
-            if (s % WBLK == 0) {
-                const int j = s / WBLK + 1;       // the next block: its buffer held block j - 2
-                if (j < nblk) {
-                    issue_w<BITS>(dw, j, lds);
-                    if (j % rp == 0) issue_sz<BITS>(dw, j / rp, lds);
-                }
-            }
-        }
-        vmcnt<0>();
-        return;
-    }
+    // prologue: the zero scan's loads, then weight block 0, window 0 and stages 0, 1
+    ZScan zs;
+    scan_issue(A, n0 + slab * 32, lane, zs);
+    Loads<BITS> L;
+    loads_setup<BITS>(A, m0, n0, nst, wave, lane, L);
+    Sched sc;
+    sc.nst = nst;
+    sc.nblk = (nst + WBLK - 1) / WBLK;
+    sc.rp = A.gs >> 5;
+    sc.aslot = 0;
+    sc.blk_in_win = 0;
+    sc.win = 0;
+    Group g0;
+    group_at<BITS, TAIL, true>(L, sc, -2, g0);    // stage 0, block 0, window 0
+    issue_group<BITS, TAIL, true>(L, g0, lds);
+    group_at<BITS, TAIL, false>(L, sc, -1, g0);   // stage 1
+    issue_group<BITS, TAIL, false>(L, g0, lds);
 
-    // compute wave: the 128 x 32 slab at columns wn * 32 of the tile
-    const int wn = wave;
+    // the 128 x 32 slab at columns slab * 32 of the tile, k half kh of every stage
     const int r32 = lane & 31;
     const int hk = lane >> 5;
     ColInfo ci;
     {
-        const int r = wn * 32 + r32;
+        const int r = slab * 32 + r32;
         const int col = min(n0 + r, A.N - 1);
         const uintptr_t row = reinterpret_cast<uintptr_t>(A.w) + (uintptr_t)col * A.wpr * 4;
-        ci.woff = r * WGeo<BITS>::PITCH + (int)(row & 15);
-        ci.soff = r * 32;
+        ci.cix = 2 * hk + kh;
+        ci.wlane = W_OFF + r * WGeo<BITS>::PITCH + (int)(row & 15) + ci.cix * (4 * BITS);
         ci.cg = (long)col * A.G;
+        ci.soff = r * 32;
+        ci.szlane = SZ_OFF<BITS> + r * 32 + 2 * (int)(ci.cg & 7);
+#pragma unroll
+        for (int kq = 0; kq < KSTEPS; ++kq)
+            ci.aaddr[kq] = A_OFF + r32 * APR * 16 + 16 * ((8 * hk + KSTEPS * kh + kq) ^ swz(r32));
     }
-    const uint32_t g = magic_vreg();
+    const bool fast = scan_finish(A, n0 + slab * 32, lane, zs);
 
     f16x acc[4];
 #pragma unroll
@@ -509,18 +568,36 @@ __global__ void __launch_bounds__(THREADS) gemm_f16_kernel(const GemmArgs A) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[a][v] = 0.f;
 
-    const int aoff = r32 * APR;                   // u4 index of row r32 in a stage
-    const int sw = swz(r32);                      // rows are 32-aligned + r32
+    vmcnt<A_Q>();                                 // block 0, window 0 and stage 0 landed
+    barrier_lds();                                // barrier 0: published
+    group_at<BITS, TAIL, true>(L, sc, 0, g0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) issue_slot<BITS, TAIL, true>(L, g0, k, lds);
 
-    barrier_lds();                                // weight block 0 and the zero-point flag
-    if (__builtin_amdgcn_readfirstlane(*reinterpret_cast<const int*>(lds + FLAG_OFF<BITS>)))
-        compute_loop<BITS, true>(A, lds, nst, ci, hk, sw, aoff, g, acc);
-    else
-        compute_loop<BITS, false>(A, lds, nst, ci, hk, sw, aoff, g, acc);
+    Ctx<BITS> c{A, lds, ci, magic_vreg(), L, sc, 0};
+    if (fast) compute_loop<BITS, TAIL, GS128, true>(c, nst, g0, acc);
+    else compute_loop<BITS, TAIL, GS128, false>(c, nst, g0, acc);
+    vmcnt<0>();                                   // the surplus loads land before the LDS is reused
+
+    // the two k halves' partial sums meet in LDS (the stage slots are free once every
+    // wave is past its last stage): the kh = 1 wave of a slab writes, the kh = 0 wave
+    // adds and stores
+    typedef __attribute__((address_space(3))) f16x lacc;
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));    // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    lds_t* red = lds + slab * (4 * 64 * 64) + lane * 64;
+    if (kh == 1) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) *reinterpret_cast<lacc*>(red + a * 64 * 64) = acc[a];
+    }
+    barrier_lds();
+    if (kh == 1) return;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) acc[a] += *reinterpret_cast<lacc*>(red + a * 64 * 64);
 
     // D layout of a 32x32 block: lane (j = lane & 31, h = lane >> 5), register
     // 4q + r holds row 8q + 4h + r, column j
-    const int n = n0 + wn * 32 + r32;
+    const int n = n0 + slab * 32 + r32;
     if (n >= A.N) return;
     const float bias = A.b ? load_f<DT_F16>(A.b, n) : 0.f;
 #pragma unroll
@@ -534,20 +611,18 @@ __global__ void __launch_bounds__(THREADS) gemm_f16_kernel(const GemmArgs A) {
 }
 
 template <int BITS>
-const void* kernel_for() {
-    return reinterpret_cast<const void*>(&gemm_f16_kernel<BITS>);
-}
-
-template <int BITS>
-int lds_for() {
-    return LDS_BYTES<BITS>;
+const void* kernel_for(bool tail, bool gs128) {
+    return tail ? (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, true>)
+                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, false>))
+                : (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, true>)
+                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, false>));
 }
 
 }  // namespace
 
 bool gemm_f16_supported(const GemmArgs& A) {
     // 16-byte activation pieces, whole octets before K, 16-byte aligned packed /
-    // scale / zero bases (the loaders' aligned pieces and the zero scan), windows of
+    // scale / zero bases (the loads' aligned pieces and the zero scan), windows of
     // 8 groups spanning whole weight blocks (group size a multiple of 32), tensors
     // within the 32-bit range of a buffer descriptor
     const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -557,8 +632,10 @@ bool gemm_f16_supported(const GemmArgs& A) {
 }
 
 hipError_t launch_gemm_f16(const GemmArgs& A, hipStream_t stream) {
-    const void* f = A.bits == 2 ? kernel_for<2>() : (A.bits == 3 ? kernel_for<3>() : kernel_for<4>());
-    const int lds = A.bits == 2 ? lds_for<2>() : (A.bits == 3 ? lds_for<3>() : lds_for<4>());
+    const bool tail = A.K % BK != 0, gs128 = A.gs == 128;
+    const void* f = A.bits == 2 ? kernel_for<2>(tail, gs128) : (A.bits == 3 ? kernel_for<3>(tail, gs128)
+                                                                         : kernel_for<4>(tail, gs128));
+    const int lds = A.bits == 2 ? LDS_BYTES<2> : (A.bits == 3 ? LDS_BYTES<3> : LDS_BYTES<4>);
     hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     const int tiles = ((A.M + BM - 1) / BM) * ((A.N + BN - 1) / BN);

@@ -247,6 +247,22 @@ def test_prefill_group_sizes(hip, gs):
     close(packed_linear(x, w), gemm_ref(x, d, torch.float16, 3, 640, gs), torch.float16)
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("K,cols", [(400, 40), (1024, 300)])
+def test_prefill_fractional_zeros(hip, bits, K, cols):
+    """Zero points that are not integers (other producers' formats) take the fp32
+    dequant: here on the first `cols` columns only, so one tile mixes column slabs
+    of both forms (and with K=400 the partial last stage)."""
+    _, _, _, d = make(300, K, bits, torch.float16)
+    d = dict(d)
+    z = d["zeros"].clone()
+    z[:cols] = z[:cols] + 0.375
+    d["zeros"] = z
+    w = from_packed_dict(d, "cuda", torch.float16)
+    x = randx(130, K, torch.float16)
+    close(packed_linear(x, w), gemm_ref(x, d, torch.float16, bits, K, 128), torch.float16)
+
+
 # ------------------------------------------------------------------ streams and graphs
 
 def test_non_default_stream(hip):
