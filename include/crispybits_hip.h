@@ -62,7 +62,7 @@ int cbk_tile_n(void);
 int cbk_max_rho(int device, int bits, int mode, int* out);
 
 /* Decode kernel families reported by cbk_decode_plan. */
-enum { CBK_KERNEL_STREAM = 1, CBK_KERNEL_BSTREAM = 2, CBK_KERNEL_MFMA = 3, CBK_KERNEL_GENERIC = 4 };
+enum { CBK_KERNEL_STREAM = 1, CBK_KERNEL_BSTREAM = 2, CBK_KERNEL_MFMA = 3, CBK_KERNEL_GENERIC = 4, CBK_KERNEL_BATCH = 5 };
 
 /* Additive policy query (no counterpart in the reference, whose tuner infers launches from
  * (split_k, rho), autotune.py:55-88): the launch a decode call with these arguments makes,

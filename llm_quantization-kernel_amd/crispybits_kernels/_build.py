@@ -23,12 +23,19 @@ LIB_NAME = "libcrispybits_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = os.environ.get("CRISPYBITS_ARCH", "gfx950")
 
-SOURCES = ["abi.cpp", "gemv_mfma.hip", "gemv_stream.hip", "gemv_generic.hip", "gemm.hip", "gemm_f16.hip", "unpack.hip", "quant.hip"]
+SOURCES = ["abi.cpp", "gemv_mfma.hip", "gemv_stream.hip", "gemv_batch.hip", "gemv_generic.hip", "gemm.hip", "gemm_f16.hip",
+           "unpack.hip", "quant.hip"]
 
 # -packed-fp32-ops is disabled: the kernels never rely on v_pk_*_f32.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-munsafe-fp-atomics",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-result", "-I" + CSRC, "-I" + os.path.join(os.path.dirname(ROOT), "include")]
+
+
+# Per-file additions.  gemv_batch.hip: no SLP vectorisation, which would pack each
+# prefetched (scale, zero) pair into one register and so wait for both loads where the
+# pair is formed, long before the values are used.
+FILE_FLAGS = {"gemv_batch.hip": ["-fno-slp-vectorize"]}
 
 
 def _hipcc() -> str:
@@ -40,7 +47,7 @@ def _hipcc() -> str:
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [_hipcc(), *HIP_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [_hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

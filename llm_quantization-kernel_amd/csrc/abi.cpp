@@ -424,6 +424,52 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     return bp;
 }
 
+// Batched plan (gemv_batch.hip), batch 3..16 in one dispatch, taken where the bstream
+// kernel would split K (its partials then need a reduce launch): the bstream kernel's
+// conditions (fp16 x with 16-byte pieces, group sizes that are multiples of 128,
+// 32-bit offsets, every 16-row block inside one projection; mixed widths: every
+// workgroup's rows).  A workgroup of 15 or 16 waves fills a CU (128 VGPRs per wave), so
+// rw (row blocks per workgroup: 1, 2 or 3) takes the fewest workgroup rounds over the
+// CUs and among equal rounds the smallest rw: every workgroup stages all of K's
+// activations, so fewer, wider workgroups only pay when they save a round.  Gate-up
+// needs an even rw (one gate and one up block per 16 pair rows).  split_k is ignored:
+// the kernel never splits K.
+struct BatchPlan {
+    bool ok = false;
+    int rw = 1, grid = 0, lds = 0;
+};
+
+BatchPlan plan_batch(const GemvArgs& A, int dtype, int mode, bool mixed, int cus) {
+    BatchPlan bp;
+    const int64_t lim = INT32_MAX;
+    bool ok = A.M >= 3 && A.M <= 16 && dtype == CBK_F16 && A.gs % 128 == 0 && A.K % 8 == 0 &&
+              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim && cus > 0;
+    for (int i = 0; i < 3; ++i)
+        ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
+    if (mode == CBK_MODE_QKV) ok = ok && A.p[0].n % 16 == 0 && A.p[1].n % 16 == 0;
+    if (!ok) return bp;
+    int64_t best_rounds = INT64_MAX;
+    // one workgroup per CU (15 or 16 waves); the fewest rounds, then the smallest rw
+    for (int rw : {1, 2, 3}) {
+        if (mode == CBK_MODE_GATEUP && rw % 2) continue;
+        const int rb = 16 * rw;
+        if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) continue;
+        const int lds = batch_lds_bytes(A.M, rw);
+        if (lds > LDS_BUDGET) continue;
+        const int64_t grid = ceil_div(A.V, rb);
+        if (grid >= lim) continue;
+        const int64_t rounds = ceil_div(grid, (int64_t)cus);
+        if (rounds < best_rounds) {
+            best_rounds = rounds;
+            bp.rw = rw;
+            bp.grid = (int)grid;
+            bp.lds = lds;
+            bp.ok = true;
+        }
+    }
+    return bp;
+}
+
 // Kernels (per device) whose dynamic-LDS limit has been raised to the whole budget.  The
 // limit is set once, to LDS_BUDGET, and never lowered, so launches of one kernel with
 // different LDS sizes from several threads cannot undercut each other.
@@ -481,7 +527,23 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         L.P = sp.P;
         return L;
     }
+    // batch 3..16: the K-split streaming kernel where it needs no split (one dispatch, the
+    // faster kernel there), the whole-K batch kernel where it would split K (one dispatch
+    // instead of a split and a reduce launch)
     const BStreamPlan bp = plan_bstream(A, dtype, mode, mixed, split_k);
+    const BatchPlan bt = (bp.ok && bp.P == 1) ? BatchPlan{} : plan_batch(A, dtype, mode, mixed, cus);
+    if (bt.ok) {
+        A.P = 1;
+        A.st_rw = bt.rw;
+        A.divG = make_fastdiv((uint32_t)(A.gs / 128));
+        L.family = CBK_KERNEL_BATCH;
+        L.f = gemv_batch_kernel_for(mode, A.p[0].bits, mixed, bt.rw);
+        L.grid = bt.grid;
+        L.block = batch_threads(bt.rw);
+        L.lds = bt.lds;
+        L.P = 1;
+        return L;
+    }
     if (bp.ok) {
         A.P = bp.P;
         A.st_ks = bp.ks;

@@ -29,6 +29,14 @@ const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb);
 // over 16 rows and one K slice of bsu (4 or 8) units.
 const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu);
 
+// gemv_batch.hip: batch 3..16, fp16, group size % 128 == 0, one dispatch.  A workgroup of
+// batch_threads(rw) threads (16 waves; 15 for rw = 3) owns rw (1, 2 or 3; 2 for gate-up)
+// blocks of 16 virtual rows over all of K, taken in phases of one 128-code unit per wave
+// whose converted activations it stages once.
+const void* gemv_batch_kernel_for(int mode, int bits, bool mixed, int rw);
+int batch_threads(int rw);
+int batch_lds_bytes(int M, int rw);
+
 // gemv_generic.hip: any dtype / group size; 32 virtual rows x 1 batch row per job.
 constexpr int GENERIC_THREADS = 256;
 constexpr int GENERIC_ROWS = 32;

@@ -325,8 +325,8 @@ py::tuple decode_plan(py::object dtype, int64_t batch, int64_t in_features, int6
     int32_t out[6] = {0, 0, 0, 0, 0, 0};
     ok(cbk_decode_plan(dt, batch, in_features, (int)group_size, ns[0], ns[1], ns[2], (int)bs[0], (int)bs[1],
                        (int)bs[2], kind_code(kind), (int)split_k, (int)rho, current_device(), out));
-    static const char* families[] = {"?", "stream", "bstream", "mfma", "generic"};
-    const char* fam = out[0] >= 1 && out[0] <= 4 ? families[out[0]] : "?";
+    static const char* families[] = {"?", "stream", "bstream", "mfma", "generic", "batch"};
+    const char* fam = out[0] >= 1 && out[0] <= 5 ? families[out[0]] : "?";
     return py::make_tuple(fam, out[1], out[2], out[3], out[4], out[5]);
 }
 

@@ -305,6 +305,20 @@ def test_baseline_gemv_shapes(hip, bits, K, N, M):
     close(packed_linear(x, w), ref_linear(x, W64), torch.float16)
 
 
+@pytest.mark.parametrize("M", [3, 8, 12, 16])
+@pytest.mark.parametrize("kind,out", [("gemv", 4096), ("gemv", 11008), ("gate_up", 11008),
+                                      ("qkv", (4096, 1024, 1024))])
+@pytest.mark.parametrize("K", [4096, 11008])
+def test_batched_decode_is_one_launch(hip, M, kind, out, K):
+    """Every batch 3..16 decode at the BASELINE widths is one dispatch: the K-split streaming
+    kernel where it needs no split, the whole-K batch kernel where it would split."""
+    fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.float16, M, K, 128, out, 3, kind, 1, 1)
+    assert launches == 1 and splits == 1, (fam, splits, launches)
+    assert fam in ("bstream", "batch")
+    if kind == "gemv" and out == 4096 and K == 11008 and M >= 8:
+        assert fam == "batch"
+
+
 def test_baseline_fused_decode(hip):
     bits = tuple(int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 3))
     q, Q64, _, _ = make(4096, 4096, bits[0], torch.float16, seed=1, scale=0.02)
