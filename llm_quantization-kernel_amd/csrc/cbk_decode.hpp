@@ -5,9 +5,10 @@
 // bit offset e (0..5) of a 16-bit half into the bit pattern of 1024.0 (0x6400,
 // ulp 1) gives the exact fp16 value 1024 + 2^e q = 2^e (2^(10-e) + q), so each half
 // keeps its field where it lies and most fields need no shift.  The activation
-// that meets half slot p is staged as x * 2^-e(p) (exact: a power-of-two scale), so
-// the MFMA sums x * (B(p) + q) with the slot offset B(p) = 2^(10 - e(p)); the
-// kernels remove sum_p x * B(p) together with the zero point.
+// that meets half slot p is staged as x * 2^-e(p) in fp16 (a power-of-two scale: exact
+// while the product stays a normal fp16, |x| 2^-e >= 2^-14; below that it rounds to a
+// subnormal and keeps fewer bits), so the MFMA sums x * (B(p) + q) with the slot offset
+// B(p) = 2^(10 - e(p)); the kernels remove sum_p x * B(p) together with the zero point.
 //
 // Half slot p (pair p >> 1, high half when p & 1) holds code kappa(p) at offset
 // expo(p).  MFMA operand m (8 halves) is pairs 4m .. 4m+3.  Each output pair is

@@ -90,8 +90,8 @@ __device__ __forceinline__ void load_x(__amdgpu_buffer_rsrc_t xr, bool ok, int b
 }
 
 // The chunk in the decode's operand order: pair p = (x[kappa(2p)] 2^-e, x[kappa(2p+1)]
-// 2^-e') (an exact power-of-two scale), with its sums B = 1024 sum 2^-e x and
-// xs = sum x.
+// 2^-e') (a power-of-two scale, exact unless the fp16 result is subnormal), with its
+// sums B = 1024 sum 2^-e x and xs = sum x.
 template <int BITS>
 __device__ __forceinline__ void convert_x(const uint32_t (&x)[16], u4 (&X)[4], float& B, float& xs) {
     const h2 one = {(_Float16)1.0f, (_Float16)1.0f};

@@ -110,8 +110,9 @@ __device__ __forceinline__ void load_x(const GemvArgs& A, int b0, int ua, int nc
 }
 
 // Stage one x task: its chunk sums X = sum x and XB = sum x B(p) and its four MFMA
-// operands, the activations in decode order scaled by 2^-expo (exact) to meet the
-// in-place decoded fields (the MFMA then sums x (B(p) + q)).
+// operands, the activations in decode order scaled by 2^-expo (exact unless the fp16
+// result is subnormal) to meet the in-place decoded fields (the MFMA then sums
+// x (B(p) + q)).
 template <int BITS>
 __device__ __forceinline__ void store_x(const XTask& t, int ua, int K, int mt, char* xw, float* Xw) {
     u4* xs = reinterpret_cast<u4*>(xw);

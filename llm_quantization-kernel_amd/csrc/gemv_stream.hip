@@ -114,7 +114,7 @@ __device__ __forceinline__ void convert_x(const uint32_t (&x)[16], u4 (&X)[4], f
                              ((uint32_t)(4 + 2 * (kb & 1)) << 16) | ((uint32_t)(5 + 2 * (kb & 1)) << 24);
         const uint32_t raw = __builtin_amdgcn_perm(x[kb >> 1], x[ka >> 1], sel);
         const h2 sc = {(_Float16)(1.0f / (float)(1 << ea)), (_Float16)(1.0f / (float)(1 << eb))};
-        const h2 v = __builtin_bit_cast(h2, raw) * sc;      // exact: power-of-two scale
+        const h2 v = __builtin_bit_cast(h2, raw) * sc;      // power-of-two scale: exact unless subnormal
         o[p] = __builtin_bit_cast(uint32_t, v);
         b = __builtin_amdgcn_fdot2(v, one, b, false);
         t = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x[p]), one, t, false);
