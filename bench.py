@@ -25,7 +25,7 @@ profiles/gemv_w3_m1_traffic.txt, written from two rocprofv3 --pmc passes
 counters' reading for a copy of known size; null if that file is absent.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
-       python bench.py --pmc-workload     (fixed launches for counter collection)
+       python bench.py --pmc-workload [gemv|gemm]   (fixed launches for counter collection)
 Prints one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -188,8 +188,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--sweeps", default="gemv,fused,gemm,stack,model,producer",
                     help="comma-separated extra sweeps after the timed step (ignored with --quick)")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="run the fixed launch sequence of the counter passes and exit")
+    ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm"),
+                    help="run the fixed launch sequence of a counter pass and exit: gemv (default: the "
+                         "W3 decode GEMV after a calibration copy) or gemm (the M=1024 W4 prefill GEMM)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one MI355X; --gpus {args.gpus} is not supported "
@@ -206,6 +207,9 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}  CUs={C.sm_count()}")
+    if args.pmc_workload == "gemm":
+        pmc_workload_gemm(torch, ops, dev)
+        return
     if args.pmc_workload:
         pmc_workload(torch, ops, dev)
         return
@@ -352,15 +356,27 @@ def weight_bytes(w):
     return w.packed.numel() * 4 + w.scales.numel() * w.scales.element_size() * 2
 
 
+def pmc_workload_gemm(torch, ops, dev):
+    """Launch sequence of the GEMM counter passes: 1 + 5 launches of the M=1024 W4 prefill
+    GEMM at 4096 x 4096 (fp16 activations, g=128); the first warms the code and is dropped."""
+    w = make_weight(torch, 4096, 4096, 4, 0, dev)
+    x = randx(torch, 1024, 4096, 1, dev)
+    torch.cuda.synchronize()
+    for _ in range(6):
+        ops.packed_linear(x, w)
+    torch.cuda.synchronize()
+    log("pmc gemm workload done")
+
+
 def gemv_sweep(torch, C, ops, dev):
-    """W2/W3/W4 x M in {1,4,8} x shapes: µs per call (graph-replayed, a split call counts its
+    """W2/W3/W4 x M in {1,4,8,16} x shapes: µs per call (graph-replayed, a split call counts its
     combine launch) over >= 1 GiB of distinct weight copies per shape."""
     rows = []
     for bits in (4, 3, 2):
         for s, (K, N) in enumerate(SHAPES):
             base = make_weight(torch, N, K, bits, 0, dev)
             ws = [base] + [clone_weight(base) for _ in range(copies_for(weight_bytes(base)) - 1)]
-            for M in (1, 4, 8):
+            for M in (1, 4, 8, 16):
                 x = randx(torch, M, K, 1, dev)
                 best = None
                 for sk, rho in [(1, 1), (2, 1), (None, 1)]:
