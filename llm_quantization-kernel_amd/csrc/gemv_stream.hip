@@ -44,7 +44,6 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int CPL = STREAM_CPL;          // chunks per lane of a slice
 constexpr int SLICE = 64 * CPL;          // chunks per K slice
-constexpr int RPW = STREAM_RPW;          // rows per wave
 constexpr int RAW = 0x00020000;          // buffer descriptor word 3: raw 32-bit data
 // A byte offset past every descriptor's range: such loads return zero.  Loads are
 // issued unconditionally (a branch around a load makes the compiler wait for it at
@@ -149,7 +148,7 @@ __device__ __forceinline__ float dpp_add(float v) {
 
 // Lane sums of 4 rows -> every lane of 16-lane row i holds the total of wave row
 // srow(i): rows (0, 2, 1, 3) for lane rows (0, 1, 2, 3).
-__device__ __forceinline__ float reduce4(const float (&a)[RPW]) {
+__device__ __forceinline__ float reduce4(const float (&a)[4]) {
     const auto p01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[0]), __float_as_uint(a[1]), false, false);
     const auto p23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[2]), __float_as_uint(a[3]), false, false);
     const float s01 = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);   // lanes 0-31 row 0, 32-63 row 1
@@ -170,11 +169,11 @@ __device__ __forceinline__ void barrier_lds() {
     __builtin_amdgcn_s_barrier();
 }
 
-template <int BITS, int MODE, int MB>
+template <int BITS, int MODE, int MB, int RPW>
 __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int KS = A.st_ks, RW = A.st_rw, RB = 4 * A.st_rw;
+    const int KS = A.st_ks, RW = A.st_rw, RB = RPW * A.st_rw;
     const int NCH = KS * SLICE;
     const int ks = (int)fdiv((uint32_t)wave, A.divRW);
     const int rw = wave - ks * RW;
@@ -285,11 +284,15 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
         }
     }
 
-    // 4. row totals of the wave, per batch row
+    // 4. row totals of the wave, per batch row, 4 rows at a time
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
-        const float tot = reduce4(acc[b]);
-        if ((lane & 15) == 0) red[(ks * MB + b) * RB + RPW * rw + lane_row(lane)] = tot;
+#pragma unroll
+        for (int q = 0; q < RPW / 4; ++q) {
+            const float a4[4] = {acc[b][4 * q], acc[b][4 * q + 1], acc[b][4 * q + 2], acc[b][4 * q + 3]};
+            const float tot = reduce4(a4);
+            if ((lane & 15) == 0) red[(ks * MB + b) * RB + RPW * rw + 4 * q + lane_row(lane)] = tot;
+        }
     }
     barrier_lds();
 
@@ -505,29 +508,30 @@ __global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
 // workgroup's rows inside one projection, so the width is uniform per workgroup.
 // MB batch rows (1 or 2; rows past M are zero).  Wider batches stage MB copies of
 // the activations, which at K = 11008 leaves one workgroup per CU; they take the
-// batch-rows MFMA kernel instead.
-template <int MODE, int BITS, int MB>
+// batch-rows MFMA kernel instead.  RPW rows per wave (4, or 8 for the host's short-K
+// batch-1 plan: half the waves for the same rows per workgroup).
+template <int MODE, int BITS, int MB, int RPW>
 __global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
-        stream_body<BITS, MODE, MB>(A, lds);
+        stream_body<BITS, MODE, MB, RPW>(A, lds);
     } else {
         int proj, r;
-        vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * 4 * A.st_rw, proj, r);
+        vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * RPW * A.st_rw, proj, r);
         const int bits = CBK_SEL(A, proj, bits);
-        if (bits == 2) stream_body<2, MODE, MB>(A, lds);
-        else if (bits == 3) stream_body<3, MODE, MB>(A, lds);
-        else stream_body<4, MODE, MB>(A, lds);
+        if (bits == 2) stream_body<2, MODE, MB, RPW>(A, lds);
+        else if (bits == 3) stream_body<3, MODE, MB, RPW>(A, lds);
+        else stream_body<4, MODE, MB, RPW>(A, lds);
     }
 }
 
-template <int MB>
+template <int MB, int RPW>
 const void* stream_kernel(int mode, int bits, bool mixed) {
-    if (mixed) return reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_QKV, 0, MB>);
+    if (mixed) return reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_QKV, 0, MB, RPW>);
 #define CBK_STREAM_K(M)                                                                            \
-    (bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 2, MB>)                      \
-               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 3, MB>)         \
-                            : reinterpret_cast<const void*>(&gemv_stream_kernel<M, 4, MB>)))
+    (bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 2, MB, RPW>)                 \
+               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 3, MB, RPW>)    \
+                            : reinterpret_cast<const void*>(&gemv_stream_kernel<M, 4, MB, RPW>)))
     if (mode == MODE_QKV) return CBK_STREAM_K(MODE_QKV);
     if (mode == MODE_GATEUP) return CBK_STREAM_K(MODE_GATEUP);
     return CBK_STREAM_K(MODE_GEMV);
@@ -549,8 +553,10 @@ const void* bstream_kernel(int mode, int bits, bool mixed) {
 
 }  // namespace
 
-const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb) {
-    return mb <= 1 ? stream_kernel<1>(mode, bits, mixed) : stream_kernel<2>(mode, bits, mixed);
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw) {
+    if (mb > 1) return stream_kernel<2, STREAM_RPW>(mode, bits, mixed);
+    return rpw == STREAM_RPW_WIDE ? stream_kernel<1, STREAM_RPW_WIDE>(mode, bits, mixed)
+                                  : stream_kernel<1, STREAM_RPW>(mode, bits, mixed);
 }
 
 const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu) {
