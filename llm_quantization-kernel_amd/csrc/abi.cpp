@@ -393,7 +393,7 @@ int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu) {
     return (int)P;
 }
 
-BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k) {
+BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int cus) {
     BStreamPlan bp;
     const int64_t lim = INT32_MAX;
     bool ok = A.M >= 3 && A.M <= 16 && dtype == CBK_F16 && A.gs % 128 == 0 && A.K % 8 == 0 &&
@@ -414,6 +414,27 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
             bp.bsu = 8;
             bp.rw = rw8;
             bp.P = p8;
+        }
+    }
+    // Every workgroup converts all of its split's activations, so at many rows the
+    // activation work, not the weight stream, sets the time: plain GEMVs whose 16-row
+    // blocks would give each CU 2.5 or more workgroups take 8-unit slices and the
+    // fewest workgroups that still cover the CUs (W3 4096 -> 11008: batch 8 13.2 -> 11.1
+    // us, batch 16 18.8 -> 14.5), and gate-up takes 8-unit slices (batch 4 20.4 -> 15.6).
+    if (bp.P == 1 && cus > 0) {
+        const int64_t U8 = ceil_div(U, 8);
+        if (mode == CBK_MODE_GEMV && !mixed && ceil_div(A.V, 16) >= (5 * (int64_t)cus) / 2) {
+            int rw = (int)std::max<int64_t>(bstream_rw(A.M, 8, false), ceil_div(ceil_div(A.V, 16), cus));
+            if (U8 * rw <= 16 && bstream_lds(U8, A.M, rw, 8) <= LDS_BUDGET) {
+                bp.bsu = 8;
+                bp.rw = rw;
+            }
+        } else if (gateup) {
+            const int rw = bstream_rw(A.M, 8, true);
+            if (U8 * rw <= 16 && bstream_lds(U8, A.M, rw, 8) <= LDS_BUDGET) {
+                bp.bsu = 8;
+                bp.rw = rw;
+            }
         }
     }
     if ((int64_t)U * bp.P >= (1ll << 32)) return bp;
@@ -536,7 +557,7 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
     // batch 3..16: the K-split streaming kernel where it needs no split (one dispatch, the
     // faster kernel there), the whole-K batch kernel where it would split K (one dispatch
     // instead of a split and a reduce launch)
-    const BStreamPlan bp = plan_bstream(A, dtype, mode, mixed, split_k);
+    const BStreamPlan bp = plan_bstream(A, dtype, mode, mixed, split_k, cus);
     const BatchPlan bt = (bp.ok && bp.P == 1) ? BatchPlan{} : plan_batch(A, dtype, mode, mixed, cus);
     if (bt.ok) {
         A.P = 1;
