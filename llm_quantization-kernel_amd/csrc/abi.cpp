@@ -297,9 +297,10 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
 // size that is a multiple of 32, 32-bit byte offsets into every tensor, and for
 // mixed-width QKV workgroups that stay inside one projection.  The K range of a
 // split is cut into slices of 64 * STREAM_CPL chunks (one wave each, at most 8);
-// rows go rpw to a wave, RW row groups to a workgroup.  Batch 1 with at most two
-// slices (K <= 4096 at one split) takes 8 rows a wave in two row groups: the same 16
-// rows per workgroup from half the waves (4096^2 W3: 4.5 -> 4.1 us per call).
+// rows go rpw to a wave, RW row groups to a workgroup.  A plain GEMV at batch 1 with
+// at most two slices (K <= 4096 at one split) takes 8 rows a wave in two row groups:
+// the same 16 rows per workgroup from half the waves (4096^2 W3: 4.5 -> 4.1 us per
+// call; fused QKV measured 3 % slower that way and keeps 4).
 struct StreamPlan {
     bool ok = false;
     int P = 1, ks = 1, rw = 2, rpw = STREAM_RPW, mb = 1, grid = 0, lds = 0;
@@ -323,7 +324,7 @@ int stream_splits(int64_t C, int split_k, int max_slices) {
     return (int)P;
 }
 
-StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k) {
+StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k) {
     StreamPlan sp;
     const int64_t lim = INT32_MAX;
     bool ok = A.M >= 1 && A.M <= 2 && dtype == CBK_F16 && A.gs % 32 == 0 && A.K % 8 == 0 &&
@@ -340,7 +341,7 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, bool mixed, int split_k) {
     if (sp.ks * STREAM_CPL > max_waves) return sp;
     sp.rw = sp.ks <= 2 ? 4 : 2;
     sp.rw = std::max(STREAM_CPL, std::min(sp.rw, max_waves / sp.ks));
-    if (sp.mb == 1 && sp.ks <= 2) {
+    if (sp.mb == 1 && sp.ks <= 2 && mode == CBK_MODE_GEMV && !mixed) {
         sp.rpw = STREAM_RPW_WIDE;
         sp.rw = std::max(STREAM_CPL, sp.rw / 2);
     }
@@ -538,7 +539,7 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
     bool xvec = (A.K % 8 == 0) && (reinterpret_cast<uintptr_t>(A.x) % 16 == 0);
     for (int i = 0; i < 3; ++i)
         xvec = xvec && reinterpret_cast<uintptr_t>(A.p[i].s) % 16 == 0 && reinterpret_cast<uintptr_t>(A.p[i].z) % 16 == 0;
-    const StreamPlan sp = plan_stream(A, dtype, mixed, split_k);
+    const StreamPlan sp = plan_stream(A, dtype, mode, mixed, split_k);
     if (sp.ok) {
         A.P = sp.P;
         A.st_ks = sp.ks;

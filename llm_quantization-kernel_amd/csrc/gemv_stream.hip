@@ -555,8 +555,13 @@ const void* bstream_kernel(int mode, int bits, bool mixed) {
 
 const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw) {
     if (mb > 1) return stream_kernel<2, STREAM_RPW>(mode, bits, mixed);
-    return rpw == STREAM_RPW_WIDE ? stream_kernel<1, STREAM_RPW_WIDE>(mode, bits, mixed)
-                                  : stream_kernel<1, STREAM_RPW>(mode, bits, mixed);
+    if (rpw == STREAM_RPW_WIDE && mode == MODE_GEMV && !mixed) {     // the host plans 8 rows for plain GEMVs only
+        constexpr int W = STREAM_RPW_WIDE;
+        return bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 2, 1, W>)
+                         : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 3, 1, W>)
+                                      : reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 4, 1, W>));
+    }
+    return stream_kernel<1, STREAM_RPW>(mode, bits, mixed);
 }
 
 const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu) {
