@@ -319,6 +319,43 @@ def test_batched_decode_is_one_launch(hip, M, kind, out, K):
         assert fam == "batch"
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("M", [12, 16])
+def test_wide_batched_workgroups(hip, bits, M):
+    """4096 -> 11008 at batch 12 / 16 takes 8-unit slices and 48- / 64-row workgroups (fewer
+    workgroups than CUs, each converting the activations once): parity and the plan."""
+    fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.float16, M, 4096, 128, 11008, bits, "gemv", 1, 1)
+    rw = 3 if M <= 12 else 4
+    assert (fam, splits, launches) == ("bstream", 1, 1)
+    assert grid == -(-11008 // (16 * rw)) and threads == 64 * 4 * rw, (grid, threads)
+    w, W64, _, _ = make(11008, 4096, bits, torch.float16, scale=0.02)
+    x = randx(M, 4096, torch.float16, seed=M)
+    close(packed_linear(x, w), ref_linear(x, W64), torch.float16)
+
+
+@pytest.mark.parametrize("B", [3, 4, 8, 12, 16])
+def test_baseline_gate_up_batched(hip, B):
+    """Fused gate-up at the BASELINE width in batch takes 8-unit slices (an even number of row
+    blocks, gate and up rows alternating between the waves)."""
+    fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.float16, B, 4096, 128, 11008, 3, "gate_up", 1, 1)
+    assert (fam, splits, launches) == ("bstream", 1, 1) and threads % 256 == 0
+    g, G64, _, _ = make(11008, 4096, 3, torch.float16, seed=4, scale=0.02)
+    u, U64, _, _ = make(11008, 4096, 3, torch.float16, seed=5, scale=0.02)
+    x = randx(B, 4096, torch.float16, seed=B)
+    gv, uv = ref_linear(x, G64), ref_linear(x, U64)
+    close(fused_gate_up(x, g, u), gv / (1 + np.exp(-gv)) * uv, torch.float16)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_batch1_wide_rows_plan(hip, bits):
+    """A plain batch-1 GEMV at K = 4096 runs 8 rows a wave in 4-wave workgroups; fused QKV keeps 4."""
+    fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.float16, 1, 4096, 128, 4096, bits, "gemv", 1, 1)
+    assert (fam, grid, threads) == ("stream", 256, 256), (fam, grid, threads)
+    fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.float16, 1, 4096, 128, (4096, 4096, 4096), bits,
+                                                               "qkv", 1, 1)
+    assert (fam, grid, threads) == ("stream", 12288 // 16, 512), (fam, grid, threads)
+
+
 def test_baseline_fused_decode(hip):
     bits = tuple(int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 3))
     q, Q64, _, _ = make(4096, 4096, bits[0], torch.float16, seed=1, scale=0.02)
