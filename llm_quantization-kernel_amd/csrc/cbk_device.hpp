@@ -142,7 +142,7 @@ struct GemvArgs {
     FastDiv divNP;                    // by raw_np
     // batch-1 streaming kernel (gemv_stream.hip)
     int st_ks;             // K slices per job (waves per row group)
-    int st_rw;             // row groups per workgroup (4 rows each)
+    int st_rw;             // row groups per workgroup (one wave's rows each)
     int st_xvec;           // x is 16-byte aligned with K % 8 == 0 (vector activation loads)
     int pad2_;
     FastDiv divRW, divGS;             // by st_rw and gs / 32

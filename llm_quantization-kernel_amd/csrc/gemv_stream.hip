@@ -6,10 +6,10 @@
 // multiple of 32.  Plain, fused-QKV and fused gate-up modes share the body; the
 // epilogue is cb_epilogue's (:54-81, cbk_device.hpp).
 //
-// Job = (block of RB = 4 RW virtual rows, K split p).  A workgroup holds KS x RW
-// waves: wave (ks, rw) takes rows 4 rw .. 4 rw + 3 of the block over K slice ks
-// of the split, 64 CPL chunks of 32 codes, lane l owning chunks l + 64 i (i < CPL)
-// of the slice.  Per wave:
+// Job = (block of RB = RPW RW virtual rows, K split p).  A workgroup holds KS x RW
+// waves: wave (ks, rw) takes rows RPW rw .. RPW rw + RPW - 1 of the block (RPW = 4,
+// or 8 for the host's short-K plain GEMVs) over K slice ks of the split, 64 CPL chunks
+// of 32 codes, lane l owning chunks l + 64 i (i < CPL) of the slice.  Per wave:
 //   1. The thread's activation chunk is requested, then every packed
 //      chunk of the wave's rows (one buffer load of BITS dwords per row and lane
 //      chunk, 64 lanes = 64 consecutive chunks) and their (scale, zero) halves --
@@ -23,7 +23,7 @@
 //      one v_and_or_b32 each, 16 v_dot2_f32_f16 against the staged pairs give
 //      sum x q + B, and acc += s * (dot - B - z * sum x)  (packed_gemv.cu:113-138
 //      algebra: the zero point is applied per chunk against the activation sum).
-//   4. The 4 rows' lane sums meet by v_permlane32_swap, v_permlane16_swap and four
+//   4. Each 4 rows' lane sums meet by v_permlane32_swap, v_permlane16_swap and four
 //      DPP row rotations (every lane of a 16-lane row ends with one row's total).
 //   5. Row totals of the slices meet in LDS and are added in slice order (so the
 //      result does not depend on wave timing); the epilogue runs per row, or with
