@@ -124,6 +124,58 @@ hipError_t scratch_for(int device, float** out) {
     return g_scratch_err[device];
 }
 
+// Arrival counters of the in-dispatch split-K combine (split_arrive, cbk_device.hpp):
+// one word per row block of a call, zero between calls (the combining workgroup
+// resets its word).  A file-scope device array, one copy per GPU, cut into windows;
+// each stream that makes split calls on a device holds a window of its own, so calls
+// in flight on different streams never share a counter.  Calls on one stream run in
+// order, so one window serves all of them.  Windows go to streams in first-use order
+// and, once all are taken, to the stream that used its window least recently; a call
+// whose row blocks outnumber a window's counters takes the reduce launch instead.
+constexpr int SPLIT_WINDOWS = 32;
+constexpr int SPLIT_COUNTERS = 8192;
+static __device__ __align__(256) uint32_t split_counters[SPLIT_WINDOWS * SPLIT_COUNTERS];
+
+struct SplitWindows {
+    std::mutex mu;
+    uint32_t* base = nullptr;
+    hipError_t err = hipSuccess;
+    bool init = false;
+    hipStream_t owner[SPLIT_WINDOWS];
+    uint64_t used[SPLIT_WINDOWS];
+    uint64_t tick = 0;
+};
+SplitWindows g_split[MAX_DEVICES];
+
+// This stream's counter window on `device` (made current by the caller), or nullptr.
+uint32_t* split_window(int device, hipStream_t stream) {
+    if (device < 0 || device >= MAX_DEVICES) return nullptr;
+    SplitWindows& W = g_split[device];
+    std::lock_guard<std::mutex> lk(W.mu);
+    if (!W.init) {
+        void* p = nullptr;
+        W.err = hipGetSymbolAddress(&p, HIP_SYMBOL(split_counters));
+        W.base = W.err == hipSuccess ? static_cast<uint32_t*>(p) : nullptr;
+        for (int i = 0; i < SPLIT_WINDOWS; ++i) {
+            W.owner[i] = nullptr;
+            W.used[i] = 0;
+        }
+        W.init = true;
+    }
+    if (!W.base) return nullptr;
+    int slot = -1, lru = 0;
+    for (int i = 0; i < SPLIT_WINDOWS && slot < 0; ++i)
+        if (W.used[i] && W.owner[i] == stream) slot = i;
+    if (slot < 0) {
+        for (int i = 1; i < SPLIT_WINDOWS; ++i)
+            if (W.used[i] < W.used[lru]) lru = i;
+        slot = lru;
+        W.owner[slot] = stream;
+    }
+    W.used[slot] = ++W.tick;
+    return W.base + (size_t)slot * SPLIT_COUNTERS;
+}
+
 constexpr int MFMA_TILE = 16;          // virtual rows per MFMA decode job
 constexpr int LDS_BUDGET = 160 * 1024; // dynamic LDS per decode workgroup (gfx950: 160 KB per CU)
 constexpr int WAVES_PER_CU = 8;        // decode occupancy target
@@ -360,11 +412,13 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
 // group), 32-bit offsets, and rows that keep every 16-row tile inside one projection
 // (fused QKV: Q and K widths multiples of 16; mixed widths: of the workgroup's rows).
 // K is split over units; a split's units are cut into slices of bsu units (one wave
-// each, at most 16 waves): 4 where that needs no split, else 8 (a split costs a
-// second launch).  The split grows until the staged activations (64 bytes per chunk
-// and batch row), the unit sums and the row sums fit the LDS.
+// each, at most 16 waves): 4 where that needs no split, else 8.  The split grows until
+// the staged activations (64 bytes per chunk and batch row), the unit sums and the row
+// sums fit the LDS; the splits of a row block combine inside the dispatch
+// (split_arrive), so a split costs no second launch.
 struct BStreamPlan {
     bool ok = false;
+    bool filled = false;         // chosen by bstream_fill
     int P = 1, ks = 1, rw = 1, bsu = 4, grid = 0, lds = 0;
 };
 
@@ -394,6 +448,88 @@ int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu) {
     return (int)P;
 }
 
+// The plan (P, bsu, rw) of the batched streaming kernel, checked against what the kernel
+// assumes: a wave per slice and row group within 16 waves, every activation item staged
+// by at most two threads, an even number of row groups for gate-up, the LDS, one
+// projection per workgroup for mixed widths, 32-bit indices, and with P > 1 a counter
+// per row block in one window (the splits combine in the dispatch).
+BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu, int rw) {
+    BStreamPlan bp;
+    const int64_t U = ceil_div(A.C, 4);
+    if (P < 1 || P > U || (int64_t)U * P >= (1ll << 32)) return bp;
+    if (rw < bstream_rw(A.M, bsu, mode == CBK_MODE_GATEUP) || (mode == CBK_MODE_GATEUP && rw % 2)) return bp;
+    bp.P = P;
+    bp.bsu = bsu;
+    bp.rw = rw;
+    bp.ks = (int)ceil_div(ceil_div(U, P), bsu);
+    if (bp.ks * rw > 16) return bp;
+    bp.lds = (int)bstream_lds(bp.ks, A.M, rw, bsu);
+    if (bp.lds > LDS_BUDGET) return bp;
+    const int rb = 16 * rw;
+    if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return bp;
+    const int64_t blocks = ceil_div(A.V, rb);
+    if (P > 1 && blocks > SPLIT_COUNTERS) return bp;
+    if (blocks * P >= INT32_MAX) return bp;
+    bp.grid = (int)(blocks * P);
+    bp.ok = true;
+    return bp;
+}
+
+// A batched call whose unsplit plan would leave half the CUs without a workgroup, or that
+// needs K splits anyway, takes the plan with P in [P0, P0 + 3] whose workgroup count is
+// closest to one per CU (then the fewest splits, the shorter slices, the fewest row
+// groups): each CU then converts only its split's activations.  Measured on W3 at the
+// Llama-2-7B shapes (us per call): 11008 -> 4096 batch 8 15.4 (whole-K batch kernel) ->
+// 13.6 (P = 2, 8-unit slices, 2 row groups), batch 16 18.1 -> 16.3 (P = 4, 4 row
+// groups); 4096^2 batch 16 10.1 -> 8.9 (P = 2).  The target is a constant -- the CU count
+// of every gfx950 part -- so cbk_gemv_partial_floats can bound P without a device.
+constexpr int BSTREAM_CU_TARGET = 256;
+constexpr int BSTREAM_FILL_SPLITS = 4;
+
+BStreamPlan bstream_fill(const GemvArgs& A, int mode, bool mixed, int P0) {
+    BStreamPlan best;
+    int64_t best_key = INT64_MAX;
+    for (int P = P0; P < P0 + BSTREAM_FILL_SPLITS; ++P) {
+        for (int bsu : {4, 8}) {
+            for (int rw = 1; rw <= 16; ++rw) {
+                const BStreamPlan c = bstream_make(A, mode, mixed, P, bsu, rw);
+                if (!c.ok) continue;
+                const int64_t dist = std::abs((int64_t)c.grid - BSTREAM_CU_TARGET);
+                const int64_t key = ((dist * 64 + (P - P0)) * 2 + (bsu == 8)) * 32 + rw;
+                if (key < best_key) {
+                    best_key = key;
+                    best = c;
+                }
+            }
+        }
+    }
+    return best;
+}
+
+// The unsplit-first plan before any widening for the CU count: 4-unit slices with the
+// fewest splits that fit, or 8-unit slices where those need fewer splits.
+BStreamPlan bstream_base(int64_t M, int64_t C, int split_k, bool gateup) {
+    BStreamPlan bp;
+    bp.bsu = 4;
+    bp.rw = bstream_rw(M, 4, gateup);
+    bp.P = bstream_splits(C, M, split_k, bp.rw, 4);
+    if (bp.P > std::max(split_k, 1)) {           // 4-unit slices would add a split: try 8
+        const int rw8 = bstream_rw(M, 8, gateup);
+        const int p8 = bstream_splits(C, M, split_k, rw8, 8);
+        if (p8 < bp.P) {
+            bp.bsu = 8;
+            bp.rw = rw8;
+            bp.P = p8;
+        }
+    }
+    return bp;
+}
+
+// Whether a call with this base plan takes bstream_fill's plan.
+bool bstream_fills(const BStreamPlan& base, int64_t V) {
+    return base.P > 1 || ceil_div(V, 16 * base.rw) * base.P * 2 <= BSTREAM_CU_TARGET;
+}
+
 BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int cus) {
     BStreamPlan bp;
     const int64_t lim = INT32_MAX;
@@ -405,16 +541,12 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     if (!ok) return bp;
     const bool gateup = mode == CBK_MODE_GATEUP;
     const int64_t U = ceil_div(A.C, 4);
-    bp.bsu = 4;
-    bp.rw = bstream_rw(A.M, 4, gateup);
-    bp.P = bstream_splits(A.C, A.M, split_k, bp.rw, 4);
-    if (bp.P > std::max(split_k, 1)) {           // 4-unit slices would add a split: try 8
-        const int rw8 = bstream_rw(A.M, 8, gateup);
-        const int p8 = bstream_splits(A.C, A.M, split_k, rw8, 8);
-        if (p8 < bp.P) {
-            bp.bsu = 8;
-            bp.rw = rw8;
-            bp.P = p8;
+    bp = bstream_base(A.M, A.C, split_k, gateup);
+    if (bstream_fills(bp, A.V)) {
+        BStreamPlan fill = bstream_fill(A, mode, mixed, std::max(split_k, 1));
+        if (fill.ok) {
+            fill.filled = true;
+            return fill;
         }
     }
     // Every workgroup converts all of its split's activations, so at many rows the
@@ -438,22 +570,12 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
             }
         }
     }
-    if ((int64_t)U * bp.P >= (1ll << 32)) return bp;
-    bp.ks = (int)ceil_div(ceil_div(U, bp.P), bp.bsu);
-    if (bp.ks * bp.rw > 16) return bp;
-    bp.lds = (int)bstream_lds(bp.ks, A.M, bp.rw, bp.bsu);
-    if (bp.lds > LDS_BUDGET) return bp;
-    const int rb = 16 * bp.rw;
-    if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return bp;
-    const int64_t grid = ceil_div(A.V, rb) * bp.P;
-    if (grid >= lim) return bp;
-    bp.grid = (int)grid;
-    bp.ok = true;
-    return bp;
+    return bstream_make(A, mode, mixed, bp.P, bp.bsu, bp.rw);
 }
 
 // Batched plan (gemv_batch.hip), batch 3..16 in one dispatch, taken where the bstream
-// kernel would split K (its partials then need a reduce launch): the bstream kernel's
+// kernel would split K and bstream_fill finds no plan (its partials would then need a
+// reduce launch): the bstream kernel's
 // conditions (fp16 x with 16-byte pieces, group sizes that are multiples of 128,
 // 32-bit offsets, every 16-row block inside one projection; mixed widths: every
 // workgroup's rows).  A workgroup of 15 or 16 waves fills a CU (128 VGPRs per wave), so
@@ -555,11 +677,11 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         L.P = sp.P;
         return L;
     }
-    // batch 3..16: the K-split streaming kernel where it needs no split (one dispatch, the
-    // faster kernel there), the whole-K batch kernel where it would split K (one dispatch
-    // instead of a split and a reduce launch)
+    // batch 3..16: the K-split streaming kernel (one dispatch: unsplit, or splits that
+    // combine in the dispatch), else the whole-K batch kernel where the streaming kernel's
+    // split would need a reduce launch
     const BStreamPlan bp = plan_bstream(A, dtype, mode, mixed, split_k, cus);
-    const BatchPlan bt = (bp.ok && bp.P == 1) ? BatchPlan{} : plan_batch(A, dtype, mode, mixed, cus);
+    const BatchPlan bt = (bp.ok && (bp.P == 1 || bp.filled)) ? BatchPlan{} : plan_batch(A, dtype, mode, mixed, cus);
     if (bt.ok) {
         A.P = 1;
         A.st_rw = bt.rw;
@@ -624,6 +746,13 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
     return L;
 }
 
+// Whether the launch's K splits combine inside the dispatch (the streaming kernels, with
+// a counter per row block in one window) rather than in a reduce launch.
+bool combines_in_dispatch(const DecodeLaunch& L) {
+    return L.P > 1 && (L.family == CBK_KERNEL_STREAM || L.family == CBK_KERNEL_BSTREAM) &&
+           L.grid / L.P <= SPLIT_COUNTERS;
+}
+
 // Common body of the three decode entry points.
 int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rho, float* partial, int device,
                void* stream) {
@@ -635,13 +764,15 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     if (L.family == CBK_KERNEL_MFMA &&
         ((int64_t)A.units * A.P >= (1ll << 31) || (int64_t)A.jobs * 16 >= (1ll << 31)))
         return fail(CBK_EINVAL, "packed_gemv: problem too large for 32-bit job indexing");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    A.split_cnt = nullptr;
     if (A.P > 1) {
         if (!partial) return fail(CBK_EINVAL, "split-K needs a partial buffer (cbk_gemv_partial_floats)");
         A.partial = partial;
+        if (combines_in_dispatch(L)) A.split_cnt = split_window(device, s);
     } else {
         A.partial = nullptr;
     }
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t e;
     if (L.family == CBK_KERNEL_GENERIC) {
         e = launch_gemv_generic(A, dtype, mode, L.grid, s);
@@ -652,7 +783,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
         e = launch(L.f, dim3(L.grid), dim3(L.block), args, (size_t)L.lds, s);
     }
     if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
-    if (A.P > 1) {
+    if (A.P > 1 && !A.split_cnt) {
         e = launch_gemv_reduce(A, dtype, mode, s);
         if (e != hipSuccess) return hip_fail(e, "packed_gemv: reduce launch");
     }
@@ -784,8 +915,13 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
         }
     }
     if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M)));
-    if (M >= 3 && M <= 16)    // 4-unit slices split at least as often as 8-unit ones; gate-up rows
-        P = std::max(P, bstream_splits(ceil_div(K, 32), M, split_k, bstream_rw(M, 4, true), 4));
+    if (M >= 3 && M <= 16) {  // 4-unit slices split at least as often as 8-unit ones; gate-up rows
+        const int64_t C = ceil_div(K, 32);
+        P = std::max(P, bstream_splits(C, M, split_k, bstream_rw(M, 4, true), 4));
+        for (bool gateup : {false, true})     // bstream_fill takes at most P0 + 3 splits
+            if (bstream_fills(bstream_base(M, C, split_k, gateup), V))
+                P = std::max<int64_t>(P, std::min<int64_t>(ceil_div(C, 4), split_k + BSTREAM_FILL_SPLITS - 1));
+    }
     return P > 1 ? (int64_t)P * M * V : 0;
 }
 
@@ -840,7 +976,7 @@ int cbk_decode_plan(int dtype, int64_t M, int64_t K, int group_size, int64_t n0,
     out[2] = L.grid;
     out[3] = L.block;
     out[4] = L.lds;
-    out[5] = L.P > 1 ? 2 : 1;      // launches per call (a split adds the combine)
+    out[5] = L.P > 1 && !combines_in_dispatch(L) ? 2 : 1;   // launches per call (a reduce launch combines)
     return CBK_OK;
 }
 

@@ -146,6 +146,9 @@ struct GemvArgs {
     int st_xvec;           // x is 16-byte aligned with K % 8 == 0 (vector activation loads)
     int pad2_;
     FastDiv divRW, divGS;             // by st_rw and gs / 32
+    // streaming kernels with P > 1: one arrival counter per row block (zero between
+    // calls); the splits combine inside the dispatch.  nullptr: a reduce launch combines.
+    uint32_t* split_cnt;
 };
 
 // Per-wave weight ring of the MFMA decode kernel (host and device).  A stage is
@@ -224,6 +227,63 @@ __device__ __forceinline__ void epilogue(const GemvArgs& A, int b, int v, float 
             y = (d < (A.head_dim >> 1)) ? (y * c - yp * s) : (y * c + yp * s);
         }
         store_f<DT>(out, (long)b * n + orig, y);
+    }
+}
+
+// ---------------------------------------------------------------- split-K combine in the dispatch
+// The P workgroups of a row block (one per K split, on any XCD) combine their fp32
+// partials without the reduce launch that cb_reduce_kernel (packed_gemv.cu:166-180)
+// stands for.  Partials are written and read with agent-scope accesses (stores and
+// loads coherent across the XCDs' L2s, `sc1`), so no L2 write-back or invalidation is
+// needed: a release / acquire pair at agent scope would write back and invalidate the
+// whole L2 of the XCD per workgroup, which serialises (a K-split batch-1 GEMV went from
+// 7.6 to 38 us that way).  Each wave waits until its partial stores have completed,
+// the workgroup meets at a barrier, and one thread counts the workgroup in; the
+// workgroup that arrives last (old count P - 1) sets the counter back to zero for the
+// next call and adds the P partials in split order 0 .. P - 1 -- gemv_reduce_kernel's
+// order, so both paths give the same bits.  No workgroup waits for another.
+__device__ __forceinline__ void partial_put(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float partial_get(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// After the workgroup's partial_put calls: returns, in every thread, whether this
+// workgroup combines row block `blk`.  `flag` is a word of LDS that no thread reads or
+// writes across this call.
+__device__ __forceinline__ bool split_arrive(const GemvArgs& A, int blk, int* flag) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");      // this wave's partials are stored
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t* c = A.split_cnt + blk;
+        const uint32_t old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1u == (uint32_t)A.P;
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = last ? 1 : 0;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
+// Sum of split partials p = 0 .. P - 1 of (batch row b, virtual row v), in that order.
+__device__ __forceinline__ float split_sum(const GemvArgs& A, int b, int v) {
+    float s = 0.f;
+    for (int p = 0; p < A.P; ++p) s += partial_get(A.partial + ((long)p * A.M + b) * A.V + v);
+    return s;
+}
+
+// The combining workgroup's epilogue: rows [vbase, vbase + RB) of every batch row,
+// `nthr` threads (fp16 outputs: the streaming kernels' dtype).
+template <int MODE>
+__device__ __forceinline__ void split_epilogue(const GemvArgs& A, int vbase, int RB, int nthr) {
+    for (int t = threadIdx.x; t < A.M * RB; t += nthr) {
+        const int b = t / RB, v = vbase + (t - b * RB);
+        if (v < A.V) {
+            const bool paired = MODE == MODE_GATEUP || (MODE == MODE_QKV && A.rope_cos != nullptr);
+            const float partner = paired && (v ^ 1) < A.V ? split_sum(A, b, v ^ 1) : 0.f;
+            epilogue<DT_F16, MODE>(A, b, v, split_sum(A, b, v), partner);
+        }
     }
 }
 

@@ -307,9 +307,12 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
                 partner += red[(k * MB + b) * RB + (row ^ 1)];
             }
             if (A.P == 1) epilogue<DT_F16, MODE>(A, b, v, mine, partner);
-            else A.partial[((long)p * A.M + b) * A.V + v] = mine;
+            else partial_put(A.partial + ((long)p * A.M + b) * A.V + v, mine);
         }
     }
+    // 6. with P > 1 and arrival counters, the last split of the block combines
+    if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
+        split_epilogue<MODE>(A, vbase, RB, 64 * KS * RW);
 }
 
 // ------------------------------------------------------------------ batch rows 3..16
@@ -484,9 +487,12 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
                 partner += red[(k * M + b) * RB + (ro ^ 1)];
             }
             if (A.P == 1) epilogue<DT_F16, MODE>(A, b, v, mine, partner);
-            else A.partial[((long)p * A.M + b) * A.V + v] = mine;
+            else partial_put(A.partial + ((long)p * A.M + b) * A.V + v, mine);
         }
     }
+    // 6. with P > 1 and arrival counters, the last split of the block combines
+    if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
+        split_epilogue<MODE>(A, vbase, RB, nthr);
 }
 
 template <int MODE, int BITS, int BSU>

@@ -310,13 +310,69 @@ def test_baseline_gemv_shapes(hip, bits, K, N, M):
                                       ("qkv", (4096, 1024, 1024))])
 @pytest.mark.parametrize("K", [4096, 11008])
 def test_batched_decode_is_one_launch(hip, M, kind, out, K):
-    """Every batch 3..16 decode at the BASELINE widths is one dispatch: the K-split streaming
-    kernel where it needs no split, the whole-K batch kernel where it would split."""
+    """Every batch 3..16 decode at the BASELINE widths is one dispatch: the batched streaming
+    kernel, whose K splits (if any) combine inside the dispatch."""
     fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.float16, M, K, 128, out, 3, kind, 1, 1)
-    assert launches == 1 and splits == 1, (fam, splits, launches)
-    assert fam in ("bstream", "batch")
+    assert launches == 1, (fam, splits, launches)
+    assert fam == "bstream", (fam, splits, grid)
     if kind == "gemv" and out == 4096 and K == 11008 and M >= 8:
-        assert fam == "batch"
+        assert splits > 1 and abs(grid - 256) <= 32, (splits, grid)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("M,K,N", [(8, 11008, 4096), (16, 11008, 4096), (16, 4096, 4096), (12, 11008, 4096)])
+def test_batched_split_in_dispatch(hip, bits, M, K, N):
+    """Batched calls that take K splits (each CU converts only its split's activations) combine
+    them in the dispatch: oracle parity, the same bits on a repeated call and on another stream
+    (the arrival counters reset themselves), and graph replays equal to the eager call."""
+    fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.float16, M, K, 128, N, bits, "gemv", 1, 1)
+    assert (fam, launches) == ("bstream", 1) and splits > 1, (fam, splits, launches)
+    w, W64, _, _ = make(N, K, bits, torch.float16, scale=0.02)
+    x = randx(M, K, torch.float16, seed=M + bits)
+    y = packed_linear(x, w)
+    close(y, ref_linear(x, W64), torch.float16)
+    assert torch.equal(packed_linear(x, w), y)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        y2 = packed_linear(x, w)
+    torch.cuda.current_stream().wait_stream(s)
+    assert torch.equal(y2, y)
+    out = torch.empty_like(y)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out.copy_(packed_linear(x, w))
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y)
+        assert torch.equal(packed_linear(x, w), y)
+
+
+@pytest.mark.parametrize("B", [8, 16])
+def test_batched_split_fused(hip, B):
+    """Fused gate-up and fused QKV (RoPE partners, mixed widths) at K = 11008 in batch take
+    in-dispatch K splits where their plan splits: parity with the oracle."""
+    g, G64, _, _ = make(512, 11008, 3, torch.float16, seed=4, scale=0.02)
+    u, U64, _, _ = make(512, 11008, 3, torch.float16, seed=5, scale=0.02)
+    x = randx(B, 11008, torch.float16, seed=B)
+    gv, uv = ref_linear(x, G64), ref_linear(x, U64)
+    close(fused_gate_up(x, g, u), gv / (1 + np.exp(-gv)) * uv, torch.float16)
+    fam, splits, *_ = _C.decode_plan(torch.float16, B, 11008, 128, 512, 3, "gate_up", 1, 1)
+    assert fam == "bstream" and splits > 1, (fam, splits)
+    hd = 128
+    q, Q64, _, _ = make(512, 11008, 4, torch.float16, seed=1, scale=0.02)
+    k, K64, _, _ = make(256, 11008, 2, torch.float16, seed=2, scale=0.02)
+    v, V64, _, _ = make(256, 11008, 3, torch.float16, seed=3, scale=0.02)
+    cos, sin = _rope_tables(B, hd)
+    oq, ok, ov = fused_qkv(x, permute_for_rope(q, hd), permute_for_rope(k, hd), v,
+                           rope=(cos.cuda(), sin.cuda(), hd))
+    close(oq, _rope64(ref_linear(x, Q64), cos, sin, hd), torch.float16)
+    close(ok, _rope64(ref_linear(x, K64), cos, sin, hd), torch.float16)
+    close(ov, ref_linear(x, V64), torch.float16)
+    fam, splits, *_ = _C.decode_plan(torch.float16, B, 11008, 128, (512, 256, 256), (4, 2, 3), "qkv", 1, 1)
+    assert fam == "bstream" and splits > 1, (fam, splits)
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
