@@ -860,6 +860,10 @@ int qkv_common(const void* x, int dtype, int64_t M, int64_t K, const int32_t* wq
 
 }  // namespace
 
+namespace cbk {
+hipError_t lds_limit_raise(const void* f, int bytes) { return ensure_lds(f, bytes); }
+}  // namespace cbk
+
 extern "C" {
 
 const char* cbk_last_error(void) { return g_err.c_str(); }

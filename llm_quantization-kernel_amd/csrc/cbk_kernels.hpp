@@ -11,6 +11,10 @@ namespace cbk {
 // (hipExtLaunchKernel), so cbk_timer_stop reports pure kernel durations.
 hipError_t launch(const void* f, dim3 grid, dim3 block, void** args, size_t lds, hipStream_t stream);
 
+// abi.cpp: raises kernel f's dynamic-LDS limit (on the current device) to cover `bytes`,
+// once per kernel and device; the limit is only ever raised.
+hipError_t lds_limit_raise(const void* f, int bytes);
+
 // gemv_mfma.hip: fp16, group size % 128 == 0.  Kernel address for the attribute
 // queries and the launch; max_batch <= 1 selects the single-row epilogue.
 const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);

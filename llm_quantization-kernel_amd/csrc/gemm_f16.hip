@@ -636,7 +636,7 @@ hipError_t launch_gemm_f16(const GemmArgs& A, hipStream_t stream) {
     const void* f = A.bits == 2 ? kernel_for<2>(tail, gs128) : (A.bits == 3 ? kernel_for<3>(tail, gs128)
                                                                          : kernel_for<4>(tail, gs128));
     const int lds = A.bits == 2 ? LDS_BYTES<2> : (A.bits == 3 ? LDS_BYTES<3> : LDS_BYTES<4>);
-    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    hipError_t e = lds_limit_raise(f, lds);
     if (e != hipSuccess) return e;
     const int tiles = ((A.M + BM - 1) / BM) * ((A.N + BN - 1) / BN);
     void* args[] = {const_cast<GemmArgs*>(&A)};

@@ -148,3 +148,45 @@ def test_llama_stack_blocks_graph_replay(hip):
             assert torch.equal(c, e), f"replay {rep}: output {j} differs from eager"
         _step(blocks, xh, xi)                     # eager work between the replays
         torch.cuda.synchronize()
+
+
+def test_llama_stack_blocks_oracle_decode_and_prefill(hip):
+    """Two blocks of the stack (config-5 bits, Llama-2-7B widths) against the CPU oracle, the
+    decode leg at M = 1 and the prefill leg at M = 2048: every linear of both blocks (fused QKV,
+    o, fused gate-up, down) against the float64 product on the oracle's dequantized weights --
+    W-hat for decode, W-hat rounded once to fp16 for the prefill GEMM (oracle/emulator.py).  The
+    GPU computes every output; the float64 reference covers 256 sampled output features of each
+    linear, and the prefill 64 sampled rows, so the oracle stays small."""
+    from oracle import emulator as E
+
+    dev = torch.device("cuda", 0)
+    bitmap = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 32)][:2]
+    rng = np.random.default_rng(7)
+    rows = np.sort(rng.choice(2048, 64, replace=False))
+    gx = torch.Generator().manual_seed(11)
+    xh = torch.randn(2048, H, generator=gx).half().to(dev)
+    xi = torch.randn(2048, I, generator=gx).half().to(dev)
+    for i, bits in enumerate(bitmap):
+        pb, _ = _stack_block(i, bits, dev)
+        cols, W64 = {}, {}
+        for nm, N, K in LINEARS:
+            c = np.sort(rng.choice(N, 256, replace=False)) if nm != "up" else cols["gate"]
+            w = pb[nm]
+            cols[nm] = c
+            W64[nm] = E.dequant64(w.packed.cpu().numpy()[c], w.scales.double().cpu().numpy()[c],
+                                  w.zeros.double().cpu().numpy()[c], bits, K, 128)
+        for M in (1, 2048):
+            a, b = (xh[:1], xi[:1]) if M == 1 else (xh, xi)
+            sel = np.arange(1) if M == 1 else rows
+            xa, xb = a[sel].double().cpu().numpy(), b[sel].double().cpu().numpy()
+            Wd = W64 if M == 1 else {nm: E.round_to(W, torch.float16) for nm, W in W64.items()}
+            oq, ok, ov = fused_qkv(a, pb["q"], pb["k"], pb["v"])
+            outs = {"q": oq, "k": ok, "v": ov, "o": packed_linear(a, pb["o"]),
+                    "gate": fused_gate_up(a, pb["gate"], pb["up"]), "down": packed_linear(b, pb["down"])}
+            refs = {nm: (xb if nm == "down" else xa) @ Wd[nm].T for nm in ("q", "k", "v", "o", "down")}
+            gv, uv = xa @ Wd["gate"].T, xa @ Wd["up"].T
+            refs["gate"] = gv / (1 + np.exp(-gv)) * uv
+            for nm, ref in refs.items():
+                got = outs[nm][torch.from_numpy(sel).to(dev)][:, torch.from_numpy(cols[nm]).to(dev)]
+                err = _rel(torch.from_numpy(ref), got.cpu())
+                assert err < 3e-3, f"block {i} (W{bits}) M={M} {nm}: rel err {err:.2e}"
