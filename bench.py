@@ -187,7 +187,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="timed step + roofline only (no sweeps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--sweeps", default="gemv,fused,gemm,stack,model,producer",
-                    help="comma-separated extra sweeps after the timed step (ignored with --quick)")
+                    help="comma-separated extra sweeps after the timed step (ignored with --quick); "
+                         "also 'batched': batched decode at the library's own plans")
     ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm"),
                     help="run the fixed launch sequence of a counter pass and exit: gemv (default: the "
                          "W3 decode GEMV after a calibration copy) or gemm (the M=1024 W4 prefill GEMM)")
@@ -287,6 +288,8 @@ def main():
         todo = {w.strip() for w in args.sweeps.split(",") if w.strip()}
         if "gemv" in todo:
             out["gemv_sweep"] = gemv_sweep(torch, C, ops, dev)
+        if "batched" in todo:
+            out["batched"] = batched_sweep(torch, C, ops, dev)
         if "fused" in todo:
             out["fused"] = fused_sweep(torch, C, ops, dev)
         if "gemm" in todo:
@@ -390,6 +393,31 @@ def gemv_sweep(torch, C, ops, dev):
                              "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "split_k": sk, "rho": rho,
                              "copies": len(ws)})
                 log(f"gemv W{bits} M={M} K={K} N={N}: {us:.2f} us {gbs:.0f} GB/s ({len(ws)} copies)")
+            del ws, base
+            torch.cuda.empty_cache()
+    return rows
+
+
+def batched_sweep(torch, C, ops, dev):
+    """Batched decode at the library's own plan (split_k=None, no candidate search): W3 and W4,
+    M in {4, 8, 16} over the three shapes, µs per call graph-replayed over >= 1 GiB of weight
+    copies, with the launch the plan makes (kernel family, K splits, workgroups, launches per
+    call).  The launch sequence of the batched decode kernel-trace profile."""
+    rows = []
+    for bits in (3, 4):
+        for K, N in SHAPES:
+            base = make_weight(torch, N, K, bits, 0, dev)
+            ws = [base] + [clone_weight(base) for _ in range(copies_for(weight_bytes(base)) - 1)]
+            for M in (4, 8, 16):
+                x = randx(torch, M, K, 1, dev)
+                fam, splits, grid, threads, lds, launches = C.decode_plan(torch.float16, M, K, GS, N, bits, "gemv",
+                                                                          1, 1)
+                us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w) for w in ws], len(ws), replays=4)
+                gbs = gemv_bytes(M, K, N, bits) / (us * 1e-6) / 1e9
+                rows.append({"bits": bits, "M": M, "K": K, "N": N, "us": round(us, 3), "GBps": round(gbs, 1),
+                             "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "kernel": fam, "splits": splits,
+                             "workgroups": grid, "threads": threads, "launches": launches, "copies": len(ws)})
+                log(f"batched W{bits} M={M} K={K} N={N}: {us:.2f} us ({fam}, P={splits}, {grid} workgroups)")
             del ws, base
             torch.cuda.empty_cache()
     return rows
