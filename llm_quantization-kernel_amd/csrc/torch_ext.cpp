@@ -224,8 +224,10 @@ std::vector<Tensor> fused_qkv(const Tensor& x, const Tensor& wq, const Tensor& s
     const void* pk = bias_ptr(bk, x, nk);
     const void* pv = bias_ptr(bv, x, nv);
     int32_t* ws = workspace_ptr(workspace, x);
-    std::vector<Tensor> outs = {at::empty({B, nq}, x.options()), at::empty({B, nk}, x.options()),
-                                at::empty({B, nv}, x.options())};
+    // one allocation carved into three contiguous [B, n] outputs (each its own block of it)
+    const Tensor flat = at::empty({B * (nq + nk + nv)}, x.options());
+    std::vector<Tensor> outs = {flat.narrow(0, 0, B * nq).view({B, nq}), flat.narrow(0, B * nq, B * nk).view({B, nk}),
+                                flat.narrow(0, B * (nq + nk), B * nv).view({B, nv})};
     if (B == 0) return outs;
     const Tensor part = partial_for(x, B, nq + nk + nv, in_features, group_size, split_k);
     const int dev = x.get_device();
