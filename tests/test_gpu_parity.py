@@ -350,6 +350,36 @@ def test_batched_split_in_dispatch(hip, bits, M, K, N):
         assert torch.equal(packed_linear(x, w), y)
 
 
+def test_split_counter_windows_across_streams(hip):
+    """Split calls in flight on several streams at once each use their stream's counter window,
+    and more streams than windows (40 > 32) take windows over in least-recently-used order:
+    every result equals the single-stream result bit for bit."""
+    w, W64, _, _ = make(4096, 11008, 3, torch.float16, scale=0.02)
+    x = randx(8, 11008, torch.float16, seed=3)
+    fam, splits, *_ = _C.decode_plan(torch.float16, 8, 11008, 128, 4096, 3, "gemv", 1, 1)
+    assert fam == "bstream" and splits > 1
+    y = packed_linear(x, w)
+    close(y, ref_linear(x, W64), torch.float16)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(40)]
+    # four streams with several calls each in flight together
+    outs = []
+    for st in streams[:4]:
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            outs.append([packed_linear(x, w) for _ in range(6)])
+    torch.cuda.synchronize()
+    for o in outs:
+        for t in o:
+            assert torch.equal(t, y)
+    # every stream once, one after another: windows are reassigned past the 32nd stream
+    for st in streams:
+        with torch.cuda.stream(st):
+            t = packed_linear(x, w)
+        st.synchronize()
+        assert torch.equal(t, y)
+
+
 @pytest.mark.parametrize("B", [8, 16])
 def test_batched_split_fused(hip, B):
     """Fused gate-up and fused QKV (RoPE partners, mixed widths) at K = 11008 in batch take
