@@ -5,8 +5,9 @@
  * `crispybits_kernels._C` (/root/reference/Crispybits/Kernel/csrc/bindings.cpp:32-40).
  * Every entry point takes plain device pointers, sizes and a hipStream_t (as void*),
  * launches asynchronously on that stream and returns a status code; no torch types
- * cross this boundary.  The Python host layer (crispybits_kernels/_C.py) binds it
- * with ctypes and keeps the reference's argument order and error behaviour.
+ * cross this boundary.  The Python host layer (crispybits_kernels/_C.py, a PyTorch-ROCm
+ * C++ extension over this header, csrc/torch_ext.cpp) binds it and keeps the reference's
+ * argument order and error behaviour.
  *
  * Conventions shared by all entry points
  *   - dtype: CBK_F16 / CBK_BF16 / CBK_F32 is the type of x, scales, zeros, bias and
@@ -25,6 +26,10 @@
  *     [0,0] contract holds trivially.  May be NULL.
  *   - partial: fp32 scratch of cbk_gemv_partial_floats(...) elements, required only when
  *     that query returns a positive count (split-K partial sums, packed_gemv.cu:193-199).
+ *     The streaming decode kernels combine the splits inside their own dispatch, using
+ *     arrival counters the library keeps per device in a window per stream (32 windows);
+ *     more than 32 streams making split calls at once on one device can share a window
+ *     and race.  The other decode kernels combine in a second launch.
  *   - device: HIP device ordinal the pointers live on (the reference's CUDAGuard,
  *     packed_gemv.cu:259); the calling thread's current device is restored on return.
  *   - return: CBK_OK, or an error code with a message from cbk_last_error().
