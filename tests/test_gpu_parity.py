@@ -350,6 +350,24 @@ def test_batched_split_in_dispatch(hip, bits, M, K, N):
         assert torch.equal(packed_linear(x, w), y)
 
 
+_SPLIT_CASES = [(int(m), int(k), int(n), int(b), int(sk)) for m, k, n, b, sk in zip(
+    np.random.default_rng(2024).integers(3, 17, 16), np.random.default_rng(2025).integers(2, 120, 16) * 128,
+    np.random.default_rng(2026).integers(16, 3000, 16), np.random.default_rng(2027).integers(2, 5, 16),
+    np.random.default_rng(2028).integers(1, 9, 16))]
+
+
+@pytest.mark.parametrize("M,K,N,bits,split_k", _SPLIT_CASES)
+def test_batched_random_shapes_and_splits(hip, M, K, N, bits, split_k):
+    """Seeded random batched decode calls (batch 3..16, K up to 15232, ragged N, a requested
+    split_k 1..8): whatever plan the library takes -- unsplit, split with the in-dispatch
+    combine, or the fallbacks -- the result matches the oracle, and a repeat is bit-identical."""
+    w, W64, _, _ = make(N, K, bits, torch.float16, seed=N, scale=0.02)
+    x = randx(M, K, torch.float16, seed=M + K)
+    y = packed_linear(x, w, split_k)
+    close(y, ref_linear(x, W64), torch.float16)
+    assert torch.equal(packed_linear(x, w, split_k), y)
+
+
 def test_split_counter_windows_across_streams(hip):
     """Split calls in flight on several streams at once each use their stream's counter window,
     and more streams than windows (40 > 32) take windows over in least-recently-used order:
