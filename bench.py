@@ -192,7 +192,13 @@ def main():
     ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm"),
                     help="run the fixed launch sequence of a counter pass and exit: gemv (default: the "
                          "W3 decode GEMV after a calibration copy) or gemm (the M=1024 W4 prefill GEMM)")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
+                    help="reduce a rocprofv3 kernel trace of a bench run to the markdown tables under "
+                         "profiles/ (the default command's timed step, or the batched sweep) and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(*args.trace_summary, steps=args.steps, warmup=args.warmup)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build targets one MI355X; --gpus {args.gpus} is not supported "
               "(one GPU's share is the same kernel at a smaller N: column-parallel linears shard output rows, "
@@ -310,6 +316,62 @@ def main():
         gw = make_weight(torch, 4096, 4096, 4, 0, dev)
         out["cpu_baseline"] = cpu_baseline(torch, base, xs, gw, randx(torch, 1024, 4096, 1, dev))
     print(json.dumps(out), flush=True)
+
+
+def trace_summary(trace_csv, bench_json, steps, warmup):
+    """Markdown tables of a rocprofv3 kernel trace of a bench run (needs no GPU).  With a
+    `batched` sweep in the bench line: per sweep row, its 6 x copies consecutive bstream
+    dispatches (eager run, warm replay, 4 timed replays; one kernel, grid and block checked) and
+    the kernel durations of the timed replays.  Otherwise: the timed step, the first run of
+    (warmup + steps) x 96 decode launches whose (kernel, grid, block) keys repeat with period 3,
+    per shape over its last steps x 96 launches, and the kernel time per step against the line."""
+    import csv
+    import re
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    line = json.loads(open(bench_json).read().strip().splitlines()[-1])
+    key = lambda r: (r["Kernel_Name"], int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
+    dur = lambda r: int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    name = lambda r: re.search(r"(gemv_\w+<[^>]*>)", r["Kernel_Name"]).group(1)
+    if "batched" in line:
+        b = [r for r in rows if re.search(r"gemv_(bstream|batch|reduce)", r["Kernel_Name"])]
+        print("| bits | M | K -> N | kernel | K splits | workgroups x threads | launches | kernel avg ns (trace) "
+              "| min ns | us per call (graph replays, traced run) |")
+        print("|---|---|---|---|---|---|---|---|---|---|")
+        i = 0
+        for j in line["batched"]:
+            part = b[i:i + 6 * j["copies"]]
+            assert len({key(r) for r in part}) == 1 and len(part) == 6 * j["copies"], j
+            t = [dur(r) for r in part[-4 * j["copies"]:]]
+            print(f"| W{j['bits']} | {j['M']} | {j['K']} -> {j['N']} | `{name(part[0])}` | {j['splits']} | "
+                  f"{int(part[0]['Grid_Size_X']) // int(part[0]['Workgroup_Size_X'])} x {part[0]['Workgroup_Size_X']} "
+                  f"| {j['launches']} | {statistics.mean(t):.0f} | {min(t)} | {j['us']} |")
+            i += 6 * j["copies"]
+        assert i == len(b), (i, len(b))
+        return
+    n = (steps + warmup) * 96
+    for i in range(len(rows) - n + 1):
+        seg = rows[i:i + n]
+        if all("gemv_stream_kernel" in r["Kernel_Name"] for r in seg) and \
+                all(key(seg[j]) == key(seg[j % 3]) for j in range(n)):
+            break
+    else:
+        raise SystemExit("timed region not found")
+    timed = seg[warmup * 96:]
+    d = [dur(r) for r in timed]
+    kms = sum(d) / steps / 1e6
+    span = (int(timed[-1]["End_Timestamp"]) - int(timed[0]["Start_Timestamp"])) / steps / 1e6
+    step_bytes = line["roofline"]["bytes_per_launch_avg"] * 96
+    print(f"traced run: ms_per_step {line['ms_per_step']}, kernel time per step {kms:.4f} ms, dispatch span per "
+          f"step {span:.4f} ms, value {line['value']}, frac (events) {line['roofline']['frac']}, frac (trace) "
+          f"{step_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS:.4f}, avg launch us (events) "
+          f"{line['roofline']['avg_launch_us']}, (trace) {sum(d) / len(d) / 1e3:.3f}")
+    print("| shape (K -> N) | kernel | grid (threads) | block | launches | avg ns | min ns | max ns |")
+    print("|---|---|---|---|---|---|---|---|")
+    for sh, (K, N) in enumerate(SHAPES):
+        ds = [dur(r) for r in timed[sh::3]]
+        r0 = timed[sh]
+        print(f"| {K} -> {N} | `{name(r0)}` | {r0['Grid_Size_X']} | {r0['Workgroup_Size_X']} | {len(ds)} | "
+              f"{statistics.mean(ds):.0f} | {min(ds)} | {max(ds)} |")
 
 
 def read_traffic():
