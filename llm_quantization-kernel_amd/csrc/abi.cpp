@@ -345,7 +345,7 @@ Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int
     return pl;
 }
 
-// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16 x with 16-byte pieces, any group
+// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16 or bf16 x with 16-byte pieces, any group
 // size that is a multiple of 32, 32-bit byte offsets into every tensor, and for
 // mixed-width QKV workgroups that stay inside one projection.  The K range of a
 // split is cut into slices of 64 * STREAM_CPL chunks (one wave each, at most 8);
@@ -358,12 +358,16 @@ struct StreamPlan {
     int P = 1, ks = 1, rw = 2, rpw = STREAM_RPW, mb = 1, grid = 0, lds = 0;
 };
 
+// Bytes the streaming kernel stages per chunk and batch row: 64 of operand pairs, then
+// (B, sum x), and for bf16 the chunk's power-of-two prescale as well.
+int stream_chunk_bytes(int dtype) { return dtype == CBK_BF16 ? 80 : 72; }
+
 // Slices a streaming job may hold: one wave each within the launch bound (16 waves),
-// and staged activations of 72 bytes per chunk and batch row plus the row-sum area
-// (at most 16 slices x 2 rows x 16 rows x 4 bytes) in the LDS.
-int stream_max_slices(int mb) {
+// and the staged activations per chunk and batch row plus the row-sum area (at most
+// 16 slices x 2 rows x 16 rows x 4 bytes) in the LDS.
+int stream_max_slices(int mb, int dtype) {
     const int waves = 16 / STREAM_CPL;
-    const int lds = (LDS_BUDGET - 16 * 2 * 16 * 4) / (64 * STREAM_CPL * 72 * mb);
+    const int lds = (LDS_BUDGET - 16 * 2 * 16 * 4) / (64 * STREAM_CPL * stream_chunk_bytes(dtype) * mb);
     return std::max(1, std::min(waves, lds));
 }
 
@@ -379,7 +383,7 @@ int stream_splits(int64_t C, int split_k, int max_slices) {
 StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k) {
     StreamPlan sp;
     const int64_t lim = INT32_MAX;
-    bool ok = A.M >= 1 && A.M <= 2 && dtype == CBK_F16 && A.gs % 32 == 0 && A.K % 8 == 0 &&
+    bool ok = A.M >= 1 && A.M <= 2 && (dtype == CBK_F16 || dtype == CBK_BF16) && A.gs % 32 == 0 && A.K % 8 == 0 &&
               reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
     for (int i = 0; i < 3; ++i)
         ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
@@ -387,7 +391,7 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
     sp.mb = A.M;
     const int max_waves = 16;                           // the kernel's launch bound: 1024 threads
     const int64_t slice = 64 * STREAM_CPL;
-    sp.P = stream_splits(A.C, split_k, stream_max_slices(sp.mb));
+    sp.P = stream_splits(A.C, split_k, stream_max_slices(sp.mb, dtype));
     if ((int64_t)A.C * sp.P >= (1ll << 32)) return sp;     // split bounds C p / P in 32 bits
     sp.ks = (int)ceil_div(ceil_div(A.C, sp.P), slice);
     if (sp.ks * STREAM_CPL > max_waves) return sp;
@@ -402,7 +406,7 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
     const int64_t grid = ceil_div(A.V, rb) * sp.P;
     if (grid >= lim) return sp;
     sp.grid = (int)grid;
-    sp.lds = (int)(sp.ks * slice * 72 * sp.mb + (int64_t)sp.ks * sp.mb * rb * 4);
+    sp.lds = (int)(sp.ks * slice * stream_chunk_bytes(dtype) * sp.mb + (int64_t)sp.ks * sp.mb * rb * 4);
     sp.ok = true;
     return sp;
 }
@@ -670,7 +674,7 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divGS = make_fastdiv((uint32_t)(A.gs / 32));
         L.family = CBK_KERNEL_STREAM;
-        L.f = gemv_stream_kernel_for(mode, A.p[0].bits, mixed, sp.mb, sp.rpw);
+        L.f = gemv_stream_kernel_for(mode, A.p[0].bits, mixed, sp.mb, sp.rpw, dtype == CBK_BF16);
         L.grid = sp.grid;
         L.block = 64 * sp.ks * sp.rw;
         L.lds = sp.lds;
@@ -918,7 +922,7 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
             }
         }
     }
-    if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M)));
+    if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M, dtype)));
     if (M >= 3 && M <= 16) {  // 4-unit slices split at least as often as 8-unit ones; gate-up rows
         const int64_t C = ceil_div(K, 32);
         P = std::max(P, bstream_splits(C, M, split_k, bstream_rw(M, 4, true), 4));

@@ -274,15 +274,15 @@ __device__ __forceinline__ float split_sum(const GemvArgs& A, int b, int v) {
 }
 
 // The combining workgroup's epilogue: rows [vbase, vbase + RB) of every batch row,
-// `nthr` threads (fp16 outputs: the streaming kernels' dtype).
-template <int MODE>
+// `nthr` threads, outputs of dtype DT.
+template <int DT, int MODE>
 __device__ __forceinline__ void split_epilogue(const GemvArgs& A, int vbase, int RB, int nthr) {
     for (int t = threadIdx.x; t < A.M * RB; t += nthr) {
         const int b = t / RB, v = vbase + (t - b * RB);
         if (v < A.V) {
             const bool paired = MODE == MODE_GATEUP || (MODE == MODE_QKV && A.rope_cos != nullptr);
             const float partner = paired && (v ^ 1) < A.V ? split_sum(A, b, v ^ 1) : 0.f;
-            epilogue<DT_F16, MODE>(A, b, v, split_sum(A, b, v), partner);
+            epilogue<DT, MODE>(A, b, v, split_sum(A, b, v), partner);
         }
     }
 }

@@ -19,7 +19,7 @@ hipError_t lds_limit_raise(const void* f, int bytes);
 // queries and the launch; max_batch <= 1 selects the single-row epilogue.
 const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);
 
-// gemv_stream.hip: batch 1 or 2 (mb staged activation rows), fp16, group size % 32 == 0.  A job is rpw * st_rw
+// gemv_stream.hip: batch 1 or 2 (mb staged activation rows), fp16 or bf16, group size % 32 == 0.  A job is rpw * st_rw
 // virtual rows x one K split; its workgroup has st_ks * st_rw waves, each over rpw rows
 // (STREAM_RPW, or STREAM_RPW_WIDE at batch 1) and one K slice of 64 * STREAM_CPL chunks.
 #ifndef CBK_STREAM_CPL
@@ -28,7 +28,7 @@ const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);
 constexpr int STREAM_CPL = CBK_STREAM_CPL;
 constexpr int STREAM_RPW = 4;
 constexpr int STREAM_RPW_WIDE = 8;
-const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw);
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw, bool bf16);
 // gemv_stream.hip: batch 3..16, fp16, group size % 128 == 0.  A job is 16 * st_rw virtual
 // rows x one K split (over 128-code units); its workgroup has st_ks * st_rw waves, each
 // over 16 rows and one K slice of bsu (4 or 8) units.

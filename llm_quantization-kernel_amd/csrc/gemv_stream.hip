@@ -1,9 +1,9 @@
-// gemv_stream.hip -- batch-1 fp16 decode GEMV that streams packed rows through VGPRs.
+// gemv_stream.hip -- decode GEMVs that stream packed rows through VGPRs.
 //
 // Replaces cb_gemv_kernel (Kernel/csrc/packed_gemv.cu:83-163) and, when the K
 // range is split, the partial write that cb_reduce_kernel (:166-180) combines,
-// for one or two activation rows (the decode step) in fp16 with any group size that is a
-// multiple of 32.  Plain, fused-QKV and fused gate-up modes share the body; the
+// for one or two activation rows (the decode step) in fp16 or bf16 with any group size
+// that is a multiple of 32.  Plain, fused-QKV and fused gate-up modes share the body; the
 // epilogue is cb_epilogue's (:54-81, cbk_device.hpp).
 //
 // Job = (block of RB = RPW RW virtual rows, K split p).  A workgroup holds KS x RW
@@ -18,7 +18,9 @@
 //      (cbk_decode.hpp): pair p = (x_a 2^-e_a, x_b 2^-e_b) for the codes kappa and
 //      field offsets expo of the chunk's half slots, with the chunk's slot-offset
 //      sum B = 1024 sum_p X_p and its plain sum sum_j x_j, into LDS; one barrier
-//      publishes them to every wave of the workgroup.
+//      publishes them to every wave of the workgroup.  bf16 chunks are first scaled
+//      by a power of two 2^-c of their own (convert_x_bf16), so the fp16 operands
+//      hold every bf16 value exactly; the chunk's terms are scaled back by 2^c.
 //   3. Per row and chunk: the BITS words decode into 16 fp16 pairs 1024 + 2^e q by
 //      one v_and_or_b32 each, 16 v_dot2_f32_f16 against the staged pairs give
 //      sum x q + B, and acc += s * (dot - B - z * sum x)  (packed_gemv.cu:113-138
@@ -124,6 +126,54 @@ __device__ __forceinline__ void convert_x(const uint32_t (&x)[16], u4 (&X)[4], f
     xs = t;
 }
 
+// bf16 activations.  The chunk is prescaled by 2^-c, c taken from its largest exponent so
+// that its largest magnitude lands in [2^14, 2^15): times 2^-e (e <= 5) that stays inside
+// fp16's range, and every element at least 2^-23 of the largest is a normal fp16 number
+// after the scaling, where its 8 significant bits are exact (smaller ones lose bits only
+// below 2^-34 of it).  X and B are the fp16 operands as in convert_x; xs = sum x 2^-c
+// (fp32) and f = 2^c scales the chunk's terms back.  Infinities and NaNs stay what they
+// are; c >= -126 keeps f a normal float.
+template <int BITS>
+__device__ __forceinline__ void convert_x_bf16(const uint32_t (&x)[16], u4 (&X)[4], float& B, float& xs, float& f) {
+    typedef uint16_t us2 __attribute__((ext_vector_type(2)));
+    us2 m = {0, 0};
+#pragma unroll
+    for (int p = 0; p < 16; ++p) m = __builtin_elementwise_max(m, __builtin_bit_cast(us2, x[p] & 0x7F807F80u));
+    const int E = (int)(max(m.x, m.y) >> 7);                 // largest biased exponent of the chunk
+    const int c = max(E - (127 + 14), -126);
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    uint32_t o[16];
+    float b = 0.f, t = 0.f;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+        const int ka = Decode<BITS>::kappa(2 * p), kb = Decode<BITS>::kappa(2 * p + 1);
+        const int ea = Decode<BITS>::expo(2 * p), eb = Decode<BITS>::expo(2 * p + 1);
+        const uint32_t wa = x[ka >> 1], wb = x[kb >> 1];
+        const float xa = __uint_as_float((ka & 1) ? (wa & 0xFFFF0000u) : (wa << 16));
+        const float xb = __uint_as_float((kb & 1) ? (wb & 0xFFFF0000u) : (wb << 16));
+        const h2 v = {(_Float16)__builtin_ldexpf(xa, -c - ea), (_Float16)__builtin_ldexpf(xb, -c - eb)};
+        o[p] = __builtin_bit_cast(uint32_t, v);
+        b = __builtin_amdgcn_fdot2(v, one, b, false);
+        t += __uint_as_float(x[p] << 16) + __uint_as_float(x[p] & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) X[q] = u4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+    B = 1024.f * b;
+    xs = __builtin_ldexpf(t, -c);
+    f = __builtin_ldexpf(1.0f, c);
+}
+
+// Bytes staged per chunk and batch row after its 64 bytes of operand pairs: (B, sum x),
+// and for bf16 also 2^c (a 16-byte entry).
+template <int DT> constexpr int XB_BYTES = DT == DT_BF16 ? 16 : 8;
+
+// A (scale, zero) half of the activations' dtype as a float.
+template <int DT>
+__device__ __forceinline__ float meta_f(uint32_t bits) {
+    if constexpr (DT == DT_BF16) return __uint_as_float(bits << 16);
+    else return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
 // sum x q + B of one row's chunk: its 16 decoded pairs against one batch row's
 // staged operands.
 __device__ __forceinline__ float pairs_dot(const uint32_t (&h)[16], const u4 (&X)[4]) {
@@ -169,7 +219,7 @@ __device__ __forceinline__ void barrier_lds() {
     __builtin_amdgcn_s_barrier();
 }
 
-template <int BITS, int MODE, int MB, int RPW>
+template <int BITS, int MODE, int MB, int RPW, int DT>
 __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -234,20 +284,27 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     }
 
     // 2. activations -> LDS: piece q of chunk c of batch row b at ((b * 4 + q) NCH + c) * 16,
-    // (B, sum x) at 64 MB NCH + 8 (b NCH + c); chunks past the split read as zero (they
-    // meet no weights)
+    // (B, sum x[, 2^c]) at 64 MB NCH + XB (b NCH + c); chunks past the split read as zero
+    // (they meet no weights)
+    constexpr int XBB = XB_BYTES<DT>;
     u4* Xl = reinterpret_cast<u4*>(lds);
-    float2* XBl = reinterpret_cast<float2*>(lds + 64 * MB * NCH);
-    float* red = reinterpret_cast<float*>(lds + 72 * MB * NCH);
+    char* XBl = lds + 64 * MB * NCH;
+    float* red = reinterpret_cast<float*>(lds + (64 + XBB) * MB * NCH);
     if (tid < NCH) {
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
             u4 X[4];
             float B, xs;
-            convert_x<BITS>(xa[b], X, B, xs);
+            if constexpr (DT == DT_BF16) {
+                float f;
+                convert_x_bf16<BITS>(xa[b], X, B, xs, f);
+                *reinterpret_cast<float4*>(XBl + XBB * (b * NCH + tid)) = make_float4(B, xs, f, 0.f);
+            } else {
+                convert_x<BITS>(xa[b], X, B, xs);
+                *reinterpret_cast<float2*>(XBl + XBB * (b * NCH + tid)) = make_float2(B, xs);
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q) Xl[(b * 4 + q) * NCH + tid] = X[q];
-            XBl[b * NCH + tid] = make_float2(B, xs);
         }
     }
     barrier_lds();
@@ -255,6 +312,7 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     // 3. rows: each chunk is decoded once and meets every batch row's activations
     u4 X[MB][CPL][4];
     float2 XB[MB][CPL];
+    float XF[MB][CPL];                   // 2^c of a bf16 chunk
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
 #pragma unroll
@@ -262,7 +320,14 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
             const int c = ks * SLICE + lane + 64 * i;
 #pragma unroll
             for (int q = 0; q < 4; ++q) X[b][i][q] = Xl[(b * 4 + q) * NCH + c];
-            XB[b][i] = XBl[b * NCH + c];
+            if constexpr (DT == DT_BF16) {
+                const float4 e = *reinterpret_cast<const float4*>(XBl + XBB * (b * NCH + c));
+                XB[b][i] = make_float2(e.x, e.y);
+                XF[b][i] = e.z;
+            } else {
+                XB[b][i] = *reinterpret_cast<const float2*>(XBl + XBB * (b * NCH + c));
+                XF[b][i] = 1.f;
+            }
         }
     }
     float acc[MB][RPW];
@@ -274,12 +339,13 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
         for (int i = 0; i < CPL; ++i) {
             uint32_t h[16];
             Decode<BITS>::run(w[j][i], h, g);
-            const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[j][i][0]);
-            const float z = (float)__builtin_bit_cast(_Float16, (uint16_t)sz[j][i][1]);
+            const float s = meta_f<DT>(sz[j][i][0]);
+            const float z = meta_f<DT>(sz[j][i][1]);
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
                 const float d = pairs_dot(h, X[b][i]);
-                acc[b][j] = fmaf(s, d - fmaf(z, XB[b][i].y, XB[b][i].x), acc[b][j]);
+                const float t = d - fmaf(z, XB[b][i].y, XB[b][i].x);
+                acc[b][j] = fmaf(s, DT == DT_BF16 ? t * XF[b][i] : t, acc[b][j]);
             }
         }
     }
@@ -306,13 +372,13 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
                 mine += red[(k * MB + b) * RB + row];
                 partner += red[(k * MB + b) * RB + (row ^ 1)];
             }
-            if (A.P == 1) epilogue<DT_F16, MODE>(A, b, v, mine, partner);
+            if (A.P == 1) epilogue<DT, MODE>(A, b, v, mine, partner);
             else partial_put(A.partial + ((long)p * A.M + b) * A.V + v, mine);
         }
     }
     // 6. with P > 1 and arrival counters, the last split of the block combines
     if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
-        split_epilogue<MODE>(A, vbase, RB, 64 * KS * RW);
+        split_epilogue<DT, MODE>(A, vbase, RB, 64 * KS * RW);
 }
 
 // ------------------------------------------------------------------ batch rows 3..16
@@ -492,7 +558,7 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     }
     // 6. with P > 1 and arrival counters, the last split of the block combines
     if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
-        split_epilogue<MODE>(A, vbase, RB, nthr);
+        split_epilogue<DT_F16, MODE>(A, vbase, RB, nthr);
 }
 
 template <int MODE, int BITS, int BSU>
@@ -516,28 +582,28 @@ __global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
 // the activations, which at K = 11008 leaves one workgroup per CU; they take the
 // batch-rows MFMA kernel instead.  RPW rows per wave (4, or 8 for the host's short-K
 // batch-1 plan: half the waves for the same rows per workgroup).
-template <int MODE, int BITS, int MB, int RPW>
+template <int MODE, int BITS, int MB, int RPW, int DT>
 __global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
-        stream_body<BITS, MODE, MB, RPW>(A, lds);
+        stream_body<BITS, MODE, MB, RPW, DT>(A, lds);
     } else {
         int proj, r;
         vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * RPW * A.st_rw, proj, r);
         const int bits = CBK_SEL(A, proj, bits);
-        if (bits == 2) stream_body<2, MODE, MB, RPW>(A, lds);
-        else if (bits == 3) stream_body<3, MODE, MB, RPW>(A, lds);
-        else stream_body<4, MODE, MB, RPW>(A, lds);
+        if (bits == 2) stream_body<2, MODE, MB, RPW, DT>(A, lds);
+        else if (bits == 3) stream_body<3, MODE, MB, RPW, DT>(A, lds);
+        else stream_body<4, MODE, MB, RPW, DT>(A, lds);
     }
 }
 
-template <int MB, int RPW>
+template <int MB, int RPW, int DT>
 const void* stream_kernel(int mode, int bits, bool mixed) {
-    if (mixed) return reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_QKV, 0, MB, RPW>);
+    if (mixed) return reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_QKV, 0, MB, RPW, DT>);
 #define CBK_STREAM_K(M)                                                                            \
-    (bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 2, MB, RPW>)                 \
-               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 3, MB, RPW>)    \
-                            : reinterpret_cast<const void*>(&gemv_stream_kernel<M, 4, MB, RPW>)))
+    (bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 2, MB, RPW, DT>)             \
+               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<M, 3, MB, RPW, DT>)\
+                            : reinterpret_cast<const void*>(&gemv_stream_kernel<M, 4, MB, RPW, DT>)))
     if (mode == MODE_QKV) return CBK_STREAM_K(MODE_QKV);
     if (mode == MODE_GATEUP) return CBK_STREAM_K(MODE_GATEUP);
     return CBK_STREAM_K(MODE_GEMV);
@@ -559,15 +625,21 @@ const void* bstream_kernel(int mode, int bits, bool mixed) {
 
 }  // namespace
 
-const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw) {
-    if (mb > 1) return stream_kernel<2, STREAM_RPW>(mode, bits, mixed);
+template <int DT>
+const void* stream_kernel_dt(int mode, int bits, bool mixed, int mb, int rpw) {
+    if (mb > 1) return stream_kernel<2, STREAM_RPW, DT>(mode, bits, mixed);
     if (rpw == STREAM_RPW_WIDE && mode == MODE_GEMV && !mixed) {     // the host plans 8 rows for plain GEMVs only
         constexpr int W = STREAM_RPW_WIDE;
-        return bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 2, 1, W>)
-                         : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 3, 1, W>)
-                                      : reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 4, 1, W>));
+        return bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 2, 1, W, DT>)
+                         : (bits == 3 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 3, 1, W, DT>)
+                                      : reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 4, 1, W, DT>));
     }
-    return stream_kernel<1, STREAM_RPW>(mode, bits, mixed);
+    return stream_kernel<1, STREAM_RPW, DT>(mode, bits, mixed);
+}
+
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw, bool bf16) {
+    return bf16 ? stream_kernel_dt<DT_BF16>(mode, bits, mixed, mb, rpw)
+                : stream_kernel_dt<DT_F16>(mode, bits, mixed, mb, rpw);
 }
 
 const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu) {

@@ -567,3 +567,86 @@ def test_baseline_prefill_activation_ranges(hip, dist, K, N):
     x = randx_dist(1024, K, dist)
     rows = torch.from_numpy(_row_sample(1024)).cuda()
     close(packed_linear(x, w)[rows], gemm_ref(x[rows], d, torch.float16, 3, K, 128), torch.float16)
+
+
+# ------------------------------------------------------------------ bf16 decode (streaming kernel)
+
+def randx_bf16(M, K, dist, seed=1):
+    """bf16 activations: N(0,1), scaled by 1e-3 ("small"), with 4 seeded channels x50
+    ("outlier"), scaled by 1e5 ("wide", past fp16's range) or by 1e-30 ("tiny", below it)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    if dist == "small":
+        x = x * 1e-3
+    elif dist == "outlier":
+        ch = np.random.default_rng(seed).choice(K, 4, replace=False)
+        x[:, torch.from_numpy(ch)] *= 50.0
+    elif dist == "wide":
+        x = x * 1e5
+    elif dist == "tiny":
+        x = x * 1e-30
+    return x.to(torch.bfloat16).cuda()
+
+
+def close_bf16(y, ref):
+    """bf16 outputs: max|y - ref| / max|ref| (no floor on the denominator, so tiny outputs are
+    held to the same relative bar) below the reference's bf16 tolerance 2e-2 and below 5e-3,
+    about one bf16 rounding of the output (2^-8) over the fp32 accumulation."""
+    yv = y.detach().float().cpu().double().numpy()
+    assert np.isfinite(yv).all()
+    e = np.abs(yv - ref).max() / np.abs(ref).max()
+    assert e < TOL[torch.bfloat16] and e < 5e-3, f"rel err {e:.2e}"
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("kind,out", [("gemv", 4096), ("gemv", 11008), ("gate_up", 11008),
+                                      ("qkv", (4096, 1024, 1024))])
+@pytest.mark.parametrize("K", [4096, 11008])
+def test_bf16_decode_streams(hip, M, kind, out, K):
+    """bf16 decode at batch 1-2 takes the streaming kernel (one dispatch), as fp16 does."""
+    fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.bfloat16, M, K, 128, out, 3, kind, 1, 1)
+    assert fam == "stream", (fam, splits, launches)
+    f16 = _C.decode_plan(torch.float16, M, K, 128, out, 3, kind, 1, 1)
+    assert (splits, grid, threads) == tuple(f16[1:4])
+    assert lds > f16[4]            # the per-chunk prescale is staged beside each chunk's sums
+
+
+@pytest.mark.parametrize("dist", ["normal", "small", "outlier", "wide", "tiny"])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096)])
+@pytest.mark.parametrize("M", [1, 2])
+def test_bf16_baseline_gemv(hip, dist, bits, K, N, M):
+    """configs[1]/[2] shapes with bf16 activations, scales and outputs against the oracle,
+    over activation ranges an fp16 staging could not hold without the per-chunk prescale."""
+    w, W64, _, _ = make(N, K, bits, torch.bfloat16, scale=0.02)
+    x = randx_bf16(M, K, dist, seed=M + bits)
+    close_bf16(packed_linear(x, w), ref_linear(x, W64))
+
+
+@pytest.mark.parametrize("split_k", [2, 5])
+@pytest.mark.parametrize("M", [1, 2])
+def test_bf16_gemv_splits(hip, split_k, M):
+    """Requested K splits of the bf16 streaming GEMV (combined in the dispatch) against the
+    oracle, and bit-equal on a repeated call."""
+    w, W64, b64, _ = make(1000, 11008, 3, torch.bfloat16, bias=True, seed=7, scale=0.02)
+    x = randx_bf16(M, 11008, "outlier", seed=split_k)
+    y = packed_linear(x, w, split_k=split_k)
+    close_bf16(y, ref_linear(x, W64, b64))
+    assert torch.equal(packed_linear(x, w, split_k=split_k), y)
+
+
+@pytest.mark.parametrize("dist", ["normal", "wide"])
+@pytest.mark.parametrize("M", [1, 2])
+def test_bf16_fused_decode(hip, dist, M):
+    """Fused QKV (mixed widths) and fused gate-up in bf16 on the streaming kernel."""
+    bits = tuple(int(b) for b in np.random.default_rng(M).choice([2, 3, 4], 3))
+    q, Q64, _, _ = make(4096, 4096, bits[0], torch.bfloat16, seed=1, scale=0.02)
+    k, K64, _, _ = make(1024, 4096, bits[1], torch.bfloat16, seed=2, scale=0.02)
+    v, V64, _, _ = make(1024, 4096, bits[2], torch.bfloat16, seed=3, scale=0.02)
+    x = randx_bf16(M, 4096, dist, seed=11)
+    for o, W in zip(fused_qkv(x, q, k, v), (Q64, K64, V64)):
+        close_bf16(o, ref_linear(x, W))
+    g, G64, _, _ = make(11008, 4096, 3, torch.bfloat16, seed=4, scale=0.02)
+    u, U64, _, _ = make(11008, 4096, 3, torch.bfloat16, seed=5, scale=0.02)
+    gv, uv = ref_linear(x, G64), ref_linear(x, U64)
+    close_bf16(fused_gate_up(x, g, u), gv / (1 + np.exp(-gv)) * uv)
