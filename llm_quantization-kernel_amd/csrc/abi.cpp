@@ -1094,7 +1094,7 @@ int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K, const int32_
     A.divG = make_fastdiv((uint32_t)group_size);
     const bool mc = use_matrix_cores && (dtype == CBK_F16 || dtype == CBK_BF16);
     hipError_t e;
-    if (mc && dtype == CBK_F16 && gemm_f16_supported(A)) e = launch_gemm_f16(A, s);
+    if (mc && gemm_f16_supported(A)) e = launch_gemm_f16(A, dtype, s);
     else e = mc ? launch_gemm_mfma(A, dtype, s) : launch_gemm_valu(A, dtype, s);
     if (e != hipSuccess) return hip_fail(e, "packed_gemm: launch");
     return CBK_OK;

@@ -67,9 +67,9 @@ struct GemmArgs {
 hipError_t launch_gemm_mfma(const GemmArgs& A, int dt, hipStream_t stream);
 hipError_t launch_gemm_valu(const GemmArgs& A, int dt, hipStream_t stream);
 
-// gemm_f16.hip: fp16, K % 8 == 0, 16-byte aligned x.
+// gemm_f16.hip: fp16 or bf16 (dt), K % 8 == 0, 16-byte aligned x.
 bool gemm_f16_supported(const GemmArgs& A);
-hipError_t launch_gemm_f16(const GemmArgs& A, hipStream_t stream);
+hipError_t launch_gemm_f16(const GemmArgs& A, int dt, hipStream_t stream);
 
 // quant.hip: group-affine quantizer + bit packer (the format's producer).
 struct QuantArgs {

@@ -1,7 +1,7 @@
-// gemm_f16.hip -- fp16 prefill packed GEMM on gfx950: out[M,N] = act(x . W-hat^T + bias).
+// gemm_f16.hip -- fp16 / bf16 prefill packed GEMM on gfx950: out[M,N] = act(x . W-hat^T + bias).
 //
-// Replaces cb_gemm_tc_kernel (Kernel/csrc/packed_gemm.cu:12-117) for fp16
-// activations, with the reference's weight rounding W-hat = RN_fp16((q - z) * s)
+// Replaces cb_gemm_tc_kernel (Kernel/csrc/packed_gemm.cu:12-117) for fp16 and bf16
+// activations, with the reference's weight rounding W-hat = RN_T((q - z) * s)
 // (packed_gemm.cu:56,60).
 //
 // Tile: 128 x 128 outputs per workgroup of eight waves, two per SIMD.  Wave w owns
@@ -35,8 +35,11 @@
 // columns is an integer below 1024 in magnitude (the reference quantizer's; each
 // wave scans its columns' zeros once): the difference is an exact integer and the
 // product rounds once, exactly RN_fp16((q - z) * s).  Other zero points take the
-// fp32 product.  Codes at k >= K meet zero activations, so the tail of the last
-// weight block contributes nothing.
+// fp32 product.  bf16 (v_mfma_f32_32x32x16_bf16): the codes go to fp32 (v_cvt_f32_ubyte),
+// W-hat = RN_bf16(fma(q, s, -z s)) with integer zeros (both products exact in fp32, so
+// the fma returns (q - z) s exactly), else RN_bf16((q - z) * s) in fp32 -- the
+// reference's fp32 value rounded once.  Codes at k >= K meet zero activations, so
+// the tail of the last weight block contributes nothing.
 #include "cbk_decode.hpp"
 #include "cbk_device.hpp"
 #include "cbk_kernels.hpp"
@@ -45,6 +48,8 @@ namespace cbk {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
@@ -238,9 +243,17 @@ __device__ __forceinline__ _Float16 half_of(uint32_t v) {
     return __builtin_bit_cast(_Float16, (uint16_t)v);
 }
 
-// An fp16 zero point allows the packed-fp16 form: an integer below 1024 in magnitude.
+// A scale or zero point of the activations' dtype (raw bits) as a float.
+template <int DT>
+__device__ __forceinline__ float meta_f(uint32_t bits) {
+    if constexpr (DT == DT_BF16) return __uint_as_float(bits << 16);
+    else return (float)half_of(bits);
+}
+
+// A zero point that allows the exact fast form: an integer below 1024 in magnitude.
+template <int DT>
 __device__ __forceinline__ bool zero_is_small_int(uint32_t zbits) {
-    const float zf = (float)half_of(zbits);
+    const float zf = meta_f<DT>(zbits & 0xFFFFu);
     return zf == __builtin_rintf(zf) && __builtin_fabsf(zf) < 1024.f;
 }
 
@@ -263,6 +276,7 @@ __device__ __forceinline__ void scan_issue(const GemmArgs& A, int c0, int lane, 
     }
 }
 
+template <int DT>
 __device__ __forceinline__ bool scan_finish(const GemmArgs& A, int c0, int lane, const ZScan& zs) {
     const uint16_t* z = reinterpret_cast<const uint16_t*>(A.z);
     const long beg = (long)c0 * A.G, end = (long)min(c0 + 32, A.N) * A.G;
@@ -271,16 +285,16 @@ __device__ __forceinline__ bool scan_finish(const GemmArgs& A, int c0, int lane,
     for (int u = 0; u < SCAN_U; ++u)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            ok &= zero_is_small_int(zs.v[u][j] & 0xFFFFu) & zero_is_small_int(zs.v[u][j] >> 16);
+            ok &= zero_is_small_int<DT>(zs.v[u][j] & 0xFFFFu) & zero_is_small_int<DT>(zs.v[u][j] >> 16);
     for (long i = beg + 8 * lane; i < end; i += 8 * 64) {
         if (i + 8 <= end) {
             if (i < beg + 512 * SCAN_U) continue;      // preloaded
             const u4 v = *reinterpret_cast<const u4*>(z + i);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                ok &= zero_is_small_int(v[j] & 0xFFFFu) & zero_is_small_int(v[j] >> 16);
+                ok &= zero_is_small_int<DT>(v[j] & 0xFFFFu) & zero_is_small_int<DT>(v[j] >> 16);
         } else {
-            for (long e = i; e < end; ++e) ok &= zero_is_small_int(z[e]);
+            for (long e = i; e < end; ++e) ok &= zero_is_small_int<DT>(z[e]);
         }
     }
     return __builtin_amdgcn_ballot_w64(!ok) == 0;
@@ -342,10 +356,28 @@ template <> struct Octet<3> {
     }
 };
 
-// B operand of the wave's step kq: octet kq of the lane's chunk.  FAST: every zero
-// point of the wave's columns is an integer below 1024 in magnitude.
-template <int BITS, bool FAST>
+// B operand of the wave's step kq: octet kq of the lane's chunk.  DQ: 0 fp16, 1 fp16
+// with every zero point of the wave's columns an integer below 1024 in magnitude (the
+// packed-fp16 form), 2 bf16, 3 bf16 with such zero points (the fma form).
+template <int BITS, int DQ>
 __device__ __forceinline__ u4 dequant_octet(const WStage<BITS>& r, int kq, uint32_t g) {
+    if constexpr (DQ >= 2) {
+        const float zf = meta_f<DT_BF16>(r.z), sf = meta_f<DT_BF16>(r.s);
+        const float czs = -zf * sf;                   // exact when DQ == 3
+        uint32_t h[4];
+        Octet<BITS>::run(r.w, kq, 0u, h);             // codes 2i, 2i+1 at bits 0 and 16
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float lo = (float)(h[i] & 0xFFu), hi = (float)((h[i] >> 16) & 0xFFu);
+            const float a = DQ == 3 ? fmaf(lo, sf, czs) : (lo - zf) * sf;
+            const float b = DQ == 3 ? fmaf(hi, sf, czs) : (hi - zf) * sf;
+            const b2 v = {(__bf16)a, (__bf16)b};
+            o[i] = __builtin_bit_cast(uint32_t, v);
+        }
+        return u4{o[0], o[1], o[2], o[3]};
+    }
+    constexpr bool FAST = DQ == 1;
     const float zf = (float)half_of(r.z);
     const _Float16 cz = (_Float16)(1024.f + zf);      // exact when FAST: an integer below 2048
     const _Float16 sh = half_of(r.s);
@@ -428,11 +460,17 @@ __device__ __forceinline__ void read_w(const GemmArgs& A, const lds_t* lds, int 
 }
 
 // One k-step: 4 MFMAs of 32 x 32 x 16 (rows 32 a .. of the slab, the lane's column).
+template <bool BF>
 __device__ __forceinline__ void mma_step(const u4 (&af)[4], const u4& bw, f16x (&acc)[4]) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-        acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(&af[a]),
-                                                        *reinterpret_cast<const h8*>(&bw), acc[a], 0, 0, 0);
+    for (int a = 0; a < 4; ++a) {
+        if constexpr (BF)
+            acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const b8*>(&af[a]),
+                                                             *reinterpret_cast<const b8*>(&bw), acc[a], 0, 0, 0);
+        else
+            acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const h8*>(&af[a]),
+                                                            *reinterpret_cast<const h8*>(&bw), acc[a], 0, 0, 0);
+    }
 }
 
 // Everything a stage needs besides its operands.
@@ -457,7 +495,7 @@ struct Ctx {
 // slots 0 .. 3 (activation stage s + 3 into the slot of stage s), read steps 0 and
 // 1 of stage s + 1 and its chunk (wn), and dequantize its step 0, leaving the entry
 // state of stage s + 1.  The last stage (!NEXT) issues nothing.  ODD: s is odd.
-template <int BITS, bool TAIL, bool GS128, bool FAST, bool NEXT, bool ODD>
+template <int BITS, bool TAIL, bool GS128, int DQ, bool NEXT, bool ODD>
 __device__ __forceinline__ void run_stage(Ctx<BITS>& c, int s, u4 (&a)[4][4], u4& bw, const WStage<BITS>& wc,
                                           WStage<BITS>& wn, const Group& gc, Group& gn, f16x (&acc)[4]) {
     const int nslot = c.cslot == NSTAGE - 1 ? 0 : c.cslot + 1;
@@ -467,9 +505,9 @@ __device__ __forceinline__ void run_stage(Ctx<BITS>& c, int s, u4 (&a)[4][4], u4
         else if (NEXT) read_a(c.lds, nslot, kq - 2, c.ci, a[(kq + 2) & 3]);
         if (NEXT && kq == 2) read_w<BITS, GS128>(c.A, c.lds, s + 1, c.ci, wn);
         u4 bwn = bw;
-        if (kq + 1 < KSTEPS) bwn = dequant_octet<BITS, FAST>(wc, kq + 1, c.g);
-        else if (NEXT) bwn = dequant_octet<BITS, FAST>(wn, 0, c.g);
-        mma_step(a[kq & 3], bw, acc);
+        if (kq + 1 < KSTEPS) bwn = dequant_octet<BITS, DQ>(wc, kq + 1, c.g);
+        else if (NEXT) bwn = dequant_octet<BITS, DQ>(wn, 0, c.g);
+        mma_step<(DQ >= 2)>(a[kq & 3], bw, acc);
         bw = bwn;
         if (NEXT && kq <= 1) {
             issue_slot<BITS, TAIL, !ODD>(c.L, gc, 4 + 2 * kq, c.lds);
@@ -491,7 +529,7 @@ __device__ __forceinline__ void run_stage(Ctx<BITS>& c, int s, u4 (&a)[4][4], u4
 // The stages, unrolled by two so the chunk and group registers of stage s and
 // stage s + 1 alternate without copies and the load-group parity is static; the
 // last stage is peeled.
-template <int BITS, bool TAIL, bool GS128, bool FAST>
+template <int BITS, bool TAIL, bool GS128, int DQ>
 __device__ __forceinline__ void compute_loop(Ctx<BITS>& c, int nst, Group& g0, f16x (&acc)[4]) {
     u4 a[4][4], bw;
     WStage<BITS> w0, w1;
@@ -499,21 +537,21 @@ __device__ __forceinline__ void compute_loop(Ctx<BITS>& c, int nst, Group& g0, f
     read_a(c.lds, 0, 0, c.ci, a[0]);
     read_a(c.lds, 0, 1, c.ci, a[1]);
     read_w<BITS, GS128>(c.A, c.lds, 0, c.ci, w0);
-    bw = dequant_octet<BITS, FAST>(w0, 0, c.g);
+    bw = dequant_octet<BITS, DQ>(w0, 0, c.g);
     int s = 0;
     for (; s + 2 < nst; s += 2) {
-        run_stage<BITS, TAIL, GS128, FAST, true, false>(c, s, a, bw, w0, w1, g0, g1, acc);
-        run_stage<BITS, TAIL, GS128, FAST, true, true>(c, s + 1, a, bw, w1, w0, g1, g0, acc);
+        run_stage<BITS, TAIL, GS128, DQ, true, false>(c, s, a, bw, w0, w1, g0, g1, acc);
+        run_stage<BITS, TAIL, GS128, DQ, true, true>(c, s + 1, a, bw, w1, w0, g1, g0, acc);
     }
     if (s + 1 < nst) {
-        run_stage<BITS, TAIL, GS128, FAST, true, false>(c, s, a, bw, w0, w1, g0, g1, acc);
-        run_stage<BITS, TAIL, GS128, FAST, false, true>(c, s + 1, a, bw, w1, w0, g1, g0, acc);
+        run_stage<BITS, TAIL, GS128, DQ, true, false>(c, s, a, bw, w0, w1, g0, g1, acc);
+        run_stage<BITS, TAIL, GS128, DQ, false, true>(c, s + 1, a, bw, w1, w0, g1, g0, acc);
     } else {
-        run_stage<BITS, TAIL, GS128, FAST, false, false>(c, s, a, bw, w0, w1, g0, g1, acc);
+        run_stage<BITS, TAIL, GS128, DQ, false, false>(c, s, a, bw, w0, w1, g0, g1, acc);
     }
 }
 
-template <int BITS, bool TAIL, bool GS128>
+template <int BITS, bool TAIL, bool GS128, int DT>
 __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_f16_kernel(const GemmArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds_raw[];
@@ -560,7 +598,7 @@ gemm_f16_kernel(const GemmArgs A) {
         for (int kq = 0; kq < KSTEPS; ++kq)
             ci.aaddr[kq] = A_OFF + r32 * APR * 16 + 16 * ((8 * hk + KSTEPS * kh + kq) ^ swz(r32));
     }
-    const bool fast = scan_finish(A, n0 + slab * 32, lane, zs);
+    const bool fast = scan_finish<DT>(A, n0 + slab * 32, lane, zs);
 
     f16x acc[4];
 #pragma unroll
@@ -575,8 +613,9 @@ gemm_f16_kernel(const GemmArgs A) {
     for (int k = 0; k < 4; ++k) issue_slot<BITS, TAIL, true>(L, g0, k, lds);
 
     Ctx<BITS> c{A, lds, ci, magic_vreg(), L, sc, 0};
-    if (fast) compute_loop<BITS, TAIL, GS128, true>(c, nst, g0, acc);
-    else compute_loop<BITS, TAIL, GS128, false>(c, nst, g0, acc);
+    constexpr int DQ0 = DT == DT_BF16 ? 2 : 0;
+    if (fast) compute_loop<BITS, TAIL, GS128, DQ0 + 1>(c, nst, g0, acc);
+    else compute_loop<BITS, TAIL, GS128, DQ0>(c, nst, g0, acc);
     vmcnt<0>();                                   // the surplus loads land before the LDS is reused
 
     // the two k halves' partial sums meet in LDS (the stage slots are free once every
@@ -599,23 +638,29 @@ gemm_f16_kernel(const GemmArgs A) {
     // 4q + r holds row 8q + 4h + r, column j
     const int n = n0 + slab * 32 + r32;
     if (n >= A.N) return;
-    const float bias = A.b ? load_f<DT_F16>(A.b, n) : 0.f;
+    const float bias = A.b ? load_f<DT>(A.b, n) : 0.f;
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int m = m0 + 32 * a + 8 * (v >> 2) + 4 * hk + (v & 3);
-            if (m < A.M) store_f<DT_F16>(A.out, (long)m * A.N + n, apply_act(acc[a][v] + bias, A.act));
+            if (m < A.M) store_f<DT>(A.out, (long)m * A.N + n, apply_act(acc[a][v] + bias, A.act));
         }
     }
 }
 
-template <int BITS>
+template <int BITS, int DT>
 const void* kernel_for(bool tail, bool gs128) {
-    return tail ? (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, true>)
-                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, false>))
-                : (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, true>)
-                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, false>));
+    return tail ? (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, true, DT>)
+                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, false, DT>))
+                : (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, true, DT>)
+                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, false, DT>));
+}
+
+template <int DT>
+const void* kernel_for_bits(int bits, bool tail, bool gs128) {
+    return bits == 2 ? kernel_for<2, DT>(tail, gs128)
+                     : (bits == 3 ? kernel_for<3, DT>(tail, gs128) : kernel_for<4, DT>(tail, gs128));
 }
 
 }  // namespace
@@ -631,10 +676,10 @@ bool gemm_f16_supported(const GemmArgs& A) {
            (long)A.M * A.K * 2 < lim && (long)A.N * A.wpr * 4 < lim && (long)A.N * A.G * 2 < lim;
 }
 
-hipError_t launch_gemm_f16(const GemmArgs& A, hipStream_t stream) {
+hipError_t launch_gemm_f16(const GemmArgs& A, int dt, hipStream_t stream) {
     const bool tail = A.K % BK != 0, gs128 = A.gs == 128;
-    const void* f = A.bits == 2 ? kernel_for<2>(tail, gs128) : (A.bits == 3 ? kernel_for<3>(tail, gs128)
-                                                                         : kernel_for<4>(tail, gs128));
+    const void* f = dt == DT_BF16 ? kernel_for_bits<DT_BF16>(A.bits, tail, gs128)
+                                  : kernel_for_bits<DT_F16>(A.bits, tail, gs128);
     const int lds = A.bits == 2 ? LDS_BYTES<2> : (A.bits == 3 ? LDS_BYTES<3> : LDS_BYTES<4>);
     hipError_t e = lds_limit_raise(f, lds);
     if (e != hipSuccess) return e;

@@ -650,3 +650,41 @@ def test_bf16_fused_decode(hip, dist, M):
     u, U64, _, _ = make(11008, 4096, 3, torch.bfloat16, seed=5, scale=0.02)
     gv, uv = ref_linear(x, G64), ref_linear(x, U64)
     close_bf16(fused_gate_up(x, g, u), gv / (1 + np.exp(-gv)) * uv)
+
+
+# ------------------------------------------------------------------ bf16 prefill (MFMA pipeline)
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096)])
+@pytest.mark.parametrize("M", [1024, 2048])
+def test_bf16_baseline_prefill(hip, bits, K, N, M):
+    """configs[3] shapes with bf16 activations, scales and outputs: W-hat rounded to bf16
+    once from the fp32 product, as the reference does; float64 reference on 256 rows."""
+    w, _, _, d = make(N, K, bits, torch.bfloat16, scale=0.02)
+    x = randx(M, K, torch.bfloat16, seed=bits)
+    y = packed_linear(x, w)
+    rows = torch.from_numpy(_row_sample(M)).cuda()
+    close_bf16(y[rows], gemm_ref(x[rows], d, torch.bfloat16, bits, K, 128))
+    assert torch.isfinite(y).all()
+
+
+@pytest.mark.parametrize("gs", [32, 64, 256])
+def test_bf16_prefill_group_sizes(hip, gs):
+    w, _, b64, d = make(300, 640, 3, torch.bfloat16, bias=True, gs=gs)
+    x = randx(70, 640, torch.bfloat16)
+    close_bf16(packed_linear(x, w, act="silu"), gemm_ref(x, d, torch.bfloat16, 3, 640, gs, b64, "silu"))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("K,cols", [(400, 40), (1024, 300)])
+def test_bf16_prefill_fractional_zeros(hip, bits, K, cols):
+    """bf16 zero points that are not integers take the (q - z) * s form, the rest the fma
+    form, in one tile (and with K=400 the partial last stage)."""
+    _, _, _, d = make(300, K, bits, torch.bfloat16)
+    d = dict(d)
+    z = d["zeros"].clone()
+    z[:cols] = z[:cols] + 0.375
+    d["zeros"] = z
+    w = from_packed_dict(d, "cuda", torch.bfloat16)
+    x = randx(130, K, torch.bfloat16)
+    close_bf16(packed_linear(x, w), gemm_ref(x, d, torch.bfloat16, bits, K, 128))
