@@ -411,7 +411,7 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
     return sp;
 }
 
-// Batched streaming plan (gemv_stream.hip, bstream), batch 3..16: fp16 x with
+// Batched streaming plan (gemv_stream.hip, bstream), batch 3..16: fp16 or bf16 x with
 // 16-byte pieces, group sizes that are multiples of 128 (a unit of 128 codes is one
 // group), 32-bit offsets, and rows that keep every 16-row tile inside one projection
 // (fused QKV: Q and K widths multiples of 16; mixed widths: of the workgroup's rows).
@@ -426,9 +426,11 @@ struct BStreamPlan {
     int P = 1, ks = 1, rw = 1, bsu = 4, grid = 0, lds = 0;
 };
 
-int64_t bstream_lds(int64_t ks, int64_t M, int64_t rw, int bsu) {
+// LDS of a batched streaming workgroup: the staged activations, two per-unit sums (three
+// for bf16: its per-unit prescale) for 16 batch rows, and the row totals.
+int64_t bstream_lds(int64_t ks, int64_t M, int64_t rw, int bsu, bool bf) {
     const int64_t nu = ks * bsu;
-    return 64 * 4 * nu * M + 2 * 16 * nu * 4 + 4 * ks * M * 16 * rw;
+    return 64 * 4 * nu * M + (bf ? 3 : 2) * 16 * nu * 4 + 4 * ks * M * 16 * rw;
 }
 
 // Row groups: enough threads to stage the activations two items per thread (4 bsu M
@@ -441,12 +443,12 @@ int bstream_rw(int64_t M, int bsu, bool gateup) {
 }
 
 // K splits of the batched streaming kernel for slices of bsu units.
-int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu) {
+int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu, bool bf) {
     const int64_t U = ceil_div(C, 4);
     int64_t P = std::max<int64_t>(1, std::min<int64_t>(split_k, U));
     while (P < U) {
         const int64_t ks = ceil_div(ceil_div(U, P), bsu);
-        if (ks * rw <= 16 && bstream_lds(ks, M, rw, bsu) <= LDS_BUDGET) break;
+        if (ks * rw <= 16 && bstream_lds(ks, M, rw, bsu, bf) <= LDS_BUDGET) break;
         ++P;
     }
     return (int)P;
@@ -457,7 +459,7 @@ int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu) {
 // by at most two threads, an even number of row groups for gate-up, the LDS, one
 // projection per workgroup for mixed widths, 32-bit indices, and with P > 1 a counter
 // per row block in one window (the splits combine in the dispatch).
-BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu, int rw) {
+BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu, int rw, bool bf) {
     BStreamPlan bp;
     const int64_t U = ceil_div(A.C, 4);
     if (P < 1 || P > U || (int64_t)U * P >= (1ll << 32)) return bp;
@@ -467,7 +469,7 @@ BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu
     bp.rw = rw;
     bp.ks = (int)ceil_div(ceil_div(U, P), bsu);
     if (bp.ks * rw > 16) return bp;
-    bp.lds = (int)bstream_lds(bp.ks, A.M, rw, bsu);
+    bp.lds = (int)bstream_lds(bp.ks, A.M, rw, bsu, bf);
     if (bp.lds > LDS_BUDGET) return bp;
     const int rb = 16 * rw;
     if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return bp;
@@ -490,13 +492,14 @@ BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu
 constexpr int BSTREAM_CU_TARGET = 256;
 constexpr int BSTREAM_FILL_SPLITS = 4;
 
-BStreamPlan bstream_fill(const GemvArgs& A, int mode, bool mixed, int P0) {
+BStreamPlan bstream_fill(const GemvArgs& A, int mode, bool mixed, int P0, bool bf) {
     BStreamPlan best;
     int64_t best_key = INT64_MAX;
     for (int P = P0; P < P0 + BSTREAM_FILL_SPLITS; ++P) {
         for (int bsu : {4, 8}) {
+            if (bf && bsu == 8) continue;             // bf16 takes 4-unit slices (see plan_bstream)
             for (int rw = 1; rw <= 16; ++rw) {
-                const BStreamPlan c = bstream_make(A, mode, mixed, P, bsu, rw);
+                const BStreamPlan c = bstream_make(A, mode, mixed, P, bsu, rw, bf);
                 if (!c.ok) continue;
                 const int64_t dist = std::abs((int64_t)c.grid - BSTREAM_CU_TARGET);
                 const int64_t key = ((dist * 64 + (P - P0)) * 2 + (bsu == 8)) * 32 + rw;
@@ -512,14 +515,14 @@ BStreamPlan bstream_fill(const GemvArgs& A, int mode, bool mixed, int P0) {
 
 // The unsplit-first plan before any widening for the CU count: 4-unit slices with the
 // fewest splits that fit, or 8-unit slices where those need fewer splits.
-BStreamPlan bstream_base(int64_t M, int64_t C, int split_k, bool gateup) {
+BStreamPlan bstream_base(int64_t M, int64_t C, int split_k, bool gateup, bool bf) {
     BStreamPlan bp;
     bp.bsu = 4;
     bp.rw = bstream_rw(M, 4, gateup);
-    bp.P = bstream_splits(C, M, split_k, bp.rw, 4);
-    if (bp.P > std::max(split_k, 1)) {           // 4-unit slices would add a split: try 8
+    bp.P = bstream_splits(C, M, split_k, bp.rw, 4, bf);
+    if (bp.P > std::max(split_k, 1) && !bf) {    // 4-unit slices would add a split: try 8
         const int rw8 = bstream_rw(M, 8, gateup);
-        const int p8 = bstream_splits(C, M, split_k, rw8, 8);
+        const int p8 = bstream_splits(C, M, split_k, rw8, 8, bf);
         if (p8 < bp.P) {
             bp.bsu = 8;
             bp.rw = rw8;
@@ -537,7 +540,11 @@ bool bstream_fills(const BStreamPlan& base, int64_t V) {
 BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int cus) {
     BStreamPlan bp;
     const int64_t lim = INT32_MAX;
-    bool ok = A.M >= 3 && A.M <= 16 && dtype == CBK_F16 && A.gs % 128 == 0 && A.K % 8 == 0 &&
+    // bf16 keeps to 4-unit slices: with 8 its per-unit prescale pushes the 1024-thread
+    // kernel past 128 VGPRs and it spills (W3 11008 -> 4096 batch 8: 22.7 us on 8-unit
+    // slices, 19.9 on 4-unit ones, 13.9 for fp16).
+    const bool bf = dtype == CBK_BF16;
+    bool ok = A.M >= 3 && A.M <= 16 && (dtype == CBK_F16 || bf) && A.gs % 128 == 0 && A.K % 8 == 0 &&
               reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
     for (int i = 0; i < 3; ++i)
         ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
@@ -545,9 +552,9 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     if (!ok) return bp;
     const bool gateup = mode == CBK_MODE_GATEUP;
     const int64_t U = ceil_div(A.C, 4);
-    bp = bstream_base(A.M, A.C, split_k, gateup);
+    bp = bstream_base(A.M, A.C, split_k, gateup, bf);
     if (bstream_fills(bp, A.V)) {
-        BStreamPlan fill = bstream_fill(A, mode, mixed, std::max(split_k, 1));
+        BStreamPlan fill = bstream_fill(A, mode, mixed, std::max(split_k, 1), bf);
         if (fill.ok) {
             fill.filled = true;
             return fill;
@@ -558,23 +565,23 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     // blocks would give each CU 2.5 or more workgroups take 8-unit slices and the
     // fewest workgroups that still cover the CUs (W3 4096 -> 11008: batch 8 13.2 -> 11.1
     // us, batch 16 18.8 -> 14.5), and gate-up takes 8-unit slices (batch 4 20.4 -> 15.6).
-    if (bp.P == 1 && cus > 0) {
+    if (bp.P == 1 && cus > 0 && !bf) {
         const int64_t U8 = ceil_div(U, 8);
         if (mode == CBK_MODE_GEMV && !mixed && ceil_div(A.V, 16) >= (5 * (int64_t)cus) / 2) {
             int rw = (int)std::max<int64_t>(bstream_rw(A.M, 8, false), ceil_div(ceil_div(A.V, 16), cus));
-            if (U8 * rw <= 16 && bstream_lds(U8, A.M, rw, 8) <= LDS_BUDGET) {
+            if (U8 * rw <= 16 && bstream_lds(U8, A.M, rw, 8, bf) <= LDS_BUDGET) {
                 bp.bsu = 8;
                 bp.rw = rw;
             }
         } else if (gateup) {
             const int rw = bstream_rw(A.M, 8, true);
-            if (U8 * rw <= 16 && bstream_lds(U8, A.M, rw, 8) <= LDS_BUDGET) {
+            if (U8 * rw <= 16 && bstream_lds(U8, A.M, rw, 8, bf) <= LDS_BUDGET) {
                 bp.bsu = 8;
                 bp.rw = rw;
             }
         }
     }
-    return bstream_make(A, mode, mixed, bp.P, bp.bsu, bp.rw);
+    return bstream_make(A, mode, mixed, bp.P, bp.bsu, bp.rw, bf);
 }
 
 // Batched plan (gemv_batch.hip), batch 3..16 in one dispatch, taken where the bstream
@@ -706,7 +713,7 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divG = make_fastdiv((uint32_t)(A.gs / 128));
         L.family = CBK_KERNEL_BSTREAM;
-        L.f = gemv_bstream_kernel_for(mode, A.p[0].bits, mixed, bp.bsu);
+        L.f = gemv_bstream_kernel_for(mode, A.p[0].bits, mixed, bp.bsu, dtype == CBK_BF16);
         L.grid = bp.grid;
         L.block = 64 * bp.ks * bp.rw;
         L.lds = bp.lds;
@@ -925,9 +932,10 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
     if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M, dtype)));
     if (M >= 3 && M <= 16) {  // 4-unit slices split at least as often as 8-unit ones; gate-up rows
         const int64_t C = ceil_div(K, 32);
-        P = std::max(P, bstream_splits(C, M, split_k, bstream_rw(M, 4, true), 4));
+        const bool bf = dtype == CBK_BF16;
+        P = std::max(P, bstream_splits(C, M, split_k, bstream_rw(M, 4, true), 4, bf));
         for (bool gateup : {false, true})     // bstream_fill takes at most P0 + 3 splits
-            if (bstream_fills(bstream_base(M, C, split_k, gateup), V))
+            if (bstream_fills(bstream_base(M, C, split_k, gateup, bf), V))
                 P = std::max<int64_t>(P, std::min<int64_t>(ceil_div(C, 4), split_k + BSTREAM_FILL_SPLITS - 1));
     }
     return P > 1 ? (int64_t)P * M * V : 0;

@@ -133,14 +133,21 @@ __device__ __forceinline__ void convert_x(const uint32_t (&x)[16], u4 (&X)[4], f
 // below 2^-34 of it).  X and B are the fp16 operands as in convert_x; xs = sum x 2^-c
 // (fp32) and f = 2^c scales the chunk's terms back.  Infinities and NaNs stay what they
 // are; c >= -126 keeps f a normal float.
-template <int BITS>
-__device__ __forceinline__ void convert_x_bf16(const uint32_t (&x)[16], u4 (&X)[4], float& B, float& xs, float& f) {
+// The largest biased exponent of a bf16 chunk.
+__device__ __forceinline__ int chunk_exp_bf16(const uint32_t (&x)[16]) {
     typedef uint16_t us2 __attribute__((ext_vector_type(2)));
     us2 m = {0, 0};
 #pragma unroll
     for (int p = 0; p < 16; ++p) m = __builtin_elementwise_max(m, __builtin_bit_cast(us2, x[p] & 0x7F807F80u));
-    const int E = (int)(max(m.x, m.y) >> 7);                 // largest biased exponent of the chunk
-    const int c = max(E - (127 + 14), -126);
+    return (int)(max(m.x, m.y) >> 7);
+}
+
+// The prescale exponent c for a largest biased exponent E.
+__device__ __forceinline__ int prescale_bf16(int E) { return max(E - (127 + 14), -126); }
+
+// The chunk's operands at a given prescale exponent c.
+template <int BITS>
+__device__ __forceinline__ void convert_x_bf16_at(const uint32_t (&x)[16], int c, u4 (&X)[4], float& B, float& xs) {
     const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
     uint32_t o[16];
     float b = 0.f, t = 0.f;
@@ -160,6 +167,12 @@ __device__ __forceinline__ void convert_x_bf16(const uint32_t (&x)[16], u4 (&X)[
     for (int q = 0; q < 4; ++q) X[q] = u4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
     B = 1024.f * b;
     xs = __builtin_ldexpf(t, -c);
+}
+
+template <int BITS>
+__device__ __forceinline__ void convert_x_bf16(const uint32_t (&x)[16], u4 (&X)[4], float& B, float& xs, float& f) {
+    const int c = prescale_bf16(chunk_exp_bf16(x));
+    convert_x_bf16_at<BITS>(x, c, X, B, xs);
     f = __builtin_ldexpf(1.0f, c);
 }
 
@@ -398,7 +411,7 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
 // same 16 pair rows), so every wave's rows lie in one projection and its buffer
 // descriptors stay uniform.
 
-template <int BITS, int MODE, int BSU>
+template <int BITS, int MODE, int BSU, int DT>
 __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -477,18 +490,30 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     }
 
     // 2. activations -> LDS: piece m of chunk c of batch row i at ((m NCH + c) M + i) * 16;
-    // per unit and batch row its sums X (at XSu[u * 16 + i]) and XB (XBu[u * 16 + i])
+    // per unit and batch row its sums X (at XSu[u * 16 + i]) and XB (XBu[u * 16 + i]), and
+    // for bf16 the unit's prescale 2^c (XFu[u * 16 + i]; the four chunks of a unit share
+    // c, from their largest exponent, since the MFMA sums over the unit)
     u4* Xl = reinterpret_cast<u4*>(lds);
     float* XSu = reinterpret_cast<float*>(lds + 64 * NCH * M);
     float* XBu = XSu + 16 * NU;
-    float* red = XBu + 16 * NU;
+    float* XFu = XBu + 16 * NU;
+    float* red = XBu + (DT == DT_BF16 ? 32 : 16) * NU;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int t = tid + e * nthr, i = t / NCH, c = t - i * NCH;
         if (t >= NCH * M) break;                  // whole quads of threads leave together (NCH % 4 == 0)
         u4 X[4];
         float B, xs;
-        convert_x<BITS>(xa[e], X, B, xs);
+        int cu = 0;
+        if constexpr (DT == DT_BF16) {
+            int E = chunk_exp_bf16(xa[e]);
+            E = max(E, __shfl_xor(E, 1, 64));
+            E = max(E, __shfl_xor(E, 2, 64));
+            cu = prescale_bf16(E);
+            convert_x_bf16_at<BITS>(xa[e], cu, X, B, xs);
+        } else {
+            convert_x<BITS>(xa[e], X, B, xs);
+        }
 #pragma unroll
         for (int m = 0; m < 4; ++m) Xl[(m * NCH + c) * M + i] = X[m];
         // the 4 chunks of a unit are 4 consecutive threads (NCH % 4 == 0)
@@ -499,6 +524,7 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
         if ((c & 3) == 0) {
             XSu[(c >> 2) * 16 + i] = xs;
             XBu[(c >> 2) * 16 + i] = B;
+            if constexpr (DT == DT_BF16) XFu[(c >> 2) * 16 + i] = __builtin_ldexpf(1.0f, cu);
         }
     }
     barrier_lds();
@@ -528,10 +554,16 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
         // unit u's scale and zero sit in lane (j, u % 4), set u / 4
         const uint32_t su = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (j + 16 * (u & 3)), (int)s_own[u >> 2]);
         const uint32_t zu = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (j + 16 * (u & 3)), (int)z_own[u >> 2]);
-        const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)su);
-        const float ze = (float)__builtin_bit_cast(_Float16, (uint16_t)zu);
+        const float sc = meta_f<DT>(su);
+        const float ze = meta_f<DT>(zu);
+        if constexpr (DT == DT_BF16) {
+            const f4 F4 = *reinterpret_cast<const f4*>(XFu + uj * 16 + 4 * kq);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] = fmaf(sc, fmaf(-ze, X4[q], d[q] - XB4[q]), acc[q]);
+            for (int q = 0; q < 4; ++q) acc[q] = fmaf(sc, fmaf(-ze, X4[q], d[q] - XB4[q]) * F4[q], acc[q]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] = fmaf(sc, fmaf(-ze, X4[q], d[q] - XB4[q]), acc[q]);
+        }
     }
 
     // 4. row totals per slice: lane (j, kq) holds batch rows 4 kq + q of row j
@@ -552,27 +584,27 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
                 mine += red[(k * M + b) * RB + ro];
                 partner += red[(k * M + b) * RB + (ro ^ 1)];
             }
-            if (A.P == 1) epilogue<DT_F16, MODE>(A, b, v, mine, partner);
+            if (A.P == 1) epilogue<DT, MODE>(A, b, v, mine, partner);
             else partial_put(A.partial + ((long)p * A.M + b) * A.V + v, mine);
         }
     }
     // 6. with P > 1 and arrival counters, the last split of the block combines
     if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
-        split_epilogue<DT_F16, MODE>(A, vbase, RB, nthr);
+        split_epilogue<DT, MODE>(A, vbase, RB, nthr);
 }
 
-template <int MODE, int BITS, int BSU>
+template <int MODE, int BITS, int BSU, int DT>
 __global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
-        bstream_body<BITS, MODE, BSU>(A, lds);
+        bstream_body<BITS, MODE, BSU, DT>(A, lds);
     } else {
         int proj, r;
         vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * 16 * A.st_rw, proj, r);
         const int bits = CBK_SEL(A, proj, bits);
-        if (bits == 2) bstream_body<2, MODE, BSU>(A, lds);
-        else if (bits == 3) bstream_body<3, MODE, BSU>(A, lds);
-        else bstream_body<4, MODE, BSU>(A, lds);
+        if (bits == 2) bstream_body<2, MODE, BSU, DT>(A, lds);
+        else if (bits == 3) bstream_body<3, MODE, BSU, DT>(A, lds);
+        else bstream_body<4, MODE, BSU, DT>(A, lds);
     }
 }
 
@@ -610,13 +642,13 @@ const void* stream_kernel(int mode, int bits, bool mixed) {
 #undef CBK_STREAM_K
 }
 
-template <int BSU>
+template <int BSU, int DT>
 const void* bstream_kernel(int mode, int bits, bool mixed) {
-    if (mixed) return reinterpret_cast<const void*>(&gemv_bstream_kernel<MODE_QKV, 0, BSU>);
+    if (mixed) return reinterpret_cast<const void*>(&gemv_bstream_kernel<MODE_QKV, 0, BSU, DT>);
 #define CBK_BSTREAM_K(M)                                                                           \
-    (bits == 2 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 2, BSU>)                    \
-               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 3, BSU>)       \
-                            : reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 4, BSU>)))
+    (bits == 2 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 2, BSU, DT>)                \
+               : (bits == 3 ? reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 3, BSU, DT>)   \
+                            : reinterpret_cast<const void*>(&gemv_bstream_kernel<M, 4, BSU, DT>)))
     if (mode == MODE_QKV) return CBK_BSTREAM_K(MODE_QKV);
     if (mode == MODE_GATEUP) return CBK_BSTREAM_K(MODE_GATEUP);
     return CBK_BSTREAM_K(MODE_GEMV);
@@ -642,8 +674,9 @@ const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int r
                 : stream_kernel_dt<DT_F16>(mode, bits, mixed, mb, rpw);
 }
 
-const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu) {
-    return bsu == 8 ? bstream_kernel<8>(mode, bits, mixed) : bstream_kernel<4>(mode, bits, mixed);
+const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu, bool bf16) {
+    if (bf16) return bsu == 8 ? bstream_kernel<8, DT_BF16>(mode, bits, mixed) : bstream_kernel<4, DT_BF16>(mode, bits, mixed);
+    return bsu == 8 ? bstream_kernel<8, DT_F16>(mode, bits, mixed) : bstream_kernel<4, DT_F16>(mode, bits, mixed);
 }
 
 

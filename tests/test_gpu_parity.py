@@ -688,3 +688,44 @@ def test_bf16_prefill_fractional_zeros(hip, bits, K, cols):
     w = from_packed_dict(d, "cuda", torch.bfloat16)
     x = randx(130, K, torch.bfloat16)
     close_bf16(packed_linear(x, w), gemm_ref(x, d, torch.bfloat16, bits, K, 128))
+
+
+# ------------------------------------------------------------------ bf16 batched decode
+
+@pytest.mark.parametrize("M", [3, 8, 16])
+@pytest.mark.parametrize("kind,out", [("gemv", 4096), ("gemv", 11008), ("gate_up", 11008),
+                                      ("qkv", (4096, 1024, 1024))])
+@pytest.mark.parametrize("K", [4096, 11008])
+def test_bf16_batched_decode_is_one_launch(hip, M, kind, out, K):
+    fam, splits, grid, threads, lds, launches = _C.decode_plan(torch.bfloat16, M, K, 128, out, 3, kind, 1, 1)
+    assert (fam, launches) == ("bstream", 1), (fam, splits, launches)
+
+
+@pytest.mark.parametrize("dist", ["normal", "outlier", "wide", "tiny"])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096)])
+@pytest.mark.parametrize("M", [3, 8, 16])
+def test_bf16_batched_gemv(hip, dist, bits, K, N, M):
+    """Batch 3..16 bf16 decode (K splits combined in the dispatch where planned): each
+    128-code unit and batch row shares one power-of-two prescale, since the MFMA sums over
+    the unit."""
+    w, W64, _, _ = make(N, K, bits, torch.bfloat16, scale=0.02)
+    x = randx_bf16(M, K, dist, seed=M * bits)
+    y = packed_linear(x, w)
+    close_bf16(y, ref_linear(x, W64))
+    assert torch.equal(packed_linear(x, w), y)
+
+
+@pytest.mark.parametrize("M", [4, 12])
+def test_bf16_batched_fused(hip, M):
+    bits = tuple(int(b) for b in np.random.default_rng(M).choice([2, 3, 4], 3))
+    q, Q64, _, _ = make(4096, 4096, bits[0], torch.bfloat16, seed=1, scale=0.02)
+    k, K64, _, _ = make(1024, 4096, bits[1], torch.bfloat16, seed=2, scale=0.02)
+    v, V64, _, _ = make(1024, 4096, bits[2], torch.bfloat16, seed=3, scale=0.02)
+    x = randx_bf16(M, 4096, "outlier", seed=M)
+    for o, W in zip(fused_qkv(x, q, k, v), (Q64, K64, V64)):
+        close_bf16(o, ref_linear(x, W))
+    g, G64, _, _ = make(11008, 4096, 3, torch.bfloat16, seed=4, scale=0.02)
+    u, U64, _, _ = make(11008, 4096, 3, torch.bfloat16, seed=5, scale=0.02)
+    gv, uv = ref_linear(x, G64), ref_linear(x, U64)
+    close_bf16(fused_gate_up(x, g, u), gv / (1 + np.exp(-gv)) * uv)
