@@ -188,7 +188,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--sweeps", default="gemv,fused,gemm,stack,model,producer",
                     help="comma-separated extra sweeps after the timed step (ignored with --quick); "
-                         "also 'batched': batched decode at the library's own plans")
+                         "also 'batched': batched decode at the library's own plans; 'dtypes': fp16 against "
+                         "bf16 activations")
     ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm"),
                     help="run the fixed launch sequence of a counter pass and exit: gemv (default: the "
                          "W3 decode GEMV after a calibration copy) or gemm (the M=1024 W4 prefill GEMM)")
@@ -296,6 +297,8 @@ def main():
             out["gemv_sweep"] = gemv_sweep(torch, C, ops, dev)
         if "batched" in todo:
             out["batched"] = batched_sweep(torch, C, ops, dev)
+        if "dtypes" in todo:
+            out["dtypes"] = dtype_sweep(torch, C, ops, dev)
         if "fused" in todo:
             out["fused"] = fused_sweep(torch, C, ops, dev)
         if "gemm" in todo:
@@ -482,6 +485,36 @@ def batched_sweep(torch, C, ops, dev):
                 log(f"batched W{bits} M={M} K={K} N={N}: {us:.2f} us ({fam}, P={splits}, {grid} workgroups)")
             del ws, base
             torch.cuda.empty_cache()
+    return rows
+
+
+def dtype_sweep(torch, C, ops, dev):
+    """fp16 against bf16 activations (scales, zeros and outputs of the same dtype, the same codes):
+    W3 decode at M = 1 and 8 over the three shapes, graph-replayed over >= 1 GiB of weight copies,
+    and the W3 prefill GEMM at M = 1024, with the kernel family each decode plan takes."""
+    from dataclasses import replace
+    rows = []
+    for K, N in SHAPES:
+        base = make_weight(torch, N, K, 3, 0, dev)
+        n = copies_for(weight_bytes(base))
+        for M in (1, 8, 1024):
+            r = {"bits": 3, "M": M, "K": K, "N": N}
+            for dt, tag in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+                k = n if M <= 16 else 4
+                ws = [replace(clone_weight(base), scales=base.scales.to(dt), zeros=base.zeros.to(dt)) for _ in range(k)]
+                x = randx(torch, M, K, 1, dev).to(dt)
+                us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w) for w in ws], len(ws), replays=4)
+                r[tag + "_us"] = round(us, 3)
+                if M <= 16:
+                    r[tag + "_kernel"] = C.decode_plan(dt, M, K, GS, N, 3, "gemv", 1, 1)[0]
+                    r[tag + "_GBps"] = round(gemv_bytes(M, K, N, 3) / (us * 1e-6) / 1e9, 1)
+                else:
+                    r[tag + "_TFLOPs"] = round(2 * M * N * K / (us * 1e-6) / 1e12, 1)
+                del ws
+                torch.cuda.empty_cache()
+            log(f"dtypes W3 M={M} K={K} N={N}: fp16 {r['fp16_us']:.2f} us, bf16 {r['bf16_us']:.2f} us")
+            rows.append(r)
+        del base
     return rows
 
 
