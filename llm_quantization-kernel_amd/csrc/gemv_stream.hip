@@ -131,7 +131,7 @@ __device__ __forceinline__ void convert_x(const uint32_t (&x)[16], u4 (&X)[4], f
 // fp16's range, and every element at least 2^-23 of the largest is a normal fp16 number
 // after the scaling, where its 8 significant bits are exact (smaller ones lose bits only
 // below 2^-34 of it).  X and B are the fp16 operands as in convert_x; xs = sum x 2^-c
-// (fp32) and f = 2^c scales the chunk's terms back.  Infinities and NaNs stay what they
+// (fp32, formed from the operands) and f = 2^c scales the chunk's terms back.  Infinities and NaNs stay what they
 // are; c >= -126 keeps f a normal float.
 // The largest biased exponent of a bf16 chunk.
 __device__ __forceinline__ int chunk_exp_bf16(const uint32_t (&x)[16]) {
@@ -161,12 +161,14 @@ __device__ __forceinline__ void convert_x_bf16_at(const uint32_t (&x)[16], int c
         const h2 v = {(_Float16)__builtin_ldexpf(xa, -c - ea), (_Float16)__builtin_ldexpf(xb, -c - eb)};
         o[p] = __builtin_bit_cast(uint32_t, v);
         b = __builtin_amdgcn_fdot2(v, one, b, false);
-        t += __uint_as_float(x[p] << 16) + __uint_as_float(x[p] & 0xFFFF0000u);
+        // sum x 2^-c from the operands: v 2^e (exact powers of two in fp16, exact products)
+        const h2 up = {(_Float16)(float)(1 << ea), (_Float16)(float)(1 << eb)};
+        t = __builtin_amdgcn_fdot2(v, up, t, false);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) X[q] = u4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
     B = 1024.f * b;
-    xs = __builtin_ldexpf(t, -c);
+    xs = t;
 }
 
 template <int BITS>
