@@ -23,7 +23,7 @@ LIB_NAME = "libcrispybits_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = os.environ.get("CRISPYBITS_ARCH", "gfx950")
 
-SOURCES = ["abi.cpp", "gemv_mfma.hip", "gemv_stream.hip", "gemv_batch.hip", "gemv_generic.hip", "gemm.hip", "gemm_f16.hip",
+SOURCES = ["abi.cpp", "gemv_stream.hip", "gemv_any.hip", "gemm.hip", "gemm_f16.hip", "gemm_f32.hip",
            "unpack.hip", "quant.hip"]
 
 # -packed-fp32-ops is disabled: the kernels never rely on v_pk_*_f32.
@@ -32,10 +32,8 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-munsafe-f
              "-Wno-unused-result", "-I" + CSRC, "-I" + os.path.join(os.path.dirname(ROOT), "include")]
 
 
-# Per-file additions.  gemv_batch.hip: no SLP vectorisation, which would pack each
-# prefetched (scale, zero) pair into one register and so wait for both loads where the
-# pair is formed, long before the values are used.
-FILE_FLAGS = {"gemv_batch.hip": ["-fno-slp-vectorize"]}
+# Per-file compiler flags beside HIP_FLAGS (none at present).
+FILE_FLAGS: dict = {}
 
 
 def _hipcc() -> str:

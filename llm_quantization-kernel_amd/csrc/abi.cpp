@@ -125,15 +125,20 @@ hipError_t scratch_for(int device, float** out) {
 }
 
 // Arrival counters of the in-dispatch split-K combine (split_arrive, cbk_device.hpp):
-// one word per row block of a call, zero between calls (the combining workgroup
-// resets its word).  A file-scope device array, one copy per GPU, cut into windows;
-// each stream that makes split calls on a device holds a window of its own, so calls
-// in flight on different streams never share a counter.  Calls on one stream run in
-// order, so one window serves all of them.  Windows go to streams in first-use order
-// and, once all are taken, to the stream that used its window least recently; a call
-// whose row blocks outnumber a window's counters takes the reduce launch instead.
-constexpr int SPLIT_WINDOWS = 32;
-constexpr int SPLIT_COUNTERS = 8192;
+// one word per row block of a call, zero between calls (the combining workgroup resets
+// its word).  A file-scope device array, one copy per GPU, cut into windows.  A window
+// has one holder for good:
+//  * a stream, for its eager calls -- calls on one stream run in order, so one window
+//    serves all of them;
+//  * a graph capture -- the captured launches keep the window's address and may be
+//    replayed at any time on any stream, so the window is never handed to eager calls
+//    or to another capture.
+// A window is never taken from its holder (a stream may still have split calls in
+// flight).  A call that finds no window of its own and no free one, or whose row blocks
+// outnumber a window's counters, takes the combine launch instead: correct, one launch
+// more.  One graph must not be replayed while another replay of it runs.
+constexpr int SPLIT_WINDOWS = 256;
+constexpr int SPLIT_COUNTERS = 4096;
 static __device__ __align__(256) uint32_t split_counters[SPLIT_WINDOWS * SPLIT_COUNTERS];
 
 struct SplitWindows {
@@ -141,47 +146,46 @@ struct SplitWindows {
     uint32_t* base = nullptr;
     hipError_t err = hipSuccess;
     bool init = false;
-    hipStream_t owner[SPLIT_WINDOWS];
-    uint64_t used[SPLIT_WINDOWS];
-    uint64_t tick = 0;
+    int used = 0;                                   // windows [0, used) have holders
+    bool by_capture[SPLIT_WINDOWS];
+    hipStream_t stream[SPLIT_WINDOWS];              // holder stream (eager windows)
+    unsigned long long capture[SPLIT_WINDOWS];      // holder capture id (capture windows)
 };
 SplitWindows g_split[MAX_DEVICES];
 
-// This stream's counter window on `device` (made current by the caller), or nullptr.
+// The counter window of this call on `device` (made current by the caller), or nullptr.
 uint32_t* split_window(int device, hipStream_t stream) {
     if (device < 0 || device >= MAX_DEVICES) return nullptr;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    if (hipStreamGetCaptureInfo(stream, &st, &id) != hipSuccess) return nullptr;
+    const bool cap = st == hipStreamCaptureStatusActive;
     SplitWindows& W = g_split[device];
     std::lock_guard<std::mutex> lk(W.mu);
     if (!W.init) {
         void* p = nullptr;
         W.err = hipGetSymbolAddress(&p, HIP_SYMBOL(split_counters));
         W.base = W.err == hipSuccess ? static_cast<uint32_t*>(p) : nullptr;
-        for (int i = 0; i < SPLIT_WINDOWS; ++i) {
-            W.owner[i] = nullptr;
-            W.used[i] = 0;
-        }
         W.init = true;
     }
     if (!W.base) return nullptr;
-    int slot = -1, lru = 0;
-    for (int i = 0; i < SPLIT_WINDOWS && slot < 0; ++i)
-        if (W.used[i] && W.owner[i] == stream) slot = i;
+    int slot = -1;
+    for (int i = 0; i < W.used && slot < 0; ++i)
+        if (W.by_capture[i] == cap && (cap ? W.capture[i] == id : W.stream[i] == stream)) slot = i;
     if (slot < 0) {
-        for (int i = 1; i < SPLIT_WINDOWS; ++i)
-            if (W.used[i] < W.used[lru]) lru = i;
-        slot = lru;
-        W.owner[slot] = stream;
+        if (W.used == SPLIT_WINDOWS) return nullptr;
+        slot = W.used++;
+        W.by_capture[slot] = cap;
+        W.stream[slot] = cap ? nullptr : stream;
+        W.capture[slot] = cap ? id : 0;
     }
-    W.used[slot] = ++W.tick;
     return W.base + (size_t)slot * SPLIT_COUNTERS;
 }
 
-constexpr int MFMA_TILE = 16;          // virtual rows per MFMA decode job
+constexpr int MFMA_TILE = 16;          // virtual rows per decode job tile (the policy's tile_n)
 constexpr int LDS_BUDGET = 160 * 1024; // dynamic LDS per decode workgroup (gfx950: 160 KB per CU)
-constexpr int WAVES_PER_CU = 8;        // decode occupancy target
-constexpr int MFMA_STAGE_UNITS = Ring<4>::S;   // units per weight-ring stage (gemv_mfma.hip)
-constexpr int MFMA_MAX_WAVES = 8;      // waves per decode workgroup, batch rows (launch bound 512 threads)
-constexpr int MFMA_MAX_WAVES_B1 = 16;  // ... at batch 1 (launch bound 1024 threads)
+constexpr int ANY_FILL_WAVES = 4096;   // waves the fp32 matrix-core decode aims for
+constexpr int ANY_MIN_CHUNKS = 4;      // ... keeping at least this many chunks per wave
 
 bool valid_dtype(int dt) { return dt == CBK_F16 || dt == CBK_BF16 || dt == CBK_F32; }
 
@@ -209,139 +213,29 @@ int check_x(const void* x, int dtype, int64_t M, int64_t K) {
 }
 
 // ----------------------------------------------------------------------------- decode plan
-struct LdsLayout {
-    int xs_bytes = 0, meta_off = 0, ring_off = 0, wave_bytes = 0, red_off = 0, total = 0;
-    int sum_off = 0, tab_off = 0, raw_off = 0, raw_np = 0;
+// Plan of the fp32 matrix-core decode (gemv_any.hip): jobs of 16 virtual rows x 16 batch
+// rows x one K split (the requested one), one workgroup each.  The CUs are filled with
+// waves rather than extra splits -- a split needs a partial buffer the caller sized for
+// its own split_k: a job's workgroup takes enough waves (1..16) that the launch holds
+// about ANY_FILL_WAVES waves (four per SIMD of the 256-CU parts), while every wave keeps
+// at least ANY_MIN_CHUNKS chunks of its split.  rho is not used: the kernel is not
+// persistent.
+struct AnyPlan {
+    int P = 1, ntiles = 0, mtiles = 0, waves = 1;
+    int64_t jobs = 0;
 };
 
-struct Plan {
-    bool mfma = false;
-    bool unit_rows = false;            // batch-1 MFMA layout (units as MFMA rows, shared staging)
-    int P = 1, ntiles = 0, mtiles = 0, jobs = 0, grid = 0;
-    int nw = 1, units = 0, lds = 0;
-    int ring = 1;
-    LdsLayout L;
-};
-
-// Ring stages of the busiest wave of a job (batch rows).
-int64_t mfma_wave_stages(int64_t units, int P, int nw) {
-    return ceil_div(ceil_div(ceil_div(units, P), nw), MFMA_STAGE_UNITS);
-}
-
-// LDS of one MFMA decode workgroup (gemv_mfma.hip).
-// Batch 1 (unit_rows), for the stg stages of the largest K split: shared
-// activation operands of ceil(4 stg / 16) groups of 16 units (4 KB each), their
-// unit sums, the masked scale table (1 KB per stage), the raw (scale, zero) row
-// spans (32 spans of np 16-byte pieces, in whole 1 KB DMA instructions), 16 row
-// sums per wave, then the packed tile: 16 rows of nb 1 KB blocks at pitch
-// RP = 1024 nb + 16 (returned as wave_bytes).
-// Batch rows: NW private regions (operands per batch row, [unit][2][16] float
-// sums, packed (scale, zero) halves [row][unit], the ring) and the cross-wave
-// reduction area.
-LdsLayout mfma_lds(int64_t units, int P, int mt, int nw, int bits, int gs, int ring, bool unit_rows) {
-    LdsLayout L;
-    const int64_t nu = ceil_div(units, P);
-    const int64_t slot = ring_slot_bytes(bits);
-    if (unit_rows) {
-        const int64_t stg = ceil_div(nu, MFMA_STAGE_UNITS);
-        const int64_t ngrp = ceil_div(MFMA_STAGE_UNITS * stg, 16);
-        const int64_t groups = ceil_div(nu, std::max(gs / 128, 1)) + 1;   // groups a split touches, at most
-        const int64_t np = ceil_div(2 * groups + 14, 16);                  // 16-byte pieces per row span
-        const int64_t sum_off = ngrp * 4096;
-        const int64_t tab_off = sum_off + ngrp * 16 * 8;
-        const int64_t raw_off = tab_off + stg * 1024;
-        const int64_t red_off = raw_off + ceil_div(32 * np, 64) * 1024;
-        const int64_t ring_off = red_off + MFMA_MAX_WAVES_B1 * 16 * 4;
-        const int64_t rp = ceil_div(nu * 16 * bits, 1024) * 1024 + 16;
-        const int64_t total = ring_off + 16 * rp;
-        L.sum_off = (int)sum_off;
-        L.tab_off = (int)tab_off;
-        L.raw_off = (int)raw_off;
-        L.red_off = (int)red_off;
-        L.ring_off = (int)ring_off;
-        L.raw_np = (int)np;
-        L.wave_bytes = (int)std::min<int64_t>(rp, INT32_MAX);
-        L.total = (int)std::min<int64_t>(total, INT32_MAX);
-        return L;
-    }
-    const int64_t nuw = ceil_div(nu, nw);                       // units of the busiest wave
-    const int64_t xs = nuw * 256 * mt;
-    const int64_t meta_off = xs + nuw * 32 * 4;
-    const int64_t ring_off = (meta_off + 16 * nuw * 4 + 15) / 16 * 16;
-    const int64_t wave_bytes = ring_off + (int64_t)ring * slot;
-    L.xs_bytes = (int)xs;
-    L.meta_off = (int)meta_off;
-    L.ring_off = (int)ring_off;
-    L.wave_bytes = (int)wave_bytes;
-    L.red_off = (int)(nw * wave_bytes);
-    L.total = (int)std::min<int64_t>(nw * wave_bytes + (int64_t)std::max(nw - 1, 1) * 1024, INT32_MAX);
-    return L;
-}
-
-// Decode launch plan.  MFMA path: jobs of 16 rows x one K split, NW waves per job
-// (about two stages of units each, raised towards WAVES_PER_CU per CU).  Batch 1
-// holds the split's whole tile in LDS, so K is split further when it does not
-// fit.  Batch rows use a per-wave ring deep enough to request every stage of a
-// wave at once; when the LDS is short the ring shrinks to 2 slots, then the
-// workgroup loses waves, then the ring drops to 1 slot, and only then K is split
-// further.
-Plan plan_gemv(int dtype, int64_t M, int64_t V, int64_t K, int gs, int bits, int split_k, int rho, int cus,
-               bool mfma_ok, bool xvec) {
-    Plan pl;
+AnyPlan plan_any(int64_t M, int64_t V, int64_t K, int split_k) {
+    AnyPlan pl;
     const int64_t C = ceil_div(K, 32);
-    // MFMA path: fp16, whole 128-code units per group, rows a multiple of 16 bytes
-    pl.mfma = mfma_ok && dtype == CBK_F16 && gs % 128 == 0 && (C * bits) % 4 == 0;
-    const int64_t sm = std::max(cus, 1);
-    if (pl.mfma) {
-        pl.units = (int)ceil_div(C, 4);
-        const int mt = (int)std::min<int64_t>(16, std::max<int64_t>(M, 1));
-        // batch 1 with 16-byte x pieces: activations and scales staged by LDS-DMA
-        pl.unit_rows = M <= 1 && xvec;
-        pl.ntiles = (int)ceil_div(V, MFMA_TILE);
-        pl.mtiles = (int)ceil_div(std::max<int64_t>(M, 1), 16);
-        const int S = MFMA_STAGE_UNITS;
-        const int RMAX = Ring<4>::RMAX;
-        for (pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, pl.units));; ++pl.P) {
-            const int64_t jobs = (int64_t)pl.mtiles * pl.ntiles * pl.P;
-            pl.jobs = (int)jobs;
-            // batch 1 runs one workgroup per job whatever rho asks: its workgroup does
-            // not overlap consecutive jobs, so persistence only serialises them
-            pl.grid = (int)(rho > 0 && !pl.unit_rows ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm))
-                                                     : jobs);
-            const int64_t units_job = std::max<int64_t>(ceil_div(pl.units, pl.P), 1);
-            int64_t nw = ceil_div(units_job, 2 * S);
-            if ((int64_t)pl.grid * nw < (int64_t)WAVES_PER_CU * sm)
-                nw = std::min<int64_t>(ceil_div((int64_t)WAVES_PER_CU * sm, pl.grid), ceil_div(units_job, S));
-            nw = std::max<int64_t>(1, std::min<int64_t>(nw, pl.unit_rows ? MFMA_MAX_WAVES_B1 : MFMA_MAX_WAVES));
-            auto fits = [&](int w, int r) {
-                return mfma_lds(pl.units, pl.P, mt, w, bits, gs, r, pl.unit_rows).total <= LDS_BUDGET;
-            };
-            auto stages = [&](int w) { return mfma_wave_stages(pl.units, pl.P, w); };
-            int w = (int)nw;
-            int r = (int)std::min<int64_t>(stages(w), RMAX);
-            while (r > 2 && !fits(w, r)) --r;
-            while (w > 1 && !fits(w, r)) {
-                --w;
-                r = (int)std::min<int64_t>({stages(w), RMAX, (int64_t)std::max(r, 2)});
-                while (r > 2 && !fits(w, r)) --r;
-            }
-            if (!fits(w, r)) r = 1;
-            if (fits(w, r) || pl.P >= pl.units) {
-                pl.L = mfma_lds(pl.units, pl.P, mt, w, bits, gs, r, pl.unit_rows);
-                pl.nw = w;
-                pl.ring = r;
-                pl.lds = pl.L.total;
-                break;
-            }
-        }
-    } else {
-        pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, C));
-        pl.ntiles = (int)ceil_div(V, GENERIC_ROWS);
-        pl.mtiles = (int)std::max<int64_t>(M, 1);
-        const int64_t jobs = (int64_t)pl.mtiles * pl.ntiles * pl.P;
-        pl.jobs = (int)jobs;
-        pl.grid = (int)(rho > 0 ? std::max<int64_t>(1, std::min<int64_t>(jobs, (int64_t)rho * sm)) : jobs);
-    }
+    pl.ntiles = (int)ceil_div(V, 16);
+    pl.mtiles = (int)ceil_div(std::max<int64_t>(M, 1), 16);
+    pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(split_k, C));
+    pl.jobs = (int64_t)pl.ntiles * pl.mtiles * pl.P;
+    const int64_t chunks = ceil_div(C, pl.P);
+    int64_t w = ceil_div(ANY_FILL_WAVES, pl.jobs);
+    w = std::min<int64_t>(w, std::max<int64_t>(1, chunks / ANY_MIN_CHUNKS));
+    pl.waves = (int)std::max<int64_t>(1, std::min<int64_t>(w, ANY_MAX_THREADS / 64));
     return pl;
 }
 
@@ -386,7 +280,7 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
     bool ok = A.M >= 1 && A.M <= 2 && (dtype == CBK_F16 || dtype == CBK_BF16) && A.gs % 32 == 0 && A.K % 8 == 0 &&
               reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
     for (int i = 0; i < 3; ++i)
-        ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
+        ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * 2 < lim;
     if (!ok) return sp;
     sp.mb = A.M;
     const int max_waves = 16;                           // the kernel's launch bound: 1024 threads
@@ -402,7 +296,7 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
         sp.rw = std::max(STREAM_CPL, sp.rw / 2);
     }
     const int rb = sp.rpw * sp.rw;
-    if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return sp;
+    if (mixed && (A.src[0].n % rb != 0 || A.src[1].n % rb != 0)) return sp;
     const int64_t grid = ceil_div(A.V, rb) * sp.P;
     if (grid >= lim) return sp;
     sp.grid = (int)grid;
@@ -472,7 +366,7 @@ BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu
     bp.lds = (int)bstream_lds(bp.ks, A.M, rw, bsu, bf);
     if (bp.lds > LDS_BUDGET) return bp;
     const int rb = 16 * rw;
-    if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) return bp;
+    if (mixed && (A.src[0].n % rb != 0 || A.src[1].n % rb != 0)) return bp;
     const int64_t blocks = ceil_div(A.V, rb);
     if (P > 1 && blocks > SPLIT_COUNTERS) return bp;
     if (blocks * P >= INT32_MAX) return bp;
@@ -547,8 +441,8 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     bool ok = A.M >= 3 && A.M <= 16 && (dtype == CBK_F16 || bf) && A.gs % 128 == 0 && A.K % 8 == 0 &&
               reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
     for (int i = 0; i < 3; ++i)
-        ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
-    if (mode == CBK_MODE_QKV) ok = ok && A.p[0].n % 16 == 0 && A.p[1].n % 16 == 0;
+        ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * 2 < lim;
+    if (mode == CBK_MODE_QKV) ok = ok && A.src[0].n % 16 == 0 && A.src[1].n % 16 == 0;
     if (!ok) return bp;
     const bool gateup = mode == CBK_MODE_GATEUP;
     const int64_t U = ceil_div(A.C, 4);
@@ -584,53 +478,6 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     return bstream_make(A, mode, mixed, bp.P, bp.bsu, bp.rw, bf);
 }
 
-// Batched plan (gemv_batch.hip), batch 3..16 in one dispatch, taken where the bstream
-// kernel would split K and bstream_fill finds no plan (its partials would then need a
-// reduce launch): the bstream kernel's
-// conditions (fp16 x with 16-byte pieces, group sizes that are multiples of 128,
-// 32-bit offsets, every 16-row block inside one projection; mixed widths: every
-// workgroup's rows).  A workgroup of 15 or 16 waves fills a CU (128 VGPRs per wave), so
-// rw (row blocks per workgroup: 1, 2 or 3) takes the fewest workgroup rounds over the
-// CUs and among equal rounds the smallest rw: every workgroup stages all of K's
-// activations, so fewer, wider workgroups only pay when they save a round.  Gate-up
-// needs an even rw (one gate and one up block per 16 pair rows).  split_k is ignored:
-// the kernel never splits K.
-struct BatchPlan {
-    bool ok = false;
-    int rw = 1, grid = 0, lds = 0;
-};
-
-BatchPlan plan_batch(const GemvArgs& A, int dtype, int mode, bool mixed, int cus) {
-    BatchPlan bp;
-    const int64_t lim = INT32_MAX;
-    bool ok = A.M >= 3 && A.M <= 16 && dtype == CBK_F16 && A.gs % 128 == 0 && A.K % 8 == 0 &&
-              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim && cus > 0;
-    for (int i = 0; i < 3; ++i)
-        ok = ok && (int64_t)A.p[i].n * A.p[i].wpr * 4 < lim && (int64_t)A.p[i].n * A.G * 2 < lim;
-    if (mode == CBK_MODE_QKV) ok = ok && A.p[0].n % 16 == 0 && A.p[1].n % 16 == 0;
-    if (!ok) return bp;
-    int64_t best_rounds = INT64_MAX;
-    // one workgroup per CU (15 or 16 waves); the fewest rounds, then the smallest rw
-    for (int rw : {1, 2, 3}) {
-        if (mode == CBK_MODE_GATEUP && rw % 2) continue;
-        const int rb = 16 * rw;
-        if (mixed && (A.p[0].n % rb != 0 || A.p[1].n % rb != 0)) continue;
-        const int lds = batch_lds_bytes(A.M, rw);
-        if (lds > LDS_BUDGET) continue;
-        const int64_t grid = ceil_div(A.V, rb);
-        if (grid >= lim) continue;
-        const int64_t rounds = ceil_div(grid, (int64_t)cus);
-        if (rounds < best_rounds) {
-            best_rounds = rounds;
-            bp.rw = rw;
-            bp.grid = (int)grid;
-            bp.lds = lds;
-            bp.ok = true;
-        }
-    }
-    return bp;
-}
-
 // Kernels (per device) whose dynamic-LDS limit has been raised to the whole budget.  The
 // limit is set once, to LDS_BUDGET, and never lowered, so launches of one kernel with
 // different LDS sizes from several threads cannot undercut each other.
@@ -651,27 +498,18 @@ hipError_t ensure_lds(const void* f, int bytes) {
     return e;
 }
 
-int max_bits(const GemvArgs& A) { return std::max({A.p[0].bits, A.p[1].bits, A.p[2].bits}); }
-
 // The launch a decode call makes: kernel family, the kernel, its grid, workgroup size,
 // dynamic LDS and K splits.  plan_decode also fills the plan fields of A the kernels read.
 struct DecodeLaunch {
     int family = 0;              // CBK_KERNEL_*
-    const void* f = nullptr;     // kernel address (the generic kernel is chosen at launch)
+    const void* f = nullptr;     // kernel address
     int grid = 0, block = 0, lds = 0, P = 1;
 };
 
 DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rho, int cus) {
+    (void)rho;
     DecodeLaunch L;
-    bool mfma_ok = !mixed || (A.p[0].n % MFMA_TILE == 0 && A.p[1].n % MFMA_TILE == 0);
-    // direct-to-LDS dwordx4 streaming needs 16-byte aligned rows
-    for (int i = 0; i < 3; ++i)
-        mfma_ok = mfma_ok && (reinterpret_cast<uintptr_t>(A.p[i].w) % 16 == 0) && ((int64_t)A.C * A.p[i].bits) % 4 == 0;
-    // batch 1 stages x through 16-byte pieces and fetches (scale, zero) spans as
-    // 16-byte-aligned pieces
-    bool xvec = (A.K % 8 == 0) && (reinterpret_cast<uintptr_t>(A.x) % 16 == 0);
-    for (int i = 0; i < 3; ++i)
-        xvec = xvec && reinterpret_cast<uintptr_t>(A.p[i].s) % 16 == 0 && reinterpret_cast<uintptr_t>(A.p[i].z) % 16 == 0;
+    // batch 1 and 2: the streaming kernel
     const StreamPlan sp = plan_stream(A, dtype, mode, mixed, split_k);
     if (sp.ok) {
         A.P = sp.P;
@@ -681,30 +519,16 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divGS = make_fastdiv((uint32_t)(A.gs / 32));
         L.family = CBK_KERNEL_STREAM;
-        L.f = gemv_stream_kernel_for(mode, A.p[0].bits, mixed, sp.mb, sp.rpw, dtype == CBK_BF16);
+        L.f = gemv_stream_kernel_for(mode, A.src[0].bits, mixed, sp.mb, sp.rpw, dtype == CBK_BF16);
         L.grid = sp.grid;
         L.block = 64 * sp.ks * sp.rw;
         L.lds = sp.lds;
         L.P = sp.P;
         return L;
     }
-    // batch 3..16: the K-split streaming kernel (one dispatch: unsplit, or splits that
-    // combine in the dispatch), else the whole-K batch kernel where the streaming kernel's
-    // split would need a reduce launch
+    // batch 3..16: the K-split streaming kernel (unsplit, or splits that combine in the
+    // dispatch)
     const BStreamPlan bp = plan_bstream(A, dtype, mode, mixed, split_k, cus);
-    const BatchPlan bt = (bp.ok && (bp.P == 1 || bp.filled)) ? BatchPlan{} : plan_batch(A, dtype, mode, mixed, cus);
-    if (bt.ok) {
-        A.P = 1;
-        A.st_rw = bt.rw;
-        A.divG = make_fastdiv((uint32_t)(A.gs / 128));
-        L.family = CBK_KERNEL_BATCH;
-        L.f = gemv_batch_kernel_for(mode, A.p[0].bits, mixed, bt.rw);
-        L.grid = bt.grid;
-        L.block = batch_threads(bt.rw);
-        L.lds = bt.lds;
-        L.P = 1;
-        return L;
-    }
     if (bp.ok) {
         A.P = bp.P;
         A.st_ks = bp.ks;
@@ -713,54 +537,38 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divG = make_fastdiv((uint32_t)(A.gs / 128));
         L.family = CBK_KERNEL_BSTREAM;
-        L.f = gemv_bstream_kernel_for(mode, A.p[0].bits, mixed, bp.bsu, dtype == CBK_BF16);
+        L.f = gemv_bstream_kernel_for(mode, A.src[0].bits, mixed, bp.bsu, dtype == CBK_BF16);
         L.grid = bp.grid;
         L.block = 64 * bp.ks * bp.rw;
         L.lds = bp.lds;
         L.P = bp.P;
         return L;
     }
-    const Plan pl = plan_gemv(dtype, A.M, A.V, A.K, A.gs, max_bits(A), split_k, rho, cus, mfma_ok, xvec);
+    // everything else: the fp32 matrix-core kernel
+    const AnyPlan pl = plan_any(A.M, A.V, A.K, split_k);
     A.P = pl.P;
     A.ntiles = pl.ntiles;
     A.mtiles = pl.mtiles;
-    A.jobs = pl.jobs;
-    A.nw = pl.nw;
-    A.units = pl.units;
-    A.xs_bytes = pl.L.xs_bytes;
-    A.meta_off = pl.L.meta_off;
-    A.ring_off = pl.L.ring_off;
-    A.wave_bytes = pl.L.wave_bytes;
-    A.red_off = pl.L.red_off;
-    A.sum_off = pl.L.sum_off;
-    A.tab_off = pl.L.tab_off;
-    A.raw_off = pl.L.raw_off;
-    A.raw_np = pl.L.raw_np;
-    A.lds_bytes = pl.lds;
-    A.ring = pl.ring;
+    A.jobs = (int)std::min<int64_t>(pl.jobs, INT32_MAX);
     A.divP = make_fastdiv((uint32_t)A.P);
     A.divT = make_fastdiv((uint32_t)std::max(A.ntiles, 1));
-    A.divW = make_fastdiv((uint32_t)std::max(A.nw, 1));
-    A.divG = make_fastdiv((uint32_t)std::max(A.gs >> 7, 1));
-    A.divNP = make_fastdiv((uint32_t)std::max(A.raw_np, 1));
+    A.divGS = make_fastdiv((uint32_t)(A.gs / 32));
+    A.st_xvec = (A.K % 8 == 0) && (reinterpret_cast<uintptr_t>(A.x) % 16 == 0);
+    L.family = CBK_KERNEL_GENERIC;
+    L.f = gemv_any_kernel_for(dtype, mode);
+    L.grid = A.jobs;
+    L.block = 64 * pl.waves;
+    L.lds = 0;
     L.P = pl.P;
-    L.grid = pl.grid;
-    if (pl.mfma) {
-        L.family = CBK_KERNEL_MFMA;
-        L.f = gemv_mfma_kernel_for(mode, A.p[0].bits, mixed, pl.unit_rows ? 1 : 16);
-        L.block = 64 * pl.nw;
-        L.lds = pl.lds;
-    } else {
-        L.family = CBK_KERNEL_GENERIC;
-        L.block = GENERIC_THREADS;
-    }
     return L;
 }
 
-// Whether the launch's K splits combine inside the dispatch (the streaming kernels, with
-// a counter per row block in one window) rather than in a reduce launch.
+// Whether the launch's K splits can combine inside the dispatch (the streaming kernels
+// and the fp32 matrix-core kernel, with a counter per row block in one window) rather
+// than in a combine launch.
 bool combines_in_dispatch(const DecodeLaunch& L) {
-    return L.P > 1 && (L.family == CBK_KERNEL_STREAM || L.family == CBK_KERNEL_BSTREAM) &&
+    return L.P > 1 &&
+           (L.family == CBK_KERNEL_STREAM || L.family == CBK_KERNEL_BSTREAM || L.family == CBK_KERNEL_GENERIC) &&
            L.grid / L.P <= SPLIT_COUNTERS;
 }
 
@@ -772,8 +580,7 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     const int cus = cu_count(device);
     if (cus <= 0) return fail(CBK_EHIP, "cannot query the compute-unit count of device %d", device);
     const DecodeLaunch L = plan_decode(A, dtype, mode, mixed, split_k, rho, cus);
-    if (L.family == CBK_KERNEL_MFMA &&
-        ((int64_t)A.units * A.P >= (1ll << 31) || (int64_t)A.jobs * 16 >= (1ll << 31)))
+    if (L.family == CBK_KERNEL_GENERIC && (int64_t)A.ntiles * A.mtiles * A.P >= (1ll << 31))
         return fail(CBK_EINVAL, "packed_gemv: problem too large for 32-bit job indexing");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     A.split_cnt = nullptr;
@@ -784,35 +591,40 @@ int run_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int rh
     } else {
         A.partial = nullptr;
     }
-    hipError_t e;
-    if (L.family == CBK_KERNEL_GENERIC) {
-        e = launch_gemv_generic(A, dtype, mode, L.grid, s);
-    } else {
-        e = ensure_lds(L.f, L.lds);
-        if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
-        void* args[] = {&A};
-        e = launch(L.f, dim3(L.grid), dim3(L.block), args, (size_t)L.lds, s);
-    }
+    hipError_t e = ensure_lds(L.f, L.lds);
+    if (e != hipSuccess) return hip_fail(e, "packed_gemv: LDS attribute");
+    void* args[] = {&A};
+    e = launch(L.f, dim3(L.grid), dim3(L.block), args, (size_t)L.lds, s);
     if (e != hipSuccess) return hip_fail(e, "packed_gemv: launch");
     if (A.P > 1 && !A.split_cnt) {
-        e = launch_gemv_reduce(A, dtype, mode, s);
-        if (e != hipSuccess) return hip_fail(e, "packed_gemv: reduce launch");
+        e = launch_gemv_combine(A, dtype, mode, s);
+        if (e != hipSuccess) return hip_fail(e, "packed_gemv: combine launch");
     }
     return CBK_OK;
 }
 
-Proj make_proj(const int32_t* w, const void* s, const void* z, const void* b, void* out, int64_t n, int bits,
-               int64_t K) {
-    Proj p{};
-    p.w = reinterpret_cast<const uint32_t*>(w);
-    p.s = s;
-    p.z = z;
-    p.b = b;
-    p.out = out;
-    p.n = (int)n;
-    p.bits = bits;
-    p.wpr = (int)(ceil_div(K, 32) * bits);
-    return p;
+// Projection i of a decode call: its weight side and its output side.
+void set_proj(GemvArgs& A, int i, const int32_t* w, const void* s, const void* z, const void* b, void* out,
+              int64_t n, int bits, int64_t K) {
+    Src& S = A.src[i];
+    S.w = reinterpret_cast<const uint32_t*>(w);
+    S.s = s;
+    S.z = z;
+    S.n = (int)n;
+    S.wpr = (int)(ceil_div(K, 32) * bits);
+    S.bits = bits;
+    S.pad_ = 0;
+    Dst& D = A.dst[i];
+    D.y = out;
+    D.bias = b;
+    D.ld = (int)n;
+    D.pad_ = 0;
+}
+
+// Projections 1 and 2 of a single-projection call repeat projection 0.
+void repeat_proj0(GemvArgs& A) {
+    A.src[1] = A.src[2] = A.src[0];
+    A.dst[1] = A.dst[2] = A.dst[0];
 }
 
 GemvArgs base_args(const void* x, int64_t M, int64_t K, int gs) {
@@ -855,9 +667,9 @@ int qkv_common(const void* x, int dtype, int64_t M, int64_t K, const int32_t* wq
     }
     if (M == 0) return CBK_OK;
     GemvArgs A = base_args(x, M, K, group_size);
-    A.p[0] = make_proj(wq, sq, zq, bq, out_q, nq, bits_q, K);
-    A.p[1] = make_proj(wk, sk, zk, bk, out_k, nk, bits_k, K);
-    A.p[2] = make_proj(wv, sv, zv, bv, out_v, nv, bits_v, K);
+    set_proj(A, 0, wq, sq, zq, bq, out_q, nq, bits_q, K);
+    set_proj(A, 1, wk, sk, zk, bk, out_k, nk, bits_k, K);
+    set_proj(A, 2, wv, sv, zv, bv, out_v, nv, bits_v, K);
     A.V = (int)(nq + nk + nv);
     A.perm_hd = perm_hd;
     if (rope) {
@@ -906,10 +718,10 @@ int cbk_max_rho(int device, int bits, int mode, int* out) {
     const int64_t n = mode == CBK_MODE_GATEUP ? 11008 : 4096;
     GemvArgs A = base_args(a, 1, 4096, 128);
     for (int i = 0; i < 3; ++i)
-        A.p[i] = make_proj(reinterpret_cast<const int32_t*>(base), a, a, nullptr, nullptr, n, bits, 4096);
+        set_proj(A, i, reinterpret_cast<const int32_t*>(base), a, a, nullptr, nullptr, n, bits, 4096);
     A.V = (int)(mode == CBK_MODE_QKV ? 3 * n : (mode == CBK_MODE_GATEUP ? 2 * n : n));
     const DecodeLaunch L = plan_decode(A, CBK_F16, mode, false, 1, 1, cus);
-    const void* f = L.f ? L.f : gemv_generic_kernel_for(CBK_F16, mode);
+    const void* f = L.f;
     int blocks = 0;
     hipError_t e = ensure_lds(f, L.lds);
     if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, L.block, (size_t)L.lds);
@@ -920,15 +732,7 @@ int cbk_max_rho(int device, int bits, int mode, int* out) {
 
 int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int group_size, int split_k) {
     if (M <= 0 || V <= 0 || K <= 0 || group_size <= 0 || split_k < 1) return 0;
-    int P = 1;
-    for (bool mf : {true, false}) {
-        for (int bits : {2, 3, 4}) {
-            for (bool xv : {true, false}) {
-                const Plan pl = plan_gemv(dtype, M, V, K, group_size, bits, split_k, 0, 256, mf, xv);
-                P = std::max(P, pl.P);
-            }
-        }
-    }
+    int P = plan_any(M, V, K, split_k).P;
     if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M, dtype)));
     if (M >= 3 && M <= 16) {  // 4-unit slices split at least as often as 8-unit ones; gate-up rows
         const int64_t C = ceil_div(K, 32);
@@ -953,9 +757,8 @@ int cbk_packed_gemv(const void* x, int dtype, int64_t M, int64_t K, const int32_
     if (!out) return fail(CBK_EINVAL, "packed_gemv: out must be non-null");
     if (M == 0) return CBK_OK;
     GemvArgs A = base_args(x, M, K, group_size);
-    A.p[0] = make_proj(packed, scales, zeros, bias, out, N, bits, K);
-    A.p[1] = A.p[0];
-    A.p[2] = A.p[0];
+    set_proj(A, 0, packed, scales, zeros, bias, out, N, bits, K);
+    repeat_proj0(A);
     A.V = (int)N;
     A.act = act;
     return run_decode(A, dtype, CBK_MODE_GEMV, false, split_k, rho, partial, device, stream);
@@ -983,7 +786,7 @@ int cbk_decode_plan(int dtype, int64_t M, int64_t K, int group_size, int64_t n0,
     const void* a = reinterpret_cast<const void*>(base);
     GemvArgs A = base_args(a, M, K, group_size);
     for (int i = 0; i < 3; ++i)
-        A.p[i] = make_proj(reinterpret_cast<const int32_t*>(base), a, a, nullptr, nullptr, ns[i], bs[i], K);
+        set_proj(A, i, reinterpret_cast<const int32_t*>(base), a, a, nullptr, nullptr, ns[i], bs[i], K);
     A.V = (int)(mode == CBK_MODE_QKV ? ns[0] + ns[1] + ns[2] : (mode == CBK_MODE_GATEUP ? 2 * ns[0] : ns[0]));
     const bool mixed = mode == CBK_MODE_QKV && !(bs[0] == bs[1] && bs[1] == bs[2]);
     const DecodeLaunch L = plan_decode(A, dtype, mode, mixed, split_k, rho, cus);
@@ -1018,9 +821,8 @@ int cbk_packed_gemv_noalloc(const void* x, int dtype, int64_t M, int64_t K, cons
     const hipError_t e = scratch_for(device, &part);
     if (e != hipSuccess) return hip_fail(e, "packed_gemv_noalloc: scratch address");
     GemvArgs A = base_args(x, M, K, group_size);
-    A.p[0] = make_proj(packed, scales, zeros, bias, out, N, bits, K);
-    A.p[1] = A.p[0];
-    A.p[2] = A.p[0];
+    set_proj(A, 0, packed, scales, zeros, bias, out, N, bits, K);
+    repeat_proj0(A);
     A.V = (int)N;
     A.act = act;
     return run_decode(A, dtype, CBK_MODE_GEMV, false, split_k, rho, need > 0 ? part : nullptr, device, stream);
@@ -1040,9 +842,10 @@ int cbk_fused_gate_up(const void* x, int dtype, int64_t M, int64_t K, const int3
     if (2 * N > (1 << 30)) return fail(CBK_EINVAL, "fused_gate_up: out_features too large");
     if (M == 0) return CBK_OK;
     GemvArgs A = base_args(x, M, K, group_size);
-    A.p[0] = make_proj(wg, sg, zg, nullptr, out, N, bits, K);
-    A.p[1] = make_proj(wu, su, zu, nullptr, out, N, bits, K);
-    A.p[2] = A.p[0];
+    set_proj(A, 0, wg, sg, zg, nullptr, out, N, bits, K);
+    set_proj(A, 1, wu, su, zu, nullptr, out, N, bits, K);
+    A.src[2] = A.src[0];
+    A.dst[2] = A.dst[0];
     A.V = (int)(2 * N);
     return run_decode(A, dtype, CBK_MODE_GATEUP, false, split_k, rho, partial, device, stream);
 }
@@ -1100,10 +903,11 @@ int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K, const int32_
     A.act = act;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     A.divG = make_fastdiv((uint32_t)group_size);
+    A.xvec = (K % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
     const bool mc = use_matrix_cores && (dtype == CBK_F16 || dtype == CBK_BF16);
     hipError_t e;
     if (mc && gemm_f16_supported(A)) e = launch_gemm_f16(A, dtype, s);
-    else e = mc ? launch_gemm_mfma(A, dtype, s) : launch_gemm_valu(A, dtype, s);
+    else e = mc ? launch_gemm_mfma(A, dtype, s) : launch_gemm_f32(A, dtype, s);
     if (e != hipSuccess) return hip_fail(e, "packed_gemm: launch");
     return CBK_OK;
 }

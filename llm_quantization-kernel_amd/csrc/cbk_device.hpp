@@ -2,9 +2,10 @@
 //
 // Covers the reference's device helpers (Kernel/csrc/common.cuh:10-70 and
 // bitpack.cuh:10-46) re-designed for CDNA4: storage-type conversion, epilogue
-// activations, the virtual-row map of the fused modes, RoPE un-permutation, and
-// scalar code extraction for the VALU kernels.  The packed-fp16 MFMA decode lives
-// in cbk_decode.hpp.
+// activations, the virtual-row map of the fused modes, RoPE un-permutation, the
+// row-pair finish stage every decode kernel ends with, the in-dispatch split-K
+// combine, and scalar code extraction.  The packed-fp16 in-place decode lives in
+// cbk_decode.hpp.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -100,20 +101,31 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
 }
 
 // ---------------------------------------------------------------- decode-call arguments
-struct Proj {
-    const uint32_t* w;   // packed [n, wpr]
-    const void* s;       // scales [n, G]
+// A decode call has up to three projections (plain GEMV: one; gate-up: gate and up;
+// QKV: q, k and v).  Each has a weight side, which the K loop of every kernel streams,
+// and an output side, which only the finish stage writes; the two are kept apart so
+// that the finish stage (finish_pair) sees nothing of the weights and the K loops
+// nothing of the outputs.
+struct Src {
+    const uint32_t* w;   // packed codes [n, wpr]
+    const void* s;       // scales [n, G], x's dtype
     const void* z;       // zeros  [n, G]
-    const void* b;       // bias [n] or nullptr
-    void* out;           // [M, n]
     int n;               // rows
+    int wpr;             // 32-bit words per row = C * bits
     int bits;            // 2 / 3 / 4
-    int wpr;             // words per row = C * bits
+    int pad_;
+};
+
+struct Dst {
+    void* y;             // outputs [M, ld]
+    const void* bias;    // [ld] or nullptr
+    int ld;              // row stride of y (the projection's rows)
     int pad_;
 };
 
 struct GemvArgs {
-    Proj p[3];
+    Src src[3];
+    Dst dst[3];
     const void* x;         // [M, K]
     float* partial;        // [P, M, V] fp32 when P > 1
     const float* rope_cos; // [M, head_dim] or nullptr
@@ -122,24 +134,9 @@ struct GemvArgs {
     int C, G, gs;          // 32-code chunks per row, groups per row, group size
     int P, act;            // K splits, activation (GEMV mode)
     int head_dim, perm_hd;
-    int ntiles, mtiles, jobs;
-    int nw;                // waves per workgroup (MFMA kernel)
-    int units;             // 128-code units per row (MFMA kernel)
-    int xs_bytes;          // per-wave LDS: bytes of the staged activations (unit sums follow)
-    int meta_off;          // per-wave LDS: offset of the (scale, zero) pairs
-    int ring_off;          // per-wave LDS: offset of the weight ring
-    int wave_bytes;        // per-wave LDS region size
-    int red_off;           // workgroup LDS: offset of the cross-wave reduction area
-    int lds_bytes;         // dynamic LDS bytes per workgroup
-    int ring;              // weight-ring slots per wave (MFMA kernel), 1 .. Ring<>::RMAX
-    // batch-1 MFMA layout: workgroup-shared staging areas (offsets into the LDS)
-    int sum_off;           // unit sums [unit][2] fp32
-    int tab_off;           // masked scales [unit][tile row][kq] fp32
-    int raw_off;           // raw (scale, zero) row spans [tensor][tile row][piece] x 16 B
-    int raw_np;            // 16-byte pieces per row span
+    int ntiles, mtiles, jobs;  // fp32 matrix-core kernel: 16-row tiles, 16-row batch tiles, jobs
     int pad_;
-    FastDiv divP, divT, divW, divG;   // by P, ntiles, nw and gs / 128 (MFMA kernel)
-    FastDiv divNP;                    // by raw_np
+    FastDiv divP, divT, divG;  // by P, ntiles and gs / 128
     // batch-1 streaming kernel (gemv_stream.hip)
     int st_ks;             // K slices per job (waves per row group)
     int st_rw;             // row groups per workgroup (one wave's rows each)
@@ -151,38 +148,41 @@ struct GemvArgs {
     uint32_t* split_cnt;
 };
 
-// Per-wave weight ring of the MFMA decode kernel (host and device).  A stage is
-// S consecutive 128-code units of the 16 rows of a job tile, copied HBM -> LDS
-// with direct-to-LDS dwordx4 loads: 16-byte piece p of a stage lands at byte 16p,
-// row r of the tile owns pieces [r*PITCH, r*PITCH + PPR) and one pad piece that
-// staggers the rows across LDS banks.  Up to RMAX stages are in flight per wave
-// (RMAX * NDMA stays well inside the 6-bit vmcnt counter).
-template <int BITS> struct Ring {
-    static constexpr int S = 4;                       // units per stage
-    static constexpr int RMAX = 8;                    // ring slots per wave, at most
-    static constexpr int RMAX1 = 4;                   // ... at batch 1 (units as MFMA rows)
-    static constexpr int PPR = S * BITS;              // 16-byte pieces of one row per stage
-    static constexpr int PITCH = PPR + 1;             // LDS row pitch in pieces
-    static constexpr int NDMA = (16 * PITCH + 63) / 64;   // dwordx4 LDS-DMA instructions per stage
-    static constexpr int SLOT = NDMA * 64 * 16;       // LDS bytes of one stage
-};
-
-__host__ __device__ constexpr int ring_slot_bytes(int bits) {
-    return bits == 2 ? Ring<2>::SLOT : (bits == 3 ? Ring<3>::SLOT : Ring<4>::SLOT);
-}
-
-// Projection field select between values of the kernel-argument struct.  The
-// empty asm pins each loaded field as an SGPR value, so LLVM cannot fold the
-// choice into a load from a chosen field address -- an address select into the
-// kernarg struct would force a copy of the whole struct to scratch.
+// ---------------------------------------------------------------- projection views
+// A projection's fields as values.  Each candidate field is pinned as an SGPR value
+// first (the empty asm), so LLVM selects between values rather than between addresses
+// inside the kernel-argument block -- an address select there would copy the whole
+// block to scratch.  `p` may differ between lanes (the select is then per lane).
 template <typename T>
-__device__ __forceinline__ T kernarg_value(T v) {
+__device__ __forceinline__ T pinned(T v) {
     asm("" : "+s"(v));
     return v;
 }
-#define CBK_SEL(A, proj, field)                                                                      \
-    ((proj) == 0 ? kernarg_value((A).p[0].field)                                                     \
-                 : ((proj) == 1 ? kernarg_value((A).p[1].field) : kernarg_value((A).p[2].field)))
+template <typename T>
+__device__ __forceinline__ T pick3(int p, T a, T b, T c) {
+    return p == 0 ? pinned(a) : (p == 1 ? pinned(b) : pinned(c));
+}
+
+__device__ __forceinline__ Src src_of(const GemvArgs& A, int p) {
+    Src r;
+    r.w = pick3(p, A.src[0].w, A.src[1].w, A.src[2].w);
+    r.s = pick3(p, A.src[0].s, A.src[1].s, A.src[2].s);
+    r.z = pick3(p, A.src[0].z, A.src[1].z, A.src[2].z);
+    r.n = pick3(p, A.src[0].n, A.src[1].n, A.src[2].n);
+    r.wpr = pick3(p, A.src[0].wpr, A.src[1].wpr, A.src[2].wpr);
+    r.bits = pick3(p, A.src[0].bits, A.src[1].bits, A.src[2].bits);
+    r.pad_ = 0;
+    return r;
+}
+
+__device__ __forceinline__ Dst dst_of(const GemvArgs& A, int p) {
+    Dst r;
+    r.y = pick3(p, A.dst[0].y, A.dst[1].y, A.dst[2].y);
+    r.bias = pick3(p, A.dst[0].bias, A.dst[1].bias, A.dst[2].bias);
+    r.ld = pick3(p, A.dst[0].ld, A.dst[1].ld, A.dst[2].ld);
+    r.pad_ = 0;
+    return r;
+}
 
 // Virtual row v -> (projection, local row): QKV concatenates [q; k; v], gate-up
 // interleaves gate row n -> 2n and up row n -> 2n+1 (packed_gemv.cu:33-42).
@@ -191,7 +191,7 @@ __device__ __forceinline__ void vmap(const GemvArgs& A, int v, int& proj, int& r
     if constexpr (MODE == MODE_GATEUP) {
         proj = v & 1; r = v >> 1;
     } else if constexpr (MODE == MODE_QKV) {
-        const int n0 = A.p[0].n, n1 = A.p[1].n;
+        const int n0 = A.src[0].n, n1 = A.src[1].n;
         if (v < n0) { proj = 0; r = v; }
         else if (v < n0 + n1) { proj = 1; r = v - n0; }
         else { proj = 2; r = v - n0 - n1; }
@@ -200,53 +200,92 @@ __device__ __forceinline__ void vmap(const GemvArgs& A, int v, int& proj, int& r
     }
 }
 
-// Final value of virtual row v for batch row b.  `partner` is the fp32 sum of row
-// v ^ 1 (the up row of a gate row; the RoPE partner of a Q/K row), before bias.
+// ---------------------------------------------------------------- finish stage
+// Every decode kernel ends here.  Outputs are finished per pair of virtual rows
+// (v0, v0 + 1), v0 even, of one batch row b, from the two rows' fp32 K sums before
+// bias -- the unit all three modes share:
+//  * gate-up: the pair is (gate n, up n), v0 = 2n, and gives the one output
+//    silu(g) * u (the fused module has no bias);
+//  * QKV with RoPE: Q and K rows are stored pair-interleaved per head, so the pair
+//    holds the original rows (h hd + d, h hd + d + hd/2) that the rotation mixes --
+//    both outputs come from one thread, each row's bias read once;
+//  * plain rows, and QKV without RoPE: two independent outputs (act(y + bias) for a
+//    plain GEMV; Q and K rows still go back to their original order).
+// `two` is false when v0 + 1 is past V (an odd V).
+
+// One QKV row with no rotation: bias, then the store at its original position.
+template <int DT>
+__device__ __forceinline__ void qkv_plain_row(const GemvArgs& A, int b, int v, float y) {
+    int p, r;
+    vmap<MODE_QKV>(A, v, p, r);
+    const Dst D = dst_of(A, p);
+    if (D.bias) y += load_f<DT>(D.bias, r);
+    store_f<DT>(D.y, (long)b * D.ld + rope_unperm(r, p < 2 ? A.perm_hd : 0), y);
+}
+
 template <int DT, int MODE>
-__device__ __forceinline__ void epilogue(const GemvArgs& A, int b, int v, float mine, float partner) {
-    int proj, r;
-    vmap<MODE>(A, v, proj, r);
-    if constexpr (MODE == MODE_GEMV) {
-        const float bias = A.p[0].b ? load_f<DT>(A.p[0].b, r) : 0.f;
-        store_f<DT>(A.p[0].out, (long)b * A.p[0].n + r, apply_act(mine + bias, A.act));
-    } else if constexpr (MODE == MODE_GATEUP) {
-        if (proj != 0) return;
-        store_f<DT>(A.p[0].out, (long)b * A.p[0].n + r, silu(mine) * partner);
-    } else {
-        const void* bias = CBK_SEL(A, proj, b);
-        void* out = CBK_SEL(A, proj, out);
-        const int n = CBK_SEL(A, proj, n);
-        float y = mine + (bias ? load_f<DT>(bias, r) : 0.f);
-        const int hd = proj < 2 ? A.perm_hd : 0;
-        const int orig = rope_unperm(r, hd);
-        if (A.rope_cos != nullptr && proj < 2) {
-            const float yp = partner + (bias ? load_f<DT>(bias, r ^ 1) : 0.f);
-            const int d = orig % A.head_dim;
-            const float c = A.rope_cos[(long)b * A.head_dim + d];
-            const float s = A.rope_sin[(long)b * A.head_dim + d];
-            y = (d < (A.head_dim >> 1)) ? (y * c - yp * s) : (y * c + yp * s);
+__device__ __forceinline__ void finish_pair(const GemvArgs& A, int b, int v0, float y0, float y1, bool two) {
+    if constexpr (MODE == MODE_GATEUP) {
+        store_f<DT>(A.dst[0].y, (long)b * A.dst[0].ld + (v0 >> 1), silu(y0) * y1);
+    } else if constexpr (MODE == MODE_GEMV) {
+        const void* bias = A.dst[0].bias;
+        if (bias) {
+            y0 += load_f<DT>(bias, v0);
+            if (two) y1 += load_f<DT>(bias, v0 + 1);
         }
-        store_f<DT>(out, (long)b * n + orig, y);
+        const long o = (long)b * A.dst[0].ld + v0;
+        store_f<DT>(A.dst[0].y, o, apply_act(y0, A.act));
+        if (two) store_f<DT>(A.dst[0].y, o + 1, apply_act(y1, A.act));
+    } else {
+        int p, r;
+        vmap<MODE_QKV>(A, v0, p, r);
+        if (A.rope_cos != nullptr && p < 2) {
+            // Q and K widths are multiples of the even head_dim (host check), so row
+            // v0 + 1 is row r + 1 of the same projection and head
+            const Dst D = dst_of(A, p);
+            if (D.bias) {
+                y0 += load_f<DT>(D.bias, r);
+                y1 += load_f<DT>(D.bias, r + 1);
+            }
+            const int hd = A.head_dim, half = hd >> 1;
+            const int lo = rope_unperm(r, hd);            // original row of stored row r
+            const int d = lo % hd;                        // < hd / 2
+            const float* cs = A.rope_cos + (long)b * hd;
+            const float* sn = A.rope_sin + (long)b * hd;
+            const long o = (long)b * D.ld + lo;
+            store_f<DT>(D.y, o, y0 * cs[d] - y1 * sn[d]);
+            store_f<DT>(D.y, o + half, y1 * cs[d + half] + y0 * sn[d + half]);
+        } else {
+            qkv_plain_row<DT>(A, b, v0, y0);
+            if (two) qkv_plain_row<DT>(A, b, v0 + 1, y1);
+        }
     }
 }
 
 // ---------------------------------------------------------------- split-K combine in the dispatch
 // The P workgroups of a row block (one per K split, on any XCD) combine their fp32
-// partials without the reduce launch that cb_reduce_kernel (packed_gemv.cu:166-180)
-// stands for.  Partials are written and read with agent-scope accesses (stores and
-// loads coherent across the XCDs' L2s, `sc1`), so no L2 write-back or invalidation is
-// needed: a release / acquire pair at agent scope would write back and invalidate the
-// whole L2 of the XCD per workgroup, which serialises (a K-split batch-1 GEMV went from
-// 7.6 to 38 us that way).  Each wave waits until its partial stores have completed,
-// the workgroup meets at a barrier, and one thread counts the workgroup in; the
-// workgroup that arrives last (old count P - 1) sets the counter back to zero for the
-// next call and adds the P partials in split order 0 .. P - 1 -- gemv_reduce_kernel's
-// order, so both paths give the same bits.  No workgroup waits for another.
+// partials without a second launch.  Partials are written and read with agent-scope
+// accesses (stores and loads coherent across the XCDs' L2s, `sc1`), so no L2
+// write-back or invalidation is needed: a release / acquire pair at agent scope would
+// write back and invalidate the whole L2 of the XCD per workgroup, which serialises
+// (a K-split batch-1 GEMV went from 7.6 to 38 us that way).  Each wave waits until its
+// partial stores have completed, the workgroup meets at a barrier, and one thread
+// counts the workgroup in; the workgroup that arrives last (old count P - 1) sets the
+// counter back to zero for the next call and adds the P partials in split order
+// 0 .. P - 1 -- the order of the combine launch, so both paths give the same bits.  No
+// workgroup waits for another.
 __device__ __forceinline__ void partial_put(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float partial_get(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A split's sums of the pair (v0, v0 + 1) of batch row b into the partial buffer.
+__device__ __forceinline__ void put_pair(const GemvArgs& A, int p, int b, int v0, float y0, float y1, bool two) {
+    float* row = A.partial + ((long)p * A.M + b) * A.V;
+    partial_put(row + v0, y0);
+    if (two) partial_put(row + v0 + 1, y1);
 }
 
 // After the workgroup's partial_put calls: returns, in every thread, whether this
@@ -266,25 +305,41 @@ __device__ __forceinline__ bool split_arrive(const GemvArgs& A, int blk, int* fl
     return *flag != 0;
 }
 
-// Sum of split partials p = 0 .. P - 1 of (batch row b, virtual row v), in that order.
-__device__ __forceinline__ float split_sum(const GemvArgs& A, int b, int v) {
-    float s = 0.f;
-    for (int p = 0; p < A.P; ++p) s += partial_get(A.partial + ((long)p * A.M + b) * A.V + v);
-    return s;
+// The pair (v0, v0 + 1) of batch row b summed over splits 0 .. P - 1 in that order,
+// then finished.
+template <int DT, int MODE>
+__device__ __forceinline__ void finish_from_partials(const GemvArgs& A, int b, int v0) {
+    const bool two = v0 + 1 < A.V;
+    const long stride = (long)A.M * A.V;
+    const float* q = A.partial + (long)b * A.V + v0;
+    float y0 = 0.f, y1 = 0.f;
+    for (int p = 0; p < A.P; ++p, q += stride) {
+        y0 += partial_get(q);
+        if (two) y1 += partial_get(q + 1);
+    }
+    finish_pair<DT, MODE>(A, b, v0, y0, y1, two);
 }
 
-// The combining workgroup's epilogue: rows [vbase, vbase + RB) of every batch row,
-// `nthr` threads, outputs of dtype DT.
+// The combining workgroup's finish: the pairs of rows [vbase, vbase + RB) (vbase and
+// RB even) of every batch row, over `nthr` threads.
 template <int DT, int MODE>
-__device__ __forceinline__ void split_epilogue(const GemvArgs& A, int vbase, int RB, int nthr) {
-    for (int t = threadIdx.x; t < A.M * RB; t += nthr) {
-        const int b = t / RB, v = vbase + (t - b * RB);
-        if (v < A.V) {
-            const bool paired = MODE == MODE_GATEUP || (MODE == MODE_QKV && A.rope_cos != nullptr);
-            const float partner = paired && (v ^ 1) < A.V ? split_sum(A, b, v ^ 1) : 0.f;
-            epilogue<DT, MODE>(A, b, v, split_sum(A, b, v), partner);
-        }
+__device__ __forceinline__ void split_finish(const GemvArgs& A, int vbase, int RB, int nthr) {
+    const int np = RB >> 1;
+    for (int t = threadIdx.x; t < A.M * np; t += nthr) {
+        const int b = t / np, v0 = vbase + 2 * (t - b * np);
+        if (v0 < A.V) finish_from_partials<DT, MODE>(A, b, v0);
     }
+}
+
+// LDS barrier for code that keeps global loads in flight across it: waits for this
+// wave's LDS accesses only (lgkmcnt), then meets the workgroup.  The compiler-level
+// memory clobbers on both sides keep LLVM from moving LDS loads or stores across the
+// barrier (the wait and barrier intrinsics alone do not order memory in the IR).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));    // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // ---------------------------------------------------------------- scalar code access

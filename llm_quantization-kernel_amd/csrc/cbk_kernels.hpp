@@ -15,10 +15,6 @@ hipError_t launch(const void* f, dim3 grid, dim3 block, void** args, size_t lds,
 // once per kernel and device; the limit is only ever raised.
 hipError_t lds_limit_raise(const void* f, int bytes);
 
-// gemv_mfma.hip: fp16, group size % 128 == 0.  Kernel address for the attribute
-// queries and the launch; max_batch <= 1 selects the single-row epilogue.
-const void* gemv_mfma_kernel_for(int mode, int bits, bool mixed, int max_batch);
-
 // gemv_stream.hip: batch 1 or 2 (mb staged activation rows), fp16 or bf16, group size % 32 == 0.  A job is rpw * st_rw
 // virtual rows x one K split; its workgroup has st_ks * st_rw waves, each over rpw rows
 // (STREAM_RPW, or STREAM_RPW_WIDE at batch 1) and one K slice of 64 * STREAM_CPL chunks.
@@ -34,22 +30,14 @@ const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int r
 // over 16 rows and one K slice of bsu (4 or 8) units.
 const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu, bool bf16);
 
-// gemv_batch.hip: batch 3..16, fp16, group size % 128 == 0, one dispatch.  A workgroup of
-// batch_threads(rw) threads (16 waves; 15 for rw = 3) owns rw (1, 2 or 3; 2 for gate-up)
-// blocks of 16 virtual rows over all of K, taken in phases of one 128-code unit per wave
-// whose converted activations it stages once.
-const void* gemv_batch_kernel_for(int mode, int bits, bool mixed, int rw);
-int batch_threads(int rw);
-int batch_lds_bytes(int M, int rw);
+// gemv_any.hip: any dtype / group size / alignment, on the fp32 matrix cores.  A job is
+// 16 virtual rows x 16 batch rows x one K split, one workgroup of 64 to ANY_MAX_THREADS
+// threads (whole waves) that share the split's chunks.
+constexpr int ANY_MAX_THREADS = 1024;
+const void* gemv_any_kernel_for(int dt, int mode);
 
-// gemv_generic.hip: any dtype / group size; 32 virtual rows x 1 batch row per job.
-constexpr int GENERIC_THREADS = 256;
-constexpr int GENERIC_ROWS = 32;
-hipError_t launch_gemv_generic(const GemvArgs& A, int dt, int mode, int grid, hipStream_t stream);
-const void* gemv_generic_kernel_for(int dt, int mode);
-
-// gemv_generic.hip: split-K combine + epilogue (P > 1).
-hipError_t launch_gemv_reduce(const GemvArgs& A, int dt, int mode, hipStream_t stream);
+// gemv_any.hip: the combine launch of split-K partials (P > 1 without arrival counters).
+hipError_t launch_gemv_combine(const GemvArgs& A, int dt, int mode, hipStream_t stream);
 
 struct GemmArgs {
     const void* x;          // [M, K]
@@ -59,13 +47,15 @@ struct GemmArgs {
     const void* b;          // bias [N] or nullptr
     void* out;              // [M, N]
     int M, N, K, C, G, gs, wpr, bits, act;
-    int pad_;
-    FastDiv divG;           // by the group size (gemm_f16.hip)
+    int xvec;               // x is 16-byte aligned and K % 8 == 0 (vector activation loads)
+    FastDiv divG;           // by the group size
 };
 
-// gemm.hip
+// gemm.hip: fp16 / bf16 on the 16-bit matrix cores, any alignment.
 hipError_t launch_gemm_mfma(const GemmArgs& A, int dt, hipStream_t stream);
-hipError_t launch_gemm_valu(const GemmArgs& A, int dt, hipStream_t stream);
+
+// gemm_f32.hip: any dtype, fp32 operands on the fp32 matrix cores, W-hat unrounded.
+hipError_t launch_gemm_f32(const GemmArgs& A, int dt, hipStream_t stream);
 
 // gemm_f16.hip: fp16 or bf16 (dt), K % 8 == 0, 16-byte aligned x.
 bool gemm_f16_supported(const GemmArgs& A);

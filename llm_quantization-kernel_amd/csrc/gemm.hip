@@ -1,6 +1,8 @@
 // gemm.hip -- prefill packed GEMM: out[M,N] = act(x . W-hat^T + bias).
 //
-// Replaces cb_gemm_tc_kernel / cb_gemm_scalar_kernel (Kernel/csrc/packed_gemm.cu:12-156).
+// The matrix-core prefill for fp16 / bf16 shapes gemm_f16.hip does not take (K % 8 != 0,
+// x or metadata not 16-byte aligned): cb_gemm_tc_kernel's contract
+// (Kernel/csrc/packed_gemm.cu:12-115).
 //
 // gemm_mfma_kernel (fp16 / bf16): 128x128 output tile, 4 waves in a 2x2 grid of
 // 64x64 wave tiles, K staged one 32-code chunk at a time through double-buffered
@@ -9,9 +11,6 @@
 // float is exact in fp32, so this equals the reference's rounding
 // (packed_gemm.cu:56,60).  Products run on v_mfma_f32_16x16x32_{f16,bf16} with fp32
 // accumulation; bias and activation are applied in fp32 before the final rounding.
-//
-// gemm_valu_kernel (any dtype, fp32 W-hat): the use_tensor_cores=False / fp32 path
-// (packed_gemm.cu:119-156 semantics), 16x16 outputs per workgroup.
 #include "cbk_device.hpp"
 #include "cbk_kernels.hpp"
 
@@ -181,53 +180,11 @@ __global__ void __launch_bounds__(THREADS) gemm_mfma_kernel(const GemmArgs A) {
     }
 }
 
-// fp32 VALU path: W-hat = (q - z) * s kept in fp32.
-constexpr int VT = 16;
-template <int DT, int BITS>
-__global__ void __launch_bounds__(VT * VT) gemm_valu_kernel(const GemmArgs A) {
-    __shared__ float sx[VT][33];
-    __shared__ float sw[VT][33];
-    const int tx = threadIdx.x % VT, ty = threadIdx.x / VT, tid = threadIdx.x;
-    const int m = blockIdx.y * VT + ty, n = blockIdx.x * VT + tx;
-    float acc = 0.f;
-    for (int kc = 0; kc < A.C; ++kc) {
-        for (int e = tid; e < VT * 32; e += VT * VT) {
-            const int mm = e / 32, kk = e % 32, gm = blockIdx.y * VT + mm, gk = kc * 32 + kk;
-            sx[mm][kk] = (gm < A.M && gk < A.K) ? load_f<DT>(A.x, (long)gm * A.K + gk) : 0.f;
-        }
-        for (int e = tid; e < VT * 32; e += VT * VT) {
-            const int nn = e / 32, kk = e % 32, gn = blockIdx.x * VT + nn;
-            float wv = 0.f;
-            if (gn < A.N) {
-                const int g = (kc * 32) / A.gs;
-                const uint32_t q = row_code(A.w + (long)gn * A.wpr, kc * 32 + kk, BITS);
-                wv = ((float)q - load_f<DT>(A.z, (long)gn * A.G + g)) * load_f<DT>(A.s, (long)gn * A.G + g);
-            }
-            sw[nn][kk] = wv;
-        }
-        __syncthreads();
-#pragma unroll 8
-        for (int kk = 0; kk < 32; ++kk) acc = fmaf(sx[ty][kk], sw[tx][kk], acc);
-        __syncthreads();
-    }
-    if (m < A.M && n < A.N) {
-        if (A.b) acc += load_f<DT>(A.b, n);
-        store_f<DT>(A.out, (long)m * A.N + n, apply_act(acc, A.act));
-    }
-}
-
 template <int DT>
 const void* mfma_for_bits(int bits) {
     if (bits == 2) return reinterpret_cast<const void*>(&gemm_mfma_kernel<DT, 2>);
     if (bits == 3) return reinterpret_cast<const void*>(&gemm_mfma_kernel<DT, 3>);
     return reinterpret_cast<const void*>(&gemm_mfma_kernel<DT, 4>);
-}
-
-template <int DT>
-const void* valu_for_bits(int bits) {
-    if (bits == 2) return reinterpret_cast<const void*>(&gemm_valu_kernel<DT, 2>);
-    if (bits == 3) return reinterpret_cast<const void*>(&gemm_valu_kernel<DT, 3>);
-    return reinterpret_cast<const void*>(&gemm_valu_kernel<DT, 4>);
 }
 
 }  // namespace
@@ -236,13 +193,6 @@ hipError_t launch_gemm_mfma(const GemmArgs& A, int dt, hipStream_t stream) {
     const void* f = dt == DT_F16 ? mfma_for_bits<DT_F16>(A.bits) : mfma_for_bits<DT_BF16>(A.bits);
     void* args[] = {const_cast<GemmArgs*>(&A)};
     return launch(f, dim3((A.N + BN - 1) / BN, (A.M + BM - 1) / BM), dim3(THREADS), args, 0, stream);
-}
-
-hipError_t launch_gemm_valu(const GemmArgs& A, int dt, hipStream_t stream) {
-    const void* f = dt == DT_F16 ? valu_for_bits<DT_F16>(A.bits)
-                  : dt == DT_BF16 ? valu_for_bits<DT_BF16>(A.bits) : valu_for_bits<DT_F32>(A.bits);
-    void* args[] = {const_cast<GemmArgs*>(&A)};
-    return launch(f, dim3((A.N + VT - 1) / VT, (A.M + VT - 1) / VT), dim3(VT * VT), args, 0, stream);
 }
 
 }  // namespace cbk

@@ -4,7 +4,7 @@
 // range is split, the partial write that cb_reduce_kernel (:166-180) combines,
 // for one or two activation rows (the decode step) in fp16 or bf16 with any group size
 // that is a multiple of 32.  Plain, fused-QKV and fused gate-up modes share the body; the
-// epilogue is cb_epilogue's (:54-81, cbk_device.hpp).
+// outputs are finished a row pair at a time (finish_pair, cbk_device.hpp).
 //
 // Job = (block of RB = RPW RW virtual rows, K split p).  A workgroup holds KS x RW
 // waves: wave (ks, rw) takes rows RPW rw .. RPW rw + RPW - 1 of the block (RPW = 4,
@@ -28,8 +28,8 @@
 //   4. Each 4 rows' lane sums meet by v_permlane32_swap, v_permlane16_swap and four
 //      DPP row rotations (every lane of a 16-lane row ends with one row's total).
 //   5. Row totals of the slices meet in LDS and are added in slice order (so the
-//      result does not depend on wave timing); the epilogue runs per row, or with
-//      P > 1 the fp32 partial is written for the split-K combine.
+//      result does not depend on wave timing); the finish stage runs per row pair, or
+//      with P > 1 the fp32 partials are written for the split-K combine.
 #include "cbk_decode.hpp"
 #include "cbk_device.hpp"
 #include "cbk_kernels.hpp"
@@ -80,7 +80,7 @@ struct ProjRes {
     __amdgpu_buffer_rsrc_t w, s, z;
 };
 
-__device__ __forceinline__ ProjRes proj_res(const Proj& p, int G) {
+__device__ __forceinline__ ProjRes proj_res(const Src& p, int G) {
     ProjRes r;
     r.w = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.w), (short)0, p.n * p.wpr * 4, RAW);
     r.s = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.s), (short)0, p.n * G * 2, RAW);
@@ -229,11 +229,6 @@ __device__ __forceinline__ float reduce4(const float (&a)[4]) {
 
 __device__ __forceinline__ int lane_row(int lane) { return ((lane >> 5) & 1) | (((lane >> 4) & 1) << 1); }
 
-__device__ __forceinline__ void barrier_lds() {
-    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));    // lgkmcnt(0); leaves loads in flight
-    __builtin_amdgcn_s_barrier();
-}
-
 template <int BITS, int MODE, int MB, int RPW, int DT>
 __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     const int tid = threadIdx.x, lane = tid & 63;
@@ -263,9 +258,9 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
 
     // 1b. the wave's packed chunks and their (scale, zero) halves
     ProjRes R[3];
-    R[0] = proj_res(A.p[0], A.G);
-    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.p[1], A.G);
-    if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.p[1], A.G); R[2] = proj_res(A.p[2], A.G); }
+    R[0] = proj_res(A.src[0], A.G);
+    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.src[1], A.G);
+    if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.src[1], A.G); R[2] = proj_res(A.src[2], A.G); }
     int gi[CPL];
     bool cin[CPL];
 #pragma unroll
@@ -283,7 +278,7 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
         int proj, r;
         vmap<MODE>(A, vin ? v : 0, proj, r);
         const ProjRes& P = proj == 0 ? R[0] : (proj == 1 ? R[1] : R[2]);
-        const int wpr = CBK_SEL(A, proj, wpr);
+        const int wpr = src_of(A, proj).wpr;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = ks * SLICE + lane + 64 * i;
@@ -322,7 +317,7 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
             for (int q = 0; q < 4; ++q) Xl[(b * 4 + q) * NCH + tid] = X[q];
         }
     }
-    barrier_lds();
+    lds_barrier();
 
     // 3. rows: each chunk is decoded once and meets every batch row's activations
     u4 X[MB][CPL][4];
@@ -375,25 +370,28 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
             if ((lane & 15) == 0) red[(ks * MB + b) * RB + RPW * rw + 4 * q + lane_row(lane)] = tot;
         }
     }
-    barrier_lds();
+    lds_barrier();
 
-    // 5. slices in order, then the epilogue (or the split's partial)
-    for (int t = tid; t < MB * RB; t += 64 * KS * RW) {
-        const int b = t / RB, row = t - b * RB;
+    // 5. slices in order, then the finish stage (or the split's partials), a row pair
+    //    per thread
+    const int NP = RB / 2;
+    for (int t = tid; t < MB * NP; t += 64 * KS * RW) {
+        const int b = t / NP, row = 2 * (t - b * NP);
         const int v = vbase + row;
         if (b < A.M && v < A.V) {
-            float mine = 0.f, partner = 0.f;
+            float y0 = 0.f, y1 = 0.f;
             for (int k = 0; k < KS; ++k) {
-                mine += red[(k * MB + b) * RB + row];
-                partner += red[(k * MB + b) * RB + (row ^ 1)];
+                y0 += red[(k * MB + b) * RB + row];
+                y1 += red[(k * MB + b) * RB + row + 1];
             }
-            if (A.P == 1) epilogue<DT, MODE>(A, b, v, mine, partner);
-            else partial_put(A.partial + ((long)p * A.M + b) * A.V + v, mine);
+            const bool two = v + 1 < A.V;
+            if (A.P == 1) finish_pair<DT, MODE>(A, b, v, y0, y1, two);
+            else put_pair(A, p, b, v, y0, y1, two);
         }
     }
     // 6. with P > 1 and arrival counters, the last split of the block combines
     if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
-        split_epilogue<DT, MODE>(A, vbase, RB, 64 * KS * RW);
+        split_finish<DT, MODE>(A, vbase, RB, 64 * KS * RW);
 }
 
 // ------------------------------------------------------------------ batch rows 3..16
@@ -465,11 +463,11 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
 
     // 1b. the wave's packed chunks and the (scale, zero) of each unit's group
     ProjRes R[3];
-    R[0] = proj_res(A.p[0], A.G);
-    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.p[1], A.G);
-    if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.p[1], A.G); R[2] = proj_res(A.p[2], A.G); }
+    R[0] = proj_res(A.src[0], A.G);
+    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.src[1], A.G);
+    if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.src[1], A.G); R[2] = proj_res(A.src[2], A.G); }
     const ProjRes& P = proj == 0 ? R[0] : (proj == 1 ? R[1] : R[2]);
-    const int wpr = CBK_SEL(A, proj, wpr);
+    const int wpr = src_of(A, proj).wpr;
     // the (scale, zero) of unit 4 e + kq's group of row j: BSU / 4 2-byte gathers each per
     // wave (lanes of a row then share them by ds_bpermute), rather than one per unit
     static_assert(BSU % 4 == 0, "whole units per lane quarter");
@@ -529,7 +527,7 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
             if constexpr (DT == DT_BF16) XFu[(c >> 2) * 16 + i] = __builtin_ldexpf(1.0f, cu);
         }
     }
-    barrier_lds();
+    lds_barrier();
 
     // 3. units: A operands of batch row min(j, M - 1) (rows past M repeat a staged row;
     // their D rows are not stored)
@@ -574,25 +572,28 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
         const int i = 4 * kq + q;
         if (i < M) red[(ks * M + i) * RB + roff] = acc[q];
     }
-    barrier_lds();
+    lds_barrier();
 
-    // 5. slices in order, then the epilogue (or the split's partial)
-    for (int t = tid; t < M * RB; t += nthr) {
-        const int b = t / RB, ro = t - b * RB;
+    // 5. slices in order, then the finish stage (or the split's partials), a row pair
+    //    per thread
+    const int NP = RB / 2;
+    for (int t = tid; t < M * NP; t += nthr) {
+        const int b = t / NP, ro = 2 * (t - b * NP);
         const int v = vbase + ro;
         if (v < A.V) {
-            float mine = 0.f, partner = 0.f;
+            float y0 = 0.f, y1 = 0.f;
             for (int k = 0; k < KS; ++k) {
-                mine += red[(k * M + b) * RB + ro];
-                partner += red[(k * M + b) * RB + (ro ^ 1)];
+                y0 += red[(k * M + b) * RB + ro];
+                y1 += red[(k * M + b) * RB + ro + 1];
             }
-            if (A.P == 1) epilogue<DT, MODE>(A, b, v, mine, partner);
-            else partial_put(A.partial + ((long)p * A.M + b) * A.V + v, mine);
+            const bool two = v + 1 < A.V;
+            if (A.P == 1) finish_pair<DT, MODE>(A, b, v, y0, y1, two);
+            else put_pair(A, p, b, v, y0, y1, two);
         }
     }
     // 6. with P > 1 and arrival counters, the last split of the block combines
     if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
-        split_epilogue<DT, MODE>(A, vbase, RB, nthr);
+        split_finish<DT, MODE>(A, vbase, RB, nthr);
 }
 
 template <int MODE, int BITS, int BSU, int DT>
@@ -603,7 +604,7 @@ __global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
     } else {
         int proj, r;
         vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * 16 * A.st_rw, proj, r);
-        const int bits = CBK_SEL(A, proj, bits);
+        const int bits = src_of(A, proj).bits;
         if (bits == 2) bstream_body<2, MODE, BSU, DT>(A, lds);
         else if (bits == 3) bstream_body<3, MODE, BSU, DT>(A, lds);
         else bstream_body<4, MODE, BSU, DT>(A, lds);
@@ -624,7 +625,7 @@ __global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
     } else {
         int proj, r;
         vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * RPW * A.st_rw, proj, r);
-        const int bits = CBK_SEL(A, proj, bits);
+        const int bits = src_of(A, proj).bits;
         if (bits == 2) stream_body<2, MODE, MB, RPW, DT>(A, lds);
         else if (bits == 3) stream_body<3, MODE, MB, RPW, DT>(A, lds);
         else stream_body<4, MODE, MB, RPW, DT>(A, lds);

@@ -55,7 +55,11 @@ def decode_plan(dtype, batch, in_features, group_size, out_features, bits, kind,
 # ----------------------------------------------------------------------------- numpy cores
 
 def silu64(v: np.ndarray) -> np.ndarray:
-    return v / (1.0 + np.exp(-v))
+    """v * sigmoid(v) in float64 (common.cuh:15-19 SiLU), evaluated without overflow:
+    e = exp(-|v|) <= 1, sigmoid(v) = 1 / (1 + e) for v >= 0 and e / (1 + e) for v < 0."""
+    v = np.asarray(v, dtype=np.float64)
+    e = np.exp(-np.abs(v))
+    return v * np.where(v >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
 
 
 def act64(v: np.ndarray, act: int) -> np.ndarray:

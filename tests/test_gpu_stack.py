@@ -185,7 +185,7 @@ def test_llama_stack_blocks_oracle_decode_and_prefill(hip):
                     "gate": fused_gate_up(a, pb["gate"], pb["up"]), "down": packed_linear(b, pb["down"])}
             refs = {nm: (xb if nm == "down" else xa) @ Wd[nm].T for nm in ("q", "k", "v", "o", "down")}
             gv, uv = xa @ Wd["gate"].T, xa @ Wd["up"].T
-            refs["gate"] = gv / (1 + np.exp(-gv)) * uv
+            refs["gate"] = E.silu64(gv) * uv
             for nm, ref in refs.items():
                 got = outs[nm][torch.from_numpy(sel).to(dev)][:, torch.from_numpy(cols[nm]).to(dev)]
                 err = _rel(torch.from_numpy(ref), got.cpu())

@@ -147,3 +147,17 @@ def test_rope64_is_a_complex_rotation():
     assert np.allclose(out[..., :h], z.real, atol=1e-12) and np.allclose(out[..., h:], z.imag, atol=1e-12)
     # angle zero is the identity; norms of each pair are kept
     assert np.array_equal(E.rope64(y, np.ones((M, hd)), np.zeros((M, hd)), hd), y)
+
+
+def test_silu64_is_overflow_free_and_exact():
+    """SiLU v sigmoid(v): equals v / (1 + e^-v) wherever that form does not overflow, satisfies
+    silu(v) - silu(-v) = v (sigmoid(v) + sigmoid(-v) = 1), tends to 0 for large negative v
+    without overflow (exp(-|v|) may underflow to 0, which is exact here), and to v for large
+    positive v."""
+    v = np.linspace(-30.0, 30.0, 2001)
+    np.testing.assert_allclose(E.silu64(v), v / (1.0 + np.exp(-v)), rtol=1e-14, atol=1e-300)
+    np.testing.assert_allclose(E.silu64(v) - E.silu64(-v), v, rtol=1e-13, atol=1e-13)
+    with np.errstate(over="raise", invalid="raise", divide="raise"):
+        big = np.array([-1e4, -800.0, 800.0, 1e4])
+        out = E.silu64(big)
+    assert out[0] == 0.0 and out[1] == 0.0 and out[2] == 800.0 and out[3] == 1e4
