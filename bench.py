@@ -9,6 +9,12 @@ weights, so the 256 MB Infinity Cache cannot serve repeats).  The 96 launches of
 a step are captured once in a HIP graph; `value` is the whole-step throughput in
 algorithmic GB/s (wall clock over K replays, inputs resident in HBM).
 
+Correctness gate (before anything is timed): every launch configuration the run times -- each
+candidate (split_k, rho) of the timed step, the timed graph's own outputs after its warm-up
+replays, every sweep row, the fused modes and the stack's plans -- is checked against the
+oracle's float64 dequant-matmul at the reference's bars (fp16 3e-3, bf16 2e-2); a miss exits
+with status 3 and no result line.  The line records the checks in `correctness_checked`.
+
 Also reported (outside the timed region): per-launch kernel durations from the
 library's dispatch-recorded event timer for the full decode matrix (W2/W3/W4 x
 M in {1,4,8} x the three shapes), the fused QKV / gate-up decode, the M=1024 and
@@ -81,6 +87,84 @@ def randx(torch, M, K, seed, device):
     return torch.randn(M, K, generator=g).half().to(device)
 
 
+class Gate:
+    """Correctness gate: every launch configuration the bench times is first checked against the
+    oracle's float64 dequant-matmul on the same inputs, as the reference benches refuse to time a
+    wrong kernel (Kernel/scripts/bench_gemv.py:21-24, bench_prefill.py:19-22).  Bars: max|y - ref|
+    / max|ref| below 3e-3 for fp16 and 2e-2 for bf16 outputs (Kernel/tests/test_correctness.py:10),
+    both inside the brief's 1e-2 for fp16.  A miss ends the run with exit status 3 and no result
+    line.  Prefill checks compare every 16th output row (the row within its 16-row group rotating),
+    so every 128-row tile of the GEMM is covered."""
+    BAR = {"torch.float16": 3e-3, "torch.bfloat16": 2e-2, "torch.float32": 1e-4}
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.cache = {}
+        self.checks = 0
+        self.worst = {}
+
+    def weight64(self, w):
+        """float64 W-hat of a packed weight (its metadata as stored), cached per weight object."""
+        k = id(w)
+        if k not in self.cache:
+            from oracle import emulator as E
+            W = E.dequant64_fast(w.packed.cpu().numpy(), w.scales.double().cpu().numpy(),
+                                 w.zeros.double().cpu().numpy(), w.bits, w.in_features, w.group_size)
+            self.cache[k] = (w, self.torch.from_numpy(W))
+        return self.cache[k][1]
+
+    def clear(self):
+        self.cache.clear()
+
+    @staticmethod
+    def rows(M):
+        if M <= 64:
+            return None
+        return [16 * i + (i % 16) for i in range(M // 16) if 16 * i + (i % 16) < M]
+
+    def linear64(self, x, w, rows=None, round_w=None, act=None):
+        """x W-hat^T in float64 for the given rows of x; W-hat rounded once to `round_w` (the
+        matrix-core prefill's operand) when given."""
+        torch = self.torch
+        W = self.weight64(w)
+        if round_w is not None:
+            W = W.to(round_w).double()
+        xs = x if rows is None else x[rows]
+        y = xs.double().cpu() @ W.T
+        if act == "silu":
+            from oracle import emulator as E
+            y = torch.from_numpy(E.silu64(y.numpy()))
+        return y
+
+    def check(self, tag, y, ref, rows=None):
+        torch = self.torch
+        yy = (y if rows is None else y[rows]).double().cpu()
+        den = ref.abs().max().item()
+        err = (yy - ref).abs().max().item() / (den + 1e-6)
+        bar = self.BAR[str(y.dtype)]
+        self.checks += 1
+        key = str(y.dtype).replace("torch.", "")
+        self.worst[key] = max(self.worst.get(key, 0.0), err)
+        if not (err < bar and math.isfinite(err)):
+            log(f"CORRECTNESS GATE: {tag}: rel err {err:.3e} >= {bar:.0e}; not timing")
+            raise SystemExit(3)
+
+    def gemv(self, tag, y, x, w, act=None):
+        self.check(tag, y, self.linear64(x, w, act=act))
+
+    def gemm(self, tag, y, x, w):
+        rows = self.rows(x.shape[0])
+        self.check(tag, y, self.linear64(x, w, rows, round_w=x.dtype), rows)
+
+    def record(self):
+        return {"checks": self.checks, "max_rel_err": {k: float(f"{v:.3e}") for k, v in self.worst.items()},
+                "bar": {"fp16": 3e-3, "bf16": 2e-2},
+                "reference": "oracle float64 dequant-matmul (oracle.emulator.dequant64_fast) on the same inputs; "
+                             "every timed (shape, bits, M, split_k, rho) and sweep row checked once before it "
+                             "is timed, the timed step's graph outputs (first and last layer copy) after its "
+                             "warm-up replays; prefill rows sampled one per 16"}
+
+
 def timed_kernels(C, fn, n_launch):
     """Run fn() (which makes n_launch library launches) with the dispatch timer armed."""
     C.timer_start(n_launch + 8)
@@ -113,10 +197,13 @@ def graph_launch_us(torch, fn, n_launch, replays=20):
     return ms * 1e3 / (replays * n_launch)
 
 
-def best_config(torch, C, ops, x, ws, candidates):
-    """Pick (split_k, rho) with the shortest graph-replayed time over the layer copies."""
+def best_config(torch, C, ops, x, ws, candidates, gate, base):
+    """Pick (split_k, rho) with the shortest graph-replayed time over the layer copies; each
+    candidate is checked against the oracle before it is timed."""
     best = None
     for sk, rho in candidates:
+        gate.gemv(f"W{base.bits} M={x.shape[0]} {base.in_features}->{base.out_features} split_k={sk} rho={rho}",
+                  ops.packed_linear(x, ws[0], sk, rho), x, base)
         us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w, sk, rho) for w in ws], len(ws), replays=4)
         if best is None or us < best[0]:
             best = (us, sk, rho)
@@ -134,49 +221,87 @@ def _median_ms(fn, warm=2, runs=5):
     return statistics.median(times) * 1e3
 
 
-def cpu_baseline(torch, weights, xs, gemm_weight, gemm_x):
-    """The reference's CPU path on the host cores (BASELINE.md section 3 protocol): the oracle's
-    restatement of reference.py unpack_codes -> dequantize (reference.py:30-34,58-67) followed by
-    x.float() @ W.T in torch (test_correctness.py:23-31), on the same seeded inputs as the GPU.
-    Two numbers per config: dequant + matmul per call, and the matmul alone on a pre-dequantized
-    fp32 W.  torch runs on every core this process may use; 2 warm-up runs, median of 5."""
+def cpu_baseline(torch, dev, base, xs):
+    """The reference's CPU path on the host cores (BASELINE.md section 3 protocol) on the same seeded
+    inputs as the GPU: the oracle's restatement of reference.py unpack_codes -> dequantize
+    (reference.py:30-34,58-67; unpack by code slot, oracle.reference.unpack_codes_by_slot, then
+    (q - z) s in fp32) followed by x.float() @ W.T (test_correctness.py:23-31), torch on every core
+    this process may use.  Two numbers per config: dequant + matmul per call, and the matmul alone
+    on a pre-dequantized fp32 W.  Configs 1, 2 and 4: 2 warm-up runs, median of 5; configs 3 and 5
+    (5 and 7 weights): 1 warm-up, median of 3, config 5 on one block of the 32 (x 32 for a step)."""
+    import numpy as np
     from oracle import reference as R
     affinity = len(os.sched_getaffinity(0))
     torch.set_num_threads(affinity)
 
     def host(w):
-        return (w.packed.cpu().numpy(), w.scales.float().cpu().numpy(), w.zeros.float().cpu().numpy(), w.bits,
-                w.in_features)
+        return (w.packed.cpu().numpy(), w.scales.float().cpu(), w.zeros.float().cpu(), w.bits, w.in_features)
 
     def dequant(h):
         packed, s, z, bits, K = h
-        return torch.from_numpy(R.dequantize(R.unpack_codes(packed, bits, K), s, z, GS))
+        q = torch.from_numpy(np.ascontiguousarray(R.unpack_codes_by_slot(packed, bits, K)))
+        G = s.shape[1]
+        return ((q.view(q.shape[0], G, GS).float() - z[:, :, None]) * s[:, :, None]).view(q.shape[0], K)
 
+    def row(weights, x, flop_or_bytes, unit, warm=2, runs=5):
+        hs = [host(w) for w in weights]
+        xc = x.float().cpu()
+        dense = [dequant(h) for h in hs]
+        full = _median_ms(lambda: [xc @ dequant(h).T for h in hs], warm, runs)
+        mm = _median_ms(lambda: [xc @ W.T for W in dense], warm, runs)
+        rate = flop_or_bytes / (full * 1e-3)
+        r = {"dequant_matmul_ms": round(full, 3), "matmul_only_ms": round(mm, 3)}
+        if unit == "GB/s":
+            r["GBps"] = round(rate / 1e9, 4)
+        else:
+            r["TFLOPs"] = round(rate / 1e12, 4)
+            r["TFLOPs_matmul_only"] = round(flop_or_bytes / (mm * 1e-3) / 1e12, 4)
+        return r
+
+    res = {}
+    # config 1: W4 GEMV M=1 4096 x 4096 (BASELINE configs[0])
+    w1 = make_weight(torch, 4096, 4096, 4, 0, dev)
+    x1 = randx(torch, 1, 4096, 1, dev)
+    res["config1_w4_gemv_m1_4096x4096"] = row([w1], x1, gemv_bytes(1, 4096, 4096, 4), "GB/s")
     # config 2 (the timed workload): one layer-set of the step, the three W3 GEMVs at M = 1
-    gemv = [(host(w), x.float().cpu()) for w, x in zip(weights, xs)]
-    dense = [dequant(h) for h, _ in gemv]
-    full_ms = _median_ms(lambda: [x @ dequant(h).T for h, x in gemv])
-    mm_ms = _median_ms(lambda: [x @ W.T for (_, x), W in zip(gemv, dense)])
-    nbytes = sum(gemv_bytes(1, w.in_features, w.out_features, w.bits) for w in weights)
-    # config 4 row: the M = 1024 prefill GEMM, W4 4096 x 4096
-    gh, gx = host(gemm_weight), gemm_x.float().cpu()
-    gW = dequant(gh)
-    g_full = _median_ms(lambda: gx @ dequant(gh).T)
-    g_mm = _median_ms(lambda: gx @ gW.T)
-    M, K = gemm_x.shape
-    flops = 2.0 * M * gemm_weight.out_features * K
-    return {"value": round(nbytes / (full_ms * 1e-3) / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+    c2 = [row([w], x, gemv_bytes(1, w.in_features, w.out_features, w.bits), "GB/s") for w, x in zip(base, xs)]
+    full2 = sum(r["dequant_matmul_ms"] for r in c2)
+    nbytes2 = sum(gemv_bytes(1, w.in_features, w.out_features, w.bits) for w in base)
+    res["config2_w3_gemv_m1_layer_set"] = {"dequant_matmul_ms": round(full2, 3),
+                                           "matmul_only_ms": round(sum(r["matmul_only_ms"] for r in c2), 3),
+                                           "GBps": round(nbytes2 / (full2 * 1e-3) / 1e9, 4),
+                                           "per_shape": c2}
+    # config 3: fused QKV (widths by seed) and fused gate-up (W3 2 x 11008) at M = 1
+    qkv_bits = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 3)]
+    qkv = [make_weight(torch, 4096, 4096, b, s + 1, dev) for s, b in enumerate(qkv_bits)]
+    res["config3_fused_qkv_m1"] = row(qkv, x1, sum(gemv_bytes(1, 4096, 4096, b) for b in qkv_bits), "GB/s", 1, 3)
+    gu = [make_weight(torch, 11008, 4096, 3, 4, dev), make_weight(torch, 11008, 4096, 3, 5, dev)]
+    res["config3_fused_gate_up_w3_m1"] = row(gu, x1, 2 * gemv_bytes(1, 4096, 11008, 3), "GB/s", 1, 3)
+    del qkv, gu
+    # config 4: the M = 1024 prefill GEMM, W4 4096 x 4096
+    xg = randx(torch, 1024, 4096, 1, dev)
+    res["config4_w4_gemm_m1024_4096x4096"] = row([w1], xg, 2.0 * 1024 * 4096 * 4096, "TFLOP/s")
+    # config 5: one block of the Llama-2-7B stack at decode (bits of block 0 of the bitmap)
+    bits0 = int(np.random.default_rng(0).choice([2, 3, 4], STACK_BLOCKS)[0])
+    blk = [make_weight(torch, N, K, bits0, j, dev) for j, (_, N, K) in enumerate(STACK_LINEARS)]
+    nb5 = sum(gemv_bytes(1, K, N, bits0) for _, N, K in STACK_LINEARS)
+    hs = [host(w) for w in blk]
+    xh, xi = randx(torch, 1, STACK_H, 1, "cpu").float(), randx(torch, 1, STACK_I, 2, "cpu").float()
+    xin = [xi if K == STACK_I else xh for _, _, K in STACK_LINEARS]
+    full5 = _median_ms(lambda: [x @ dequant(h).T for h, x in zip(hs, xin)], 1, 3)
+    res["config5_stack_one_block_m1"] = {"dequant_matmul_ms": round(full5, 3), "bits": bits0,
+                                         "step_estimate_ms": round(32 * full5, 1),
+                                         "GBps": round(nb5 / (full5 * 1e-3) / 1e9, 4)}
+    del blk, hs
+    value = res["config2_w3_gemv_m1_layer_set"]["GBps"]
+    return {"value": value, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
             "cpu_count": os.cpu_count(), "affinity": affinity, "torch_threads": torch.get_num_threads(),
-            "gemv_w3_m1_layer_set": {"dequant_matmul_ms": round(full_ms, 2), "matmul_only_ms": round(mm_ms, 3),
-                                     "GBps": round(nbytes / (full_ms * 1e-3) / 1e9, 4)},
-            "gemm_w4_m1024_4096x4096": {"dequant_matmul_ms": round(g_full, 2), "matmul_only_ms": round(g_mm, 2),
-                                        "TFLOPs": round(flops / (g_full * 1e-3) / 1e12, 4),
-                                        "TFLOPs_matmul_only": round(flops / (g_mm * 1e-3) / 1e12, 4)},
-            "sample": "config 2: one layer-set of the timed step (W3 GEMVs 4096x4096, 4096->11008, 11008->4096 at "
-                      "M=1); config 4: the W4 M=1024 4096x4096 GEMM.  oracle.reference unpack_codes + dequantize "
-                      "(numpy) then torch fp32 matmul on all affinity cores; 2 warm-up runs, median of 5; value = "
-                      "config 2 algorithmic bytes / dequant+matmul time"}
+            **res,
+            "sample": "value = config 2 (the timed workload's metric) on one layer-set of the step (W3 GEMVs "
+                      "4096x4096, 4096->11008, 11008->4096 at M=1): algorithmic bytes / dequant+matmul time.  "
+                      "Rows for configs 1, 3, 4 and one block of config 5.  The oracle's restatement of "
+                      "reference.py (unpack by code slot in torch int64 ops, fp32 dequant, torch fp32 matmul), "
+                      "not reference.py itself; all on the affinity cores"}
 
 
 def main():
@@ -193,9 +318,11 @@ def main():
     ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm"),
                     help="run the fixed launch sequence of a counter pass and exit: gemv (default: the "
                          "W3 decode GEMV after a calibration copy) or gemm (the M=1024 W4 prefill GEMM)")
-    ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
-                    help="reduce a rocprofv3 kernel trace of a bench run to the markdown tables under "
-                         "profiles/ (the default command's timed step, or the batched sweep) and exit")
+    ap.add_argument("--trace-summary", nargs="+", metavar="FILE",
+                    help="KERNEL_TRACE_CSV BENCH_JSON [UNTRACED_BENCH_JSON]: reduce a rocprofv3 kernel trace of a "
+                         "bench run to the markdown tables under profiles/ (the default command's timed step, or "
+                         "the batched sweep), with the tracer's inflation against an untraced run of the same "
+                         "command when given, and exit")
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(*args.trace_summary, steps=args.steps, warmup=args.warmup)
@@ -231,26 +358,35 @@ def main():
     pool_gb = sum(w.packed.numel() * 4 + w.scales.numel() * 4 for lw in layers for w in lw) / 1e9
     log(f"weights: {LAYERS} layers x 3 shapes, {pool_gb:.2f} GB packed")
 
+    gate = Gate(torch)
     cand = [(1, 0), (1, 1), (1, 2), (2, 0), (None, 1)]
-    cfg = [best_config(torch, C, ops, xs[s], [lw[s] for lw in layers], cand) for s in range(3)]
+    cfg = [best_config(torch, C, ops, xs[s], [lw[s] for lw in layers], cand, gate, base[s]) for s in range(3)]
     log(f"per-shape (split_k, rho): {cfg}")
 
-    def step_eager():
-        for lw in layers:
+    def step_eager(keep=None):
+        for li, lw in enumerate(layers):
             for s in range(3):
-                ops.packed_linear(xs[s], lw[s], cfg[s][0], cfg[s][1])
+                y = ops.packed_linear(xs[s], lw[s], cfg[s][0], cfg[s][1])
+                if keep is not None and li in (0, LAYERS - 1):
+                    keep.append((li, s, y))
 
     step_eager()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
+    graph_outs = []
     with torch.cuda.graph(graph):
-        step_eager()
+        step_eager(graph_outs)
     torch.cuda.synchronize()
 
     step_bytes = LAYERS * sum(gemv_bytes(1, K, N, bits) for K, N in SHAPES)
     for _ in range(args.warmup):
         graph.replay()
     torch.cuda.synchronize()
+    # the graph that is timed: its outputs after the warm-up replays, against the oracle
+    for li, s, y in graph_outs:
+        K, N = SHAPES[s]
+        gate.gemv(f"timed step graph, layer {li}, W{bits} M=1 {K}->{N} (split_k, rho)={cfg[s]}", y, xs[s], base[s])
+    log(f"correctness gate: timed step passed ({gate.checks} checks)")
     t0 = time.perf_counter()
     for _ in range(args.steps):
         graph.replay()
@@ -276,10 +412,13 @@ def main():
     achieved = step_bytes / (total_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                "achieved_step": round(value, 1), "frac_step": round(value / HBM_PEAK_GBS, 4),
                 "kernel": "gemv_stream_kernel<GEMV, 3, 1> (W3 decode GEMV, M=1)",
                 "bytes_per_launch_avg": round(step_bytes / (3 * LAYERS)),
                 "avg_launch_us": round(total_ms * 1e3 / (3 * LAYERS), 3), "per_shape": per_shape,
-                "timing": "HIP events on the launch stream around graph replays of 32 launches per shape"}
+                "timing": "HIP events on the launch stream around graph replays of 32 launches per shape; "
+                          "achieved_step / frac_step: the step's algorithmic bytes over ms_per_step (wall clock "
+                          "of the timed replays, gaps between kernels included)"}
     log(f"roofline: {achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of HBM peak; {per_shape}")
 
     out = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -290,21 +429,22 @@ def main():
                       "shapes_KN": SHAPES, "layers": LAYERS, "weight_pool_GB": round(pool_gb, 3)},
            "roofline": roofline}
 
-    del graph
+    del graph, graph_outs
+    gate.clear()
     if not args.quick:
         todo = {w.strip() for w in args.sweeps.split(",") if w.strip()}
         if "gemv" in todo:
-            out["gemv_sweep"] = gemv_sweep(torch, C, ops, dev)
+            out["gemv_sweep"] = gemv_sweep(torch, C, ops, dev, gate)
         if "batched" in todo:
-            out["batched"] = batched_sweep(torch, C, ops, dev)
+            out["batched"] = batched_sweep(torch, C, ops, dev, gate)
         if "dtypes" in todo:
-            out["dtypes"] = dtype_sweep(torch, C, ops, dev)
+            out["dtypes"] = dtype_sweep(torch, C, ops, dev, gate)
         if "fused" in todo:
-            out["fused"] = fused_sweep(torch, C, ops, dev)
+            out["fused"] = fused_sweep(torch, C, ops, dev, gate)
         if "gemm" in todo:
-            out["gemm"] = gemm_sweep(torch, C, ops, dev)
+            out["gemm"] = gemm_sweep(torch, C, ops, dev, gate)
         if "stack" in todo:
-            out["llama2_7b_stack"] = stack_sweep(torch, C, ops, dev)
+            out["llama2_7b_stack"] = stack_sweep(torch, C, ops, dev, gate)
         if "model" in todo:
             try:
                 out["llama2_7b_model"] = model_sweep(torch, dev)
@@ -314,14 +454,14 @@ def main():
                 torch.cuda.empty_cache()
         if "producer" in todo:
             out["producer"] = producer_sweep(torch, C, dev)
+    out["correctness_checked"] = gate.record()
     if not args.no_cpu:
         log("cpu baseline ...")
-        gw = make_weight(torch, 4096, 4096, 4, 0, dev)
-        out["cpu_baseline"] = cpu_baseline(torch, base, xs, gw, randx(torch, 1024, 4096, 1, dev))
+        out["cpu_baseline"] = cpu_baseline(torch, dev, base, xs)
     print(json.dumps(out), flush=True)
 
 
-def trace_summary(trace_csv, bench_json, steps, warmup):
+def trace_summary(trace_csv, bench_json, untraced_json=None, steps=50, warmup=5):
     """Markdown tables of a rocprofv3 kernel trace of a bench run (needs no GPU).  With a
     `batched` sweep in the bench line: per sweep row, its 6 x copies consecutive bstream
     dispatches (eager run, warm replay, 4 timed replays; one kernel, grid and block checked) and
@@ -351,23 +491,33 @@ def trace_summary(trace_csv, bench_json, steps, warmup):
             i += 6 * j["copies"]
         assert i == len(b), (i, len(b))
         return
-    n = (steps + warmup) * 96
-    for i in range(len(rows) - n + 1):
+    # the timed replays: the last run of steps x 96 decode launches whose (kernel, grid, block)
+    # keys repeat with period 3 (the eager run and warm-up replays before it have the same keys;
+    # the roofline's per-shape graphs after it do not)
+    n = steps * 96
+    for i in range(len(rows) - n, -1, -1):
         seg = rows[i:i + n]
         if all("gemv_stream_kernel" in r["Kernel_Name"] for r in seg) and \
                 all(key(seg[j]) == key(seg[j % 3]) for j in range(n)):
             break
     else:
         raise SystemExit("timed region not found")
-    timed = seg[warmup * 96:]
+    timed = seg
     d = [dur(r) for r in timed]
     kms = sum(d) / steps / 1e6
     span = (int(timed[-1]["End_Timestamp"]) - int(timed[0]["Start_Timestamp"])) / steps / 1e6
     step_bytes = line["roofline"]["bytes_per_launch_avg"] * 96
-    print(f"traced run: ms_per_step {line['ms_per_step']}, kernel time per step {kms:.4f} ms, dispatch span per "
-          f"step {span:.4f} ms, value {line['value']}, frac (events) {line['roofline']['frac']}, frac (trace) "
+    print(f"traced run: ms_per_step {line['ms_per_step']}, kernel time per step {kms:.4f} ms "
+          f"({'<=' if kms <= line['ms_per_step'] else '>'} the traced ms_per_step), dispatch span per step "
+          f"{span:.4f} ms, value {line['value']}, frac (events) {line['roofline']['frac']}, frac (trace) "
           f"{step_bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS:.4f}, avg launch us (events) "
           f"{line['roofline']['avg_launch_us']}, (trace) {sum(d) / len(d) / 1e3:.3f}")
+    if untraced_json:
+        u = json.loads(open(untraced_json).read().strip().splitlines()[-1])
+        print(f"untraced run of the same command: ms_per_step {u['ms_per_step']}, frac (events) "
+              f"{u['roofline']['frac']}, frac_step {u['roofline'].get('frac_step')}; tracer inflation of the "
+              f"step (traced / untraced ms_per_step) {line['ms_per_step'] / u['ms_per_step']:.3f}; trace kernel "
+              f"time per step / untraced ms_per_step {kms / u['ms_per_step']:.3f}")
     print("| shape (K -> N) | kernel | grid (threads) | block | launches | avg ns | min ns | max ns |")
     print("|---|---|---|---|---|---|---|---|")
     for sh, (K, N) in enumerate(SHAPES):
@@ -436,9 +586,10 @@ def pmc_workload_gemm(torch, ops, dev):
     log("pmc gemm workload done")
 
 
-def gemv_sweep(torch, C, ops, dev):
+def gemv_sweep(torch, C, ops, dev, gate):
     """W2/W3/W4 x M in {1,4,8,16} x shapes: µs per call (graph-replayed, a split call counts its
-    combine launch) over >= 1 GiB of distinct weight copies per shape."""
+    combine launch) over >= 1 GiB of distinct weight copies per shape; every candidate plan checked
+    against the oracle before it is timed."""
     rows = []
     for bits in (4, 3, 2):
         for s, (K, N) in enumerate(SHAPES):
@@ -448,6 +599,8 @@ def gemv_sweep(torch, C, ops, dev):
                 x = randx(torch, M, K, 1, dev)
                 best = None
                 for sk, rho in [(1, 1), (2, 1), (None, 1)]:
+                    gate.gemv(f"gemv sweep W{bits} M={M} {K}->{N} split_k={sk} rho={rho}",
+                              ops.packed_linear(x, ws[0], sk, rho), x, base)
                     us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w, sk, rho) for w in ws], len(ws),
                                          replays=4)
                     if best is None or us < best[0]:
@@ -459,11 +612,12 @@ def gemv_sweep(torch, C, ops, dev):
                              "copies": len(ws)})
                 log(f"gemv W{bits} M={M} K={K} N={N}: {us:.2f} us {gbs:.0f} GB/s ({len(ws)} copies)")
             del ws, base
+            gate.clear()
             torch.cuda.empty_cache()
     return rows
 
 
-def batched_sweep(torch, C, ops, dev):
+def batched_sweep(torch, C, ops, dev, gate):
     """Batched decode at the library's own plan (split_k=None, no candidate search): W3 and W4,
     M in {4, 8, 16} over the three shapes, µs per call graph-replayed over >= 1 GiB of weight
     copies, with the launch the plan makes (kernel family, K splits, workgroups, launches per
@@ -477,6 +631,7 @@ def batched_sweep(torch, C, ops, dev):
                 x = randx(torch, M, K, 1, dev)
                 fam, splits, grid, threads, lds, launches = C.decode_plan(torch.float16, M, K, GS, N, bits, "gemv",
                                                                           1, 1)
+                gate.gemv(f"batched W{bits} M={M} {K}->{N}", ops.packed_linear(x, ws[0]), x, base)
                 us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w) for w in ws], len(ws), replays=4)
                 gbs = gemv_bytes(M, K, N, bits) / (us * 1e-6) / 1e9
                 rows.append({"bits": bits, "M": M, "K": K, "N": N, "us": round(us, 3), "GBps": round(gbs, 1),
@@ -484,11 +639,12 @@ def batched_sweep(torch, C, ops, dev):
                              "workgroups": grid, "threads": threads, "launches": launches, "copies": len(ws)})
                 log(f"batched W{bits} M={M} K={K} N={N}: {us:.2f} us ({fam}, P={splits}, {grid} workgroups)")
             del ws, base
+            gate.clear()
             torch.cuda.empty_cache()
     return rows
 
 
-def dtype_sweep(torch, C, ops, dev):
+def dtype_sweep(torch, C, ops, dev, gate):
     """fp16 against bf16 activations (scales, zeros and outputs of the same dtype, the same codes):
     W3 decode at M = 1 and 8 over the three shapes, graph-replayed over >= 1 GiB of weight copies,
     and the W3 prefill GEMM at M = 1024, with the kernel family each decode plan takes."""
@@ -503,6 +659,12 @@ def dtype_sweep(torch, C, ops, dev):
                 k = n if M <= 16 else 4
                 ws = [replace(clone_weight(base), scales=base.scales.to(dt), zeros=base.zeros.to(dt)) for _ in range(k)]
                 x = randx(torch, M, K, 1, dev).to(dt)
+                y = ops.packed_linear(x, ws[0])
+                if M <= 16:
+                    gate.gemv(f"dtypes {tag} W3 M={M} {K}->{N}", y, x, ws[0])
+                else:
+                    gate.gemm(f"dtypes {tag} W3 M={M} {K}->{N}", y, x, ws[0])
+                del y
                 us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w) for w in ws], len(ws), replays=4)
                 r[tag + "_us"] = round(us, 3)
                 if M <= 16:
@@ -511,6 +673,7 @@ def dtype_sweep(torch, C, ops, dev):
                 else:
                     r[tag + "_TFLOPs"] = round(2 * M * N * K / (us * 1e-6) / 1e12, 1)
                 del ws
+                gate.clear()
                 torch.cuda.empty_cache()
             log(f"dtypes W3 M={M} K={K} N={N}: fp16 {r['fp16_us']:.2f} us, bf16 {r['bf16_us']:.2f} us")
             rows.append(r)
@@ -518,7 +681,7 @@ def dtype_sweep(torch, C, ops, dev):
     return rows
 
 
-def fused_sweep(torch, C, ops, dev):
+def fused_sweep(torch, C, ops, dev, gate):
     """Config 3 at M = 1: fused QKV (widths by seed) and fused gate-up (W3, 2 x 11008), µs per call
     graph-replayed over >= 1 GiB of weight copies."""
     import numpy as np
@@ -528,6 +691,8 @@ def fused_sweep(torch, C, ops, dev):
     n = copies_for(sum(weight_bytes(w) for w in first))
     sets = [first] + [[clone_weight(w) for w in first] for _ in range(n - 1)]
     x = randx(torch, 1, 4096, 1, dev)
+    for name, y, w in zip("qkv", ops.fused_qkv(x, *first), first):
+        gate.gemv(f"fused QKV ({name}, W{w.bits}) M=1", y, x, w)
     us = graph_launch_us(torch, lambda: [ops.fused_qkv(x, *ws) for ws in sets], len(sets), replays=4)
     nbytes = sum(gemv_bytes(1, 4096, 4096, b) for b in qkv_bits) - 2 * 4096 * 2
     res["qkv"] = {"bits": qkv_bits, "K": 4096, "N": [4096] * 3, "us": round(us, 3),
@@ -537,6 +702,9 @@ def fused_sweep(torch, C, ops, dev):
     u0 = make_weight(torch, 11008, 4096, 3, 5, dev)
     n = copies_for(weight_bytes(g0) + weight_bytes(u0))
     pairs = [(g0, u0)] + [(clone_weight(g0), clone_weight(u0)) for _ in range(n - 1)]
+    gate.check("fused gate-up W3 M=1", ops.fused_gate_up(x, g0, u0),
+               gate.linear64(x, g0, act="silu") * gate.linear64(x, u0))
+    gate.clear()
     us = graph_launch_us(torch, lambda: [ops.fused_gate_up(x, g, u) for g, u in pairs], len(pairs), replays=4)
     nbytes = 2 * gemv_bytes(1, 4096, 11008, 3) - 4096 * 2 - 11008 * 2
     res["gate_up"] = {"bits": 3, "K": 4096, "N": [11008, 11008], "us": round(us, 3),
@@ -570,9 +738,10 @@ def producer_sweep(torch, C, dev):
     return rows
 
 
-def gemm_sweep(torch, C, ops, dev):
+def gemm_sweep(torch, C, ops, dev, gate):
     """Config 4: the prefill GEMM at M in {1024, 2048}, µs per call graph-replayed over 4 weight
-    copies (the weights are read once per 128-row tile either way; the activations dominate)."""
+    copies (the weights are read once per 128-row tile either way; the activations dominate);
+    every row checked against the oracle before it is timed."""
     rows = []
     for M in (1024, 2048):
         for K, N in SHAPES:
@@ -580,6 +749,8 @@ def gemm_sweep(torch, C, ops, dev):
             for bits in (4, 3, 2):
                 ws = [make_weight(torch, N, K, bits, 0, dev)]
                 ws += [clone_weight(ws[0]) for _ in range(3)]
+                gate.gemm(f"gemm W{bits} M={M} {K}->{N}", ops.packed_linear(x, ws[0]), x, ws[0])
+                gate.clear()
                 us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w) for w in ws], len(ws), replays=5)
                 tfs = 2.0 * M * N * K / (us * 1e-6) / 1e12
                 rows.append({"M": M, "K": K, "N": N, "bits": bits, "us": round(us, 2), "TFLOPs": round(tfs, 1),
@@ -624,7 +795,32 @@ def stack_energy(torch, gr, gr16, seconds=4.0):
         sampler.close()
 
 
-def stack_sweep(torch, C, ops, dev, steps=20):
+def stack_check(torch, ops, gate, blocks, bitmap, xh, xi, Xh, Xi):
+    """The stack's launch configurations against the oracle: the first block of each bit width
+    (every (shape, mode, bits) plan a step makes), at decode and at the prefill rows."""
+    firsts = sorted({b: i for i, b in reversed(list(enumerate(bitmap)))}.values())
+    for i in firsts:
+        b = blocks[i]
+        tag = f"stack block {i} (W{bitmap[i]})"
+        for nm, y in zip("qkv", ops.fused_qkv(xh, b["q"], b["k"], b["v"])):
+            gate.gemv(f"{tag} decode fused QKV {nm}", y, xh, b[nm])
+        gate.gemv(f"{tag} decode o", ops.packed_linear(xh, b["o"]), xh, b["o"])
+        gate.check(f"{tag} decode fused gate-up", ops.fused_gate_up(xh, b["gate"], b["up"]),
+                   gate.linear64(xh, b["gate"], act="silu") * gate.linear64(xh, b["up"]))
+        gate.gemv(f"{tag} decode down", ops.packed_linear(xi, b["down"]), xi, b["down"])
+        for nm, y in zip("qkv", ops.fused_qkv(Xh, b["q"], b["k"], b["v"])):
+            gate.gemm(f"{tag} prefill QKV {nm}", y, Xh, b[nm])
+        gate.gemm(f"{tag} prefill o", ops.packed_linear(Xh, b["o"]), Xh, b["o"])
+        rows = gate.rows(Xh.shape[0])
+        ref = (gate.linear64(Xh, b["gate"], rows, round_w=Xh.dtype, act="silu")
+               * gate.linear64(Xh, b["up"], rows, round_w=Xh.dtype))
+        gate.check(f"{tag} prefill gate-up", ops.fused_gate_up(Xh, b["gate"], b["up"]), ref, rows)
+        gate.gemm(f"{tag} prefill down", ops.packed_linear(Xi, b["down"]), Xi, b["down"])
+        gate.clear()
+    log(f"correctness gate: stack blocks {firsts} passed")
+
+
+def stack_sweep(torch, C, ops, dev, gate, steps=20):
     """Config 5: the Llama-2-7B linear stack at decode (M = 1), 32 blocks, bits per block
     from default_rng(0).choice([2, 3, 4], 32); block i, linear j weights from a device
     generator seeded 1000*i + j (quantized and packed on the GPU by the HIP producer).  A step is, per block,
@@ -653,6 +849,8 @@ def stack_sweep(torch, C, ops, dev, steps=20):
     torch.cuda.synchronize()
     xh = randx(torch, 1, STACK_H, 1, dev)
     xi = randx(torch, 1, STACK_I, 2, dev)
+    stack_check(torch, ops, gate, blocks, bitmap, xh, xi, randx(torch, PREFILL_M, STACK_H, 3, dev),
+                randx(torch, PREFILL_M, STACK_I, 4, dev))
     packed_gb = sum(w.packed.numel() * 4 + w.scales.numel() * 4 for b in blocks for w in b.values()) / 1e9
     step_bytes = sum(gemv_bytes(1, K, N, b["q"].bits) for b in blocks for _, N, K in STACK_LINEARS)
 

@@ -519,7 +519,7 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divGS = make_fastdiv((uint32_t)(A.gs / 32));
         L.family = CBK_KERNEL_STREAM;
-        L.f = gemv_stream_kernel_for(mode, A.src[0].bits, mixed, sp.mb, sp.rpw, dtype == CBK_BF16);
+        L.f = gemv_stream_kernel_for(mode, A.bits[0], mixed, sp.mb, sp.rpw, dtype == CBK_BF16);
         L.grid = sp.grid;
         L.block = 64 * sp.ks * sp.rw;
         L.lds = sp.lds;
@@ -537,7 +537,7 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divG = make_fastdiv((uint32_t)(A.gs / 128));
         L.family = CBK_KERNEL_BSTREAM;
-        L.f = gemv_bstream_kernel_for(mode, A.src[0].bits, mixed, bp.bsu, dtype == CBK_BF16);
+        L.f = gemv_bstream_kernel_for(mode, A.bits[0], mixed, bp.bsu, dtype == CBK_BF16);
         L.grid = bp.grid;
         L.block = 64 * bp.ks * bp.rw;
         L.lds = bp.lds;
@@ -612,8 +612,7 @@ void set_proj(GemvArgs& A, int i, const int32_t* w, const void* s, const void* z
     S.z = z;
     S.n = (int)n;
     S.wpr = (int)(ceil_div(K, 32) * bits);
-    S.bits = bits;
-    S.pad_ = 0;
+    A.bits[i] = bits;
     Dst& D = A.dst[i];
     D.y = out;
     D.bias = b;
@@ -625,6 +624,7 @@ void set_proj(GemvArgs& A, int i, const int32_t* w, const void* s, const void* z
 void repeat_proj0(GemvArgs& A) {
     A.src[1] = A.src[2] = A.src[0];
     A.dst[1] = A.dst[2] = A.dst[0];
+    A.bits[1] = A.bits[2] = A.bits[0];
 }
 
 GemvArgs base_args(const void* x, int64_t M, int64_t K, int gs) {
@@ -846,6 +846,7 @@ int cbk_fused_gate_up(const void* x, int dtype, int64_t M, int64_t K, const int3
     set_proj(A, 1, wu, su, zu, nullptr, out, N, bits, K);
     A.src[2] = A.src[0];
     A.dst[2] = A.dst[0];
+    A.bits[2] = A.bits[0];
     A.V = (int)(2 * N);
     return run_decode(A, dtype, CBK_MODE_GATEUP, false, split_k, rho, partial, device, stream);
 }

@@ -104,7 +104,7 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
 // A decode call has up to three projections (plain GEMV: one; gate-up: gate and up;
 // QKV: q, k and v).  Each has a weight side, which the K loop of every kernel streams,
 // and an output side, which only the finish stage writes; the two are kept apart so
-// that the finish stage (finish_pair) sees nothing of the weights and the K loops
+// that the finish stage (finish) sees nothing of the weights and the K loops
 // nothing of the outputs.
 struct Src {
     const uint32_t* w;   // packed codes [n, wpr]
@@ -112,8 +112,6 @@ struct Src {
     const void* z;       // zeros  [n, G]
     int n;               // rows
     int wpr;             // 32-bit words per row = C * bits
-    int bits;            // 2 / 3 / 4
-    int pad_;
 };
 
 struct Dst {
@@ -123,29 +121,32 @@ struct Dst {
     int pad_;
 };
 
+// The fields every decode kernel reads at its start come first and densely, with no
+// padding and nothing a kernel leaves unused between them: the compiler merges
+// neighbouring kernel-argument loads into wide scalar loads, and an unused word inside
+// one lets it recycle that register for a later load, which then has to wait for the
+// first -- a serialised memory round trip at the start of every launch.
 struct GemvArgs {
     Src src[3];
-    Dst dst[3];
     const void* x;         // [M, K]
     float* partial;        // [P, M, V] fp32 when P > 1
+    // K-split calls combining in the dispatch: one arrival counter per row block (zero
+    // between calls).  nullptr: a combine launch adds the partials.
+    uint32_t* split_cnt;
+    int M, K, V, C;        // batch rows, in_features, virtual rows, 32-code chunks per row
+    int G, gs, P, act;     // groups per row, group size, K splits, activation (GEMV mode)
+    int st_ks;             // streaming kernels: K slices per job (waves per row group)
+    int st_rw;             // streaming kernels: row groups per workgroup
+    int st_xvec;           // x is 16-byte aligned with K % 8 == 0 (vector activation loads)
+    int ntiles;            // fp32 matrix-core kernel: 16-row tiles
+    FastDiv divP, divRW, divGS, divG, divT;   // by P, st_rw, gs / 32, gs / 128, ntiles
+    Dst dst[3];
     const float* rope_cos; // [M, head_dim] or nullptr
     const float* rope_sin;
-    int M, K, V;           // batch rows, in_features, virtual rows
-    int C, G, gs;          // 32-code chunks per row, groups per row, group size
-    int P, act;            // K splits, activation (GEMV mode)
     int head_dim, perm_hd;
-    int ntiles, mtiles, jobs;  // fp32 matrix-core kernel: 16-row tiles, 16-row batch tiles, jobs
+    int mtiles, jobs;      // fp32 matrix-core kernel: 16-row batch tiles, jobs
+    int bits[3];           // code width of each projection
     int pad_;
-    FastDiv divP, divT, divG;  // by P, ntiles and gs / 128
-    // batch-1 streaming kernel (gemv_stream.hip)
-    int st_ks;             // K slices per job (waves per row group)
-    int st_rw;             // row groups per workgroup (one wave's rows each)
-    int st_xvec;           // x is 16-byte aligned with K % 8 == 0 (vector activation loads)
-    int pad2_;
-    FastDiv divRW, divGS;             // by st_rw and gs / 32
-    // streaming kernels with P > 1: one arrival counter per row block (zero between
-    // calls); the splits combine inside the dispatch.  nullptr: a reduce launch combines.
-    uint32_t* split_cnt;
 };
 
 // ---------------------------------------------------------------- projection views
@@ -170,9 +171,11 @@ __device__ __forceinline__ Src src_of(const GemvArgs& A, int p) {
     r.z = pick3(p, A.src[0].z, A.src[1].z, A.src[2].z);
     r.n = pick3(p, A.src[0].n, A.src[1].n, A.src[2].n);
     r.wpr = pick3(p, A.src[0].wpr, A.src[1].wpr, A.src[2].wpr);
-    r.bits = pick3(p, A.src[0].bits, A.src[1].bits, A.src[2].bits);
-    r.pad_ = 0;
     return r;
+}
+
+__device__ __forceinline__ int bits_of(const GemvArgs& A, int p) {
+    return pick3(p, A.bits[0], A.bits[1], A.bits[2]);
 }
 
 __device__ __forceinline__ Dst dst_of(const GemvArgs& A, int p) {
@@ -201,17 +204,20 @@ __device__ __forceinline__ void vmap(const GemvArgs& A, int v, int& proj, int& r
 }
 
 // ---------------------------------------------------------------- finish stage
-// Every decode kernel ends here.  Outputs are finished per pair of virtual rows
-// (v0, v0 + 1), v0 even, of one batch row b, from the two rows' fp32 K sums before
-// bias -- the unit all three modes share:
-//  * gate-up: the pair is (gate n, up n), v0 = 2n, and gives the one output
-//    silu(g) * u (the fused module has no bias);
-//  * QKV with RoPE: Q and K rows are stored pair-interleaved per head, so the pair
-//    holds the original rows (h hd + d, h hd + d + hd/2) that the rotation mixes --
-//    both outputs come from one thread, each row's bias read once;
-//  * plain rows, and QKV without RoPE: two independent outputs (act(y + bias) for a
-//    plain GEMV; Q and K rows still go back to their original order).
-// `two` is false when v0 + 1 is past V (an odd V).
+// Every decode kernel ends here, finishing outputs from fp32 K sums taken before bias.
+// The unit of work is what a mode's outputs depend on:
+//  * plain GEMV: one row, act(y + bias) -- rows are independent;
+//  * gate-up: the pair of virtual rows (2n, 2n + 1) = (gate n, up n), which gives the one
+//    output silu(g) * u (the fused module has no bias);
+//  * QKV: the pair (v0, v0 + 1), v0 even.  With RoPE, Q and K rows are stored
+//    pair-interleaved per head, so the pair holds the original rows
+//    (h hd + d, h hd + d + hd/2) that the rotation mixes -- both outputs come from one
+//    thread, each row's bias read once.  Without RoPE the two rows are finished one after
+//    the other (Q and K rows still go back to their original order).
+// A unit is FINISH_ROWS<MODE> consecutive virtual rows; `two` is false when the second row
+// of a pair is past V (an odd V).
+template <int MODE>
+constexpr int FINISH_ROWS = MODE == MODE_GEMV ? 1 : 2;
 
 // One QKV row with no rotation: bias, then the store at its original position.
 template <int DT>
@@ -224,18 +230,13 @@ __device__ __forceinline__ void qkv_plain_row(const GemvArgs& A, int b, int v, f
 }
 
 template <int DT, int MODE>
-__device__ __forceinline__ void finish_pair(const GemvArgs& A, int b, int v0, float y0, float y1, bool two) {
+__device__ __forceinline__ void finish(const GemvArgs& A, int b, int v0, float y0, float y1, bool two) {
     if constexpr (MODE == MODE_GATEUP) {
         store_f<DT>(A.dst[0].y, (long)b * A.dst[0].ld + (v0 >> 1), silu(y0) * y1);
     } else if constexpr (MODE == MODE_GEMV) {
         const void* bias = A.dst[0].bias;
-        if (bias) {
-            y0 += load_f<DT>(bias, v0);
-            if (two) y1 += load_f<DT>(bias, v0 + 1);
-        }
-        const long o = (long)b * A.dst[0].ld + v0;
-        store_f<DT>(A.dst[0].y, o, apply_act(y0, A.act));
-        if (two) store_f<DT>(A.dst[0].y, o + 1, apply_act(y1, A.act));
+        if (bias) y0 += load_f<DT>(bias, v0);
+        store_f<DT>(A.dst[0].y, (long)b * A.dst[0].ld + v0, apply_act(y0, A.act));
     } else {
         int p, r;
         vmap<MODE_QKV>(A, v0, p, r);
@@ -281,8 +282,9 @@ __device__ __forceinline__ float partial_get(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// A split's sums of the pair (v0, v0 + 1) of batch row b into the partial buffer.
-__device__ __forceinline__ void put_pair(const GemvArgs& A, int p, int b, int v0, float y0, float y1, bool two) {
+// A split's sums of a finish unit (v0, and v0 + 1 when `two`) of batch row b into the
+// partial buffer.
+__device__ __forceinline__ void put_unit(const GemvArgs& A, int p, int b, int v0, float y0, float y1, bool two) {
     float* row = A.partial + ((long)p * A.M + b) * A.V;
     partial_put(row + v0, y0);
     if (two) partial_put(row + v0 + 1, y1);
@@ -305,11 +307,11 @@ __device__ __forceinline__ bool split_arrive(const GemvArgs& A, int blk, int* fl
     return *flag != 0;
 }
 
-// The pair (v0, v0 + 1) of batch row b summed over splits 0 .. P - 1 in that order,
-// then finished.
+// The finish unit starting at v0 of batch row b summed over splits 0 .. P - 1 in that
+// order, then finished.
 template <int DT, int MODE>
 __device__ __forceinline__ void finish_from_partials(const GemvArgs& A, int b, int v0) {
-    const bool two = v0 + 1 < A.V;
+    const bool two = FINISH_ROWS<MODE> == 2 && v0 + 1 < A.V;
     const long stride = (long)A.M * A.V;
     const float* q = A.partial + (long)b * A.V + v0;
     float y0 = 0.f, y1 = 0.f;
@@ -317,16 +319,17 @@ __device__ __forceinline__ void finish_from_partials(const GemvArgs& A, int b, i
         y0 += partial_get(q);
         if (two) y1 += partial_get(q + 1);
     }
-    finish_pair<DT, MODE>(A, b, v0, y0, y1, two);
+    finish<DT, MODE>(A, b, v0, y0, y1, two);
 }
 
-// The combining workgroup's finish: the pairs of rows [vbase, vbase + RB) (vbase and
-// RB even) of every batch row, over `nthr` threads.
+// The combining workgroup's finish: the units of rows [vbase, vbase + RB) (vbase and RB
+// even) of every batch row, over `nthr` threads.
 template <int DT, int MODE>
 __device__ __forceinline__ void split_finish(const GemvArgs& A, int vbase, int RB, int nthr) {
-    const int np = RB >> 1;
-    for (int t = threadIdx.x; t < A.M * np; t += nthr) {
-        const int b = t / np, v0 = vbase + 2 * (t - b * np);
+    constexpr int U = FINISH_ROWS<MODE>;
+    const int nu = RB / U;
+    for (int t = threadIdx.x; t < A.M * nu; t += nthr) {
+        const int b = t / nu, v0 = vbase + U * (t - b * nu);
         if (v0 < A.V) finish_from_partials<DT, MODE>(A, b, v0);
     }
 }

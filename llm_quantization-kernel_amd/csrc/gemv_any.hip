@@ -25,9 +25,10 @@
 // so the lane's eight MFMAs cover the chunk's 32 codes.  Group sizes are multiples of
 // 32, so a chunk lies in one group and a lane needs one (scale, zero) per chunk.
 // D's lane (j, kq) register r holds batch row 4 kq + r of virtual row j.  The waves'
-// tiles meet in LDS and are added in wave order; then a row pair per thread is
-// finished (finish_pair), or with P > 1 the fp32 partials are stored and the last split
-// of the block combines them in the dispatch (split_arrive), or a combine launch does.
+// tiles meet in LDS and are added in wave order; then a finish unit (a row, or a row pair
+// in the fused modes) per thread is finished (finish), or with P > 1 the fp32 partials
+// are stored and the last split of the block combines them in the dispatch
+// (split_arrive), or a combine launch does.
 #include "cbk_device.hpp"
 #include "cbk_kernels.hpp"
 
@@ -119,7 +120,7 @@ __global__ void __launch_bounds__(ANY_MAX_THREADS) gemv_any_kernel(const GemvArg
     vmap<MODE>(A, vin ? v : 0, proj, r);
     const Src S = src_of(A, proj);
     const uint32_t* wrow = S.w + (long)r * S.wpr;
-    const int bits = S.bits;
+    const int bits = bits_of(A, proj);
     const int ob = 8 * kq * bits;                   // bit offset of the lane's codes in a chunk
     const int wi = ob >> 5, sh = ob & 31;
     const bool two_words = sh + 8 * bits > 32;      // W3, kq = 1 and 2
@@ -159,40 +160,43 @@ __global__ void __launch_bounds__(ANY_MAX_THREADS) gemv_any_kernel(const GemvArg
     const float* rf = reinterpret_cast<const float*>(&red[0][0]);
     const int mt = min(16, A.M - bt * 16);           // batch rows of this tile
     const int vbase = tile * 16;
-    // a row pair per thread: t -> (batch row i, pair u); the value of (i, row) sits in
-    // lane row + 16 (i >> 2), register i & 3
-    for (int t = tid; t < 16 * 8; t += nthr) {
-        const int i = t >> 3, row = 2 * (t & 7);
+    // a finish unit (a row, or a row pair in the fused modes) per thread: t -> (batch
+    // row i, unit); the value of (i, row) sits in lane row + 16 (i >> 2), register i & 3
+    constexpr int U = FINISH_ROWS<MODE>;
+    constexpr int NU = 16 / U;
+    for (int t = tid; t < 16 * NU; t += nthr) {
+        const int i = t / NU, row = U * (t % NU);
         const int v0 = vbase + row;
         if (i < mt && v0 < A.V) {
             const int l0 = row + 16 * (i >> 2), q = i & 3;
             float y0 = 0.f, y1 = 0.f;
             for (int w = 0; w < nw; ++w) {
                 y0 += rf[(w * 64 + l0) * 4 + q];
-                y1 += rf[(w * 64 + l0 + 1) * 4 + q];
+                if constexpr (U == 2) y1 += rf[(w * 64 + l0 + 1) * 4 + q];
             }
-            const bool two = v0 + 1 < A.V;
-            if (A.P == 1) finish_pair<DT, MODE>(A, bt * 16 + i, v0, y0, y1, two);
-            else put_pair(A, p, bt * 16 + i, v0, y0, y1, two);
+            const bool two = U == 2 && v0 + 1 < A.V;
+            if (A.P == 1) finish<DT, MODE>(A, bt * 16 + i, v0, y0, y1, two);
+            else put_unit(A, p, bt * 16 + i, v0, y0, y1, two);
         }
     }
     if (A.P > 1 && A.split_cnt && split_arrive(A, (int)blk, &flag)) {
-        for (int t = tid; t < 16 * 8; t += nthr) {
-            const int i = t >> 3, v0 = vbase + 2 * (t & 7);
+        for (int t = tid; t < 16 * NU; t += nthr) {
+            const int i = t / NU, v0 = vbase + U * (t % NU);
             if (i < mt && v0 < A.V) finish_from_partials<DT, MODE>(A, bt * 16 + i, v0);
         }
     }
 }
 
-// The combine launch (P > 1 without arrival counters): a row pair of one batch row per
-// thread, the P partials added in split order.
+// The combine launch (P > 1 without arrival counters): a finish unit of one batch row
+// per thread, the P partials added in split order.
 template <int DT, int MODE>
 __global__ void __launch_bounds__(256) gemv_combine_kernel(const GemvArgs A) {
-    const int64_t np = (A.V + 1) >> 1;
+    constexpr int U = FINISH_ROWS<MODE>;
+    const int64_t nu = (A.V + U - 1) / U;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= (int64_t)A.M * np) return;
-    const int b = (int)(t / np);
-    const int v0 = (int)(2 * (t - (int64_t)b * np));
+    if (t >= (int64_t)A.M * nu) return;
+    const int b = (int)(t / nu);
+    const int v0 = (int)(U * (t - (int64_t)b * nu));
     finish_from_partials<DT, MODE>(A, b, v0);
 }
 
@@ -219,7 +223,7 @@ const void* gemv_any_kernel_for(int dt, int mode) {
 }
 
 hipError_t launch_gemv_combine(const GemvArgs& A, int dt, int mode, hipStream_t stream) {
-    const int64_t total = (int64_t)A.M * ((A.V + 1) >> 1);
+    const int64_t total = (int64_t)A.M * (mode == MODE_GEMV ? A.V : (A.V + 1) >> 1);
     const void* f = dt == DT_F16 ? combine_for_mode<DT_F16>(mode)
                   : dt == DT_BF16 ? combine_for_mode<DT_BF16>(mode) : combine_for_mode<DT_F32>(mode);
     void* args[] = {const_cast<GemvArgs*>(&A)};

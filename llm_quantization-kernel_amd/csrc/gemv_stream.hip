@@ -4,7 +4,7 @@
 // range is split, the partial write that cb_reduce_kernel (:166-180) combines,
 // for one or two activation rows (the decode step) in fp16 or bf16 with any group size
 // that is a multiple of 32.  Plain, fused-QKV and fused gate-up modes share the body; the
-// outputs are finished a row pair at a time (finish_pair, cbk_device.hpp).
+// outputs are finished per row (plain) or row pair (fused modes; finish, cbk_device.hpp).
 //
 // Job = (block of RB = RPW RW virtual rows, K split p).  A workgroup holds KS x RW
 // waves: wave (ks, rw) takes rows RPW rw .. RPW rw + RPW - 1 of the block (RPW = 4,
@@ -28,8 +28,9 @@
 //   4. Each 4 rows' lane sums meet by v_permlane32_swap, v_permlane16_swap and four
 //      DPP row rotations (every lane of a 16-lane row ends with one row's total).
 //   5. Row totals of the slices meet in LDS and are added in slice order (so the
-//      result does not depend on wave timing); the finish stage runs per row pair, or
-//      with P > 1 the fp32 partials are written for the split-K combine.
+//      result does not depend on wave timing); the finish stage runs per finish unit
+//      (a row, or a row pair in the fused modes), or with P > 1 the fp32 partials are
+//      written for the split-K combine.
 #include "cbk_decode.hpp"
 #include "cbk_device.hpp"
 #include "cbk_kernels.hpp"
@@ -372,21 +373,22 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     }
     lds_barrier();
 
-    // 5. slices in order, then the finish stage (or the split's partials), a row pair
+    // 5. slices in order, then the finish stage (or the split's partials), a finish unit
     //    per thread
-    const int NP = RB / 2;
-    for (int t = tid; t < MB * NP; t += 64 * KS * RW) {
-        const int b = t / NP, row = 2 * (t - b * NP);
+    constexpr int U = FINISH_ROWS<MODE>;
+    const int NU = RB / U;
+    for (int t = tid; t < MB * NU; t += 64 * KS * RW) {
+        const int b = t / NU, row = U * (t - b * NU);
         const int v = vbase + row;
         if (b < A.M && v < A.V) {
             float y0 = 0.f, y1 = 0.f;
             for (int k = 0; k < KS; ++k) {
                 y0 += red[(k * MB + b) * RB + row];
-                y1 += red[(k * MB + b) * RB + row + 1];
+                if constexpr (U == 2) y1 += red[(k * MB + b) * RB + row + 1];
             }
-            const bool two = v + 1 < A.V;
-            if (A.P == 1) finish_pair<DT, MODE>(A, b, v, y0, y1, two);
-            else put_pair(A, p, b, v, y0, y1, two);
+            const bool two = U == 2 && v + 1 < A.V;
+            if (A.P == 1) finish<DT, MODE>(A, b, v, y0, y1, two);
+            else put_unit(A, p, b, v, y0, y1, two);
         }
     }
     // 6. with P > 1 and arrival counters, the last split of the block combines
@@ -574,21 +576,22 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     }
     lds_barrier();
 
-    // 5. slices in order, then the finish stage (or the split's partials), a row pair
+    // 5. slices in order, then the finish stage (or the split's partials), a finish unit
     //    per thread
-    const int NP = RB / 2;
-    for (int t = tid; t < M * NP; t += nthr) {
-        const int b = t / NP, ro = 2 * (t - b * NP);
+    constexpr int FU = FINISH_ROWS<MODE>;
+    const int NFU = RB / FU;
+    for (int t = tid; t < M * NFU; t += nthr) {
+        const int b = t / NFU, ro = FU * (t - b * NFU);
         const int v = vbase + ro;
         if (v < A.V) {
             float y0 = 0.f, y1 = 0.f;
             for (int k = 0; k < KS; ++k) {
                 y0 += red[(k * M + b) * RB + ro];
-                y1 += red[(k * M + b) * RB + ro + 1];
+                if constexpr (FU == 2) y1 += red[(k * M + b) * RB + ro + 1];
             }
-            const bool two = v + 1 < A.V;
-            if (A.P == 1) finish_pair<DT, MODE>(A, b, v, y0, y1, two);
-            else put_pair(A, p, b, v, y0, y1, two);
+            const bool two = FU == 2 && v + 1 < A.V;
+            if (A.P == 1) finish<DT, MODE>(A, b, v, y0, y1, two);
+            else put_unit(A, p, b, v, y0, y1, two);
         }
     }
     // 6. with P > 1 and arrival counters, the last split of the block combines
@@ -604,7 +607,7 @@ __global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
     } else {
         int proj, r;
         vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * 16 * A.st_rw, proj, r);
-        const int bits = src_of(A, proj).bits;
+        const int bits = bits_of(A, proj);
         if (bits == 2) bstream_body<2, MODE, BSU, DT>(A, lds);
         else if (bits == 3) bstream_body<3, MODE, BSU, DT>(A, lds);
         else bstream_body<4, MODE, BSU, DT>(A, lds);
@@ -625,7 +628,7 @@ __global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
     } else {
         int proj, r;
         vmap<MODE>(A, (int)fdiv(blockIdx.x, A.divP) * RPW * A.st_rw, proj, r);
-        const int bits = src_of(A, proj).bits;
+        const int bits = bits_of(A, proj);
         if (bits == 2) stream_body<2, MODE, MB, RPW, DT>(A, lds);
         else if (bits == 3) stream_body<3, MODE, MB, RPW, DT>(A, lds);
         else stream_body<4, MODE, MB, RPW, DT>(A, lds);

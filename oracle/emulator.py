@@ -17,6 +17,7 @@ import math
 import numpy as np
 import torch
 
+from . import reference as R
 from .reference import unpack_codes
 
 IS_EMULATOR = True
@@ -76,6 +77,24 @@ def dequant64(packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray, bits: i
     q = unpack_codes(packed, bits, K).astype(np.float64)
     g = np.arange(K) // gs
     return (q - zeros.astype(np.float64)[:, g]) * scales.astype(np.float64)[:, g]
+
+
+def dequant64_fast(packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray, bits: int, K: int,
+                   gs: int) -> np.ndarray:
+    """dequant64 through unpack_codes_by_slot and per-group broadcasting on the host cores
+    (torch float64, no repeated metadata arrays); the same float64 values
+    (tests/test_oracle_format.py)."""
+    q = torch.from_numpy(np.ascontiguousarray(R.unpack_codes_by_slot(packed, bits, K)))
+    N = q.shape[0]
+    G = scales.shape[1]
+    s = torch.from_numpy(np.asarray(scales, dtype=np.float64))
+    z = torch.from_numpy(np.asarray(zeros, dtype=np.float64))
+    if K == G * gs:
+        W = q.view(N, G, gs).to(torch.float64)
+        W.sub_(z[:, :, None]).mul_(s[:, :, None])
+        return W.view(N, K).numpy()
+    g = torch.arange(K) // gs
+    return ((q.to(torch.float64) - z[:, g]) * s[:, g]).numpy()
 
 
 def split_bounds(C: int, split_k: int):

@@ -36,6 +36,25 @@ def test_pack_matches_golden(case):
     p = R.pack_codes(q, case["bits"])
     assert np.array_equal(p, _words(case["words"]))
     assert np.array_equal(R.unpack_codes(p, case["bits"], case["K"]), q)
+    assert np.array_equal(R.unpack_codes_by_slot(p, case["bits"], case["K"]), q)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("K", [32, 200, 4096, 4128])
+def test_unpack_by_slot_equals_random_access(bits, K):
+    """The slot-wise unpack (and the float64 dequant built on it) against the random-access
+    unpack on arbitrary words -- every bit pattern, including the words past K."""
+    rng = np.random.default_rng(bits * 7 + K)
+    C = math.ceil(K / 32)
+    p = rng.integers(0, 1 << 32, size=(9, C * bits), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    q = R.unpack_codes(p, bits, K)
+    assert np.array_equal(R.unpack_codes_by_slot(p, bits, K), q)
+    from oracle import emulator as E
+    for gs in (32, 128):
+        G = math.ceil(K / gs)
+        sc = rng.standard_normal((9, G)).astype(np.float16)
+        ze = rng.integers(0, 1 << bits, size=(9, G)).astype(np.float16)
+        assert np.array_equal(E.dequant64_fast(p, sc, ze, bits, K, gs), E.dequant64(p, sc, ze, bits, K, gs))
 
 
 @pytest.mark.parametrize("case", json.load(open(os.path.join(GOLDEN, "quantize.json"))),
