@@ -53,6 +53,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_w3_m1_traffic.txt")
 PMC_COPY_BYTES = 256 << 20     # calibration copy of the counter passes
 MFMA_F16_PEAK_TFS = 2500.0     # MI355X dense fp16 MFMA, published
+MFMA_F32_PEAK_TFS = 157.3      # MI355X dense fp32 matrix, published
 METRIC = "W3/W4 GEMV µs & HBM GB/s (% peak); M=1024 prefill GEMM TFLOP/s (% peak)"
 SHAPES = [(4096, 4096), (4096, 11008), (11008, 4096)]          # (K, N)
 LAYERS = 32
@@ -311,7 +312,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="timed step + roofline only (no sweeps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--sweeps", default="gemv,fused,gemm,stack,model,producer",
+    ap.add_argument("--sweeps", default="gemv,fused,gemm,fp32,stack,model,producer",
                     help="comma-separated extra sweeps after the timed step (ignored with --quick); "
                          "also 'batched': batched decode at the library's own plans; 'dtypes': fp16 against "
                          "bf16 activations")
@@ -443,6 +444,8 @@ def main():
             out["fused"] = fused_sweep(torch, C, ops, dev, gate)
         if "gemm" in todo:
             out["gemm"] = gemm_sweep(torch, C, ops, dev, gate)
+        if "fp32" in todo:
+            out["fp32"] = fp32_sweep(torch, C, ops, dev, gate)
         if "stack" in todo:
             out["llama2_7b_stack"] = stack_sweep(torch, C, ops, dev, gate)
         if "model" in todo:
@@ -713,6 +716,51 @@ def fused_sweep(torch, C, ops, dev, gate):
     torch.cuda.empty_cache()
     log(f"fused: {res}")
     return res
+
+
+def fp32_sweep(torch, C, ops, dev, gate):
+    """fp32 activations (fp32 scales, zeros and outputs; the reference's T = float): the W3 decode
+    at M in {1, 4, 8} over the three shapes on the fp32 matrix-core decode, graph-replayed over
+    >= 1 GiB of weight copies, and the W4 prefill at M = 1024 (4096 x 4096) on the fp32 matrix-core
+    GEMM, beside the fp16 prefill with the 16-bit matrix cores turned off (use_tensor_cores=False,
+    the same fp32 kernel).  Every row checked against the oracle before it is timed."""
+    from dataclasses import replace
+    rows = []
+    for K, N in SHAPES:
+        base = make_weight(torch, N, K, 3, 0, dev)
+        w32 = replace(base, scales=base.scales.float(), zeros=base.zeros.float())
+        ws = [w32] + [clone_weight(w32) for _ in range(copies_for(weight_bytes(w32)) - 1)]
+        for M in (1, 4, 8):
+            x = randx(torch, M, K, 1, dev).float()
+            gate.gemv(f"fp32 decode W3 M={M} {K}->{N}", ops.packed_linear(x, ws[0]), x, w32)
+            fam = C.decode_plan(torch.float32, M, K, GS, N, 3, "gemv", 1, 1)[0]
+            us = graph_launch_us(torch, lambda: [ops.packed_linear(x, w) for w in ws], len(ws), replays=4)
+            nbytes = N * math.ceil(K / 32) * 3 * 4 + N * math.ceil(K / GS) * 8 + M * K * 4 + M * N * 4
+            gbs = nbytes / (us * 1e-6) / 1e9
+            rows.append({"kind": "decode", "bits": 3, "M": M, "K": K, "N": N, "us": round(us, 3),
+                         "GBps": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "kernel": fam})
+            log(f"fp32 decode W3 M={M} {K}->{N}: {us:.2f} us {gbs:.0f} GB/s ({fam})")
+        del ws, base, w32
+        gate.clear()
+        torch.cuda.empty_cache()
+    w = make_weight(torch, 4096, 4096, 4, 0, dev)
+    w32 = replace(w, scales=w.scales.float(), zeros=w.zeros.float())
+    for tag, ww, x, tc in (("fp32", w32, randx(torch, 1024, 4096, 1, dev).float(), True),
+                           ("fp16, use_tensor_cores=False", w, randx(torch, 1024, 4096, 1, dev), False)):
+        y = ops.packed_linear(x, ww, use_tensor_cores=tc)
+        rs = gate.rows(1024)
+        gate.check(f"prefill {tag} W4 M=1024 4096^2", y, gate.linear64(x, ww, rs), rs)
+        ws = [ww] + [clone_weight(ww) for _ in range(3)]
+        us = graph_launch_us(torch, lambda: [ops.packed_linear(x, v, use_tensor_cores=tc) for v in ws], len(ws),
+                             replays=3)
+        tfs = 2.0 * 1024 * 4096 * 4096 / (us * 1e-6) / 1e12
+        rows.append({"kind": "prefill", "x": tag, "bits": 4, "M": 1024, "K": 4096, "N": 4096, "us": round(us, 2),
+                     "TFLOPs": round(tfs, 1), "pct_fp32_matrix_peak": round(100 * tfs / MFMA_F32_PEAK_TFS, 1)})
+        log(f"prefill {tag} W4 M=1024 4096^2: {us:.1f} us {tfs:.1f} TFLOP/s")
+        del ws, y
+    gate.clear()
+    torch.cuda.empty_cache()
+    return rows
 
 
 def producer_sweep(torch, C, dev):

@@ -17,19 +17,21 @@
  *   - scales / zeros: [N, ceil(K/group_size)] row-major; zeros hold exact integers.
  *   - bias: [N] or NULL ("no bias" is an empty tensor in the reference, host_utils.h:80-81).
  *   - act: CBK_ACT_NONE / CBK_ACT_RELU / CBK_ACT_SILU (ops.py:24, common.cuh:10).
- *   - rho <= 0: one workgroup per job; rho > 0: min(jobs, rho * CUs) persistent
- *     workgroups (host_utils.h:90-93).  The fp16 batch-1 decode path always runs one
- *     workgroup per job (its workgroups gain nothing from persistence); rho is a
- *     launch-shape hint and never changes results.
+ *   - rho: the reference's persistence factor (host_utils.h:90-93).  Every decode kernel
+ *     here runs one workgroup per job (the jobs are assigned statically and its
+ *     workgroups gain nothing from persistence), so rho is accepted and never changes the
+ *     launch or the results.
  *   - workspace: the caller's int32[2] job-queue word pair (host_utils.h:38-47).  Jobs are
  *     distributed statically here, so the workspace is accepted, never written, and its
  *     [0,0] contract holds trivially.  May be NULL.
  *   - partial: fp32 scratch of cbk_gemv_partial_floats(...) elements, required only when
  *     that query returns a positive count (split-K partial sums, packed_gemv.cu:193-199).
- *     The streaming decode kernels combine the splits inside their own dispatch, using
- *     arrival counters the library keeps per device in a window per stream (32 windows);
- *     more than 32 streams making split calls at once on one device can share a window
- *     and race.  The other decode kernels combine in a second launch.
+ *     The decode kernels combine the splits inside their own dispatch, using arrival
+ *     counters the library keeps per device in windows (256 windows of 4096 counters); a
+ *     window belongs for good to one stream (its eager calls) or one graph capture, and is
+ *     never shared.  A call that finds no window of its own and no free one, or whose row
+ *     blocks outnumber a window's counters, combines in a second launch instead (the same
+ *     bits).  A graph must not be replayed while another replay of it still runs.
  *   - device: HIP device ordinal the pointers live on (the reference's CUDAGuard,
  *     packed_gemv.cu:259); the calling thread's current device is restored on return.
  *   - return: CBK_OK, or an error code with a message from cbk_last_error().
@@ -66,7 +68,11 @@ int cbk_tile_n(void);
  * (replaces crispybits_max_rho_mode, packed_gemv.cu:343-347). */
 int cbk_max_rho(int device, int bits, int mode, int* out);
 
-/* Decode kernel families reported by cbk_decode_plan. */
+/* Decode kernel families reported by cbk_decode_plan: the streaming kernel at batch 1-2
+ * (fp16 / bf16), the batched streaming kernel at batch 3-16 (fp16 / bf16, group sizes that
+ * are multiples of 128), and the fp32 matrix-core kernel for every other call (fp32
+ * activations, unaligned x, other group sizes at batch 3-16, batch > 16).  Values 3 and 5
+ * named kernels this library no longer has and are not returned. */
 enum { CBK_KERNEL_STREAM = 1, CBK_KERNEL_BSTREAM = 2, CBK_KERNEL_MFMA = 3, CBK_KERNEL_GENERIC = 4, CBK_KERNEL_BATCH = 5 };
 
 /* Additive policy query (no counterpart in the reference, whose tuner infers launches from
@@ -138,8 +144,10 @@ int cbk_fused_qkv_mixed(const void* x, int dtype, int64_t M, int64_t K,
                         int device, void* stream);
 
 /* Prefill: out[M,N] = act(x . W-hat^T + bias).  With use_matrix_cores and fp16/bf16 x,
- * W-hat = RN_T((q - z) * s) runs on MFMA; otherwise an fp32 VALU kernel computes it
- * unrounded (replaces packed_gemm_cuda, packed_gemm.cu:182-203; bindings.cpp:7-9). */
+ * W-hat = RN_T((q - z) * s) runs on the 16-bit matrix cores; otherwise (fp32 x, or
+ * use_matrix_cores = 0) W-hat is kept unrounded in fp32 and the products run on the fp32
+ * matrix cores with fp32 accumulation (replaces packed_gemm_cuda, packed_gemm.cu:182-203;
+ * bindings.cpp:7-9). */
 int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K,
                     const int32_t* packed, const void* scales, const void* zeros, const void* bias,
                     int64_t N, int bits, int group_size, int act, int use_matrix_cores,
