@@ -316,9 +316,10 @@ def main():
                     help="comma-separated extra sweeps after the timed step (ignored with --quick); "
                          "also 'batched': batched decode at the library's own plans; 'dtypes': fp16 against "
                          "bf16 activations")
-    ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm"),
+    ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm", "bstream"),
                     help="run the fixed launch sequence of a counter pass and exit: gemv (default: the "
-                         "W3 decode GEMV after a calibration copy) or gemm (the M=1024 W4 prefill GEMM)")
+                         "W3 decode GEMV after a calibration copy), gemm (the M=1024 W4 prefill GEMM) or "
+                         "bstream (the W3 batch-8 decode at 4096^2 and 11008->4096 after a calibration copy)")
     ap.add_argument("--trace-summary", nargs="+", metavar="FILE",
                     help="KERNEL_TRACE_CSV BENCH_JSON [UNTRACED_BENCH_JSON]: reduce a rocprofv3 kernel trace of a "
                          "bench run to the markdown tables under profiles/ (the default command's timed step, or "
@@ -345,6 +346,9 @@ def main():
     log(f"device {torch.cuda.get_device_name(dev)}  CUs={C.sm_count()}")
     if args.pmc_workload == "gemm":
         pmc_workload_gemm(torch, ops, dev)
+        return
+    if args.pmc_workload == "bstream":
+        pmc_workload_bstream(torch, ops, dev)
         return
     if args.pmc_workload:
         pmc_workload(torch, ops, dev)
@@ -575,6 +579,26 @@ def copies_for(nbytes, least=8):
 
 def weight_bytes(w):
     return w.packed.numel() * 4 + w.scales.numel() * w.scales.element_size() * 2
+
+
+def pmc_workload_bstream(torch, ops, dev):
+    """Launch sequence of the batched decode counter passes: the calibration copy, then 8 copies
+    each of the W3 batch-8 decode at 4096 x 4096 and at 11008 -> 4096 (the library's own plans).
+    Dispatch order: copy, 8 x (4096, 4096), 8 x (11008, 4096)."""
+    src = torch.empty(PMC_COPY_BYTES // 2, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    for K, N in ((4096, 4096), (11008, 4096)):
+        base = make_weight(torch, N, K, 3, 0, dev)
+        ws = [base] + [clone_weight(base) for _ in range(7)]
+        x = randx(torch, 8, K, 1, dev)
+        torch.cuda.synchronize()
+        for w in ws:
+            ops.packed_linear(x, w)
+        torch.cuda.synchronize()
+    log("pmc bstream workload done")
 
 
 def pmc_workload_gemm(torch, ops, dev):

@@ -39,66 +39,60 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int MAX_WAVES = ANY_MAX_THREADS / 64;
 
-constexpr int DEPTH = 4;   // chunks whose loads a wave keeps in flight
-
-// One chunk's operands for one lane, as loaded; converted when the chunk is consumed, so a
-// wave can keep DEPTH chunks' loads in flight without waiting on any of them.
+// The lane's 8 activations of chunk c for batch row b, as fp32 (zero past M or K).
+// `vec`: x is 16-byte aligned and K % 8 == 0, so an 8-code piece lies wholly before or
+// past K and is one (fp16 / bf16) or two (fp32) aligned 16-byte loads.
 template <int DT>
-struct Chunk {
-    static constexpr int XW = DT == DT_F32 ? 8 : 4;
-    uint32_t x[XW];          // the lane's 8 activations: fp32 words, or 16-bit pairs
-    uint32_t lo, hi;         // the word(s) holding the lane's 8 codes
-    uint32_t s, z;           // the chunk's scale and zero as stored (16-bit types: low half)
-};
-
-template <int DT>
-__device__ __forceinline__ float meta_to_f(uint32_t v) {
-    if constexpr (DT == DT_F32) return __uint_as_float(v);
-    else if constexpr (DT == DT_BF16) return __uint_as_float(v << 16);
-    else return (float)__builtin_bit_cast(_Float16, (uint16_t)v);
-}
-
-// The lane's activations of chunk c for batch row b (zero past M or K).  `vec`: x is 16-byte
-// aligned and K % 8 == 0, so an 8-code piece lies wholly before or past K and is one (16-bit)
-// or two (fp32) aligned 16-byte loads.
-template <int DT>
-__device__ __forceinline__ void fetch_x(const GemvArgs& A, bool vec, int b, int k0, Chunk<DT>& R) {
+__device__ __forceinline__ void load_x8(const GemvArgs& A, bool vec, int b, int k0, float (&xf)[8]) {
+    using S = typename Dt<DT>::S;
+    const S* row = reinterpret_cast<const S*>(A.x) + (long)b * A.K;
     const bool in = b < A.M;
-    if constexpr (DT == DT_F32) {
-        const uint32_t* row = reinterpret_cast<const uint32_t*>(A.x) + (long)b * A.K;
-        if (vec) {
-            uint4 u = make_uint4(0u, 0u, 0u, 0u), w = u;
-            if (in && k0 < A.K) {
-                u = *reinterpret_cast<const uint4*>(row + k0);
-                w = *reinterpret_cast<const uint4*>(row + k0 + 4);
+    if (vec) {
+        if (in && k0 < A.K) {
+            if constexpr (DT == DT_F32) {
+                const float4 u = *reinterpret_cast<const float4*>(row + k0);
+                const float4 v = *reinterpret_cast<const float4*>(row + k0 + 4);
+                xf[0] = u.x; xf[1] = u.y; xf[2] = u.z; xf[3] = u.w;
+                xf[4] = v.x; xf[5] = v.y; xf[6] = v.z; xf[7] = v.w;
+            } else {
+                const uint4 u = *reinterpret_cast<const uint4*>(row + k0);
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    xf[2 * e] = Dt<DT>::to_f((S)(uint16_t)(w[e] & 0xffffu));
+                    xf[2 * e + 1] = Dt<DT>::to_f((S)(uint16_t)(w[e] >> 16));
+                }
             }
-            R.x[0] = u.x; R.x[1] = u.y; R.x[2] = u.z; R.x[3] = u.w;
-            R.x[4] = w.x; R.x[5] = w.y; R.x[6] = w.z; R.x[7] = w.w;
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) R.x[e] = (in && k0 + e < A.K) ? row[k0 + e] : 0u;
+            for (int e = 0; e < 8; ++e) xf[e] = 0.f;
         }
     } else {
-        const uint16_t* row = reinterpret_cast<const uint16_t*>(A.x) + (long)b * A.K;
-        if (vec) {
-            uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (in && k0 < A.K) u = *reinterpret_cast<const uint4*>(row + k0);
-            R.x[0] = u.x; R.x[1] = u.y; R.x[2] = u.z; R.x[3] = u.w;
-        } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t l = (in && k0 + 2 * e < A.K) ? row[k0 + 2 * e] : 0u;
-                const uint32_t h = (in && k0 + 2 * e + 1 < A.K) ? row[k0 + 2 * e + 1] : 0u;
-                R.x[e] = l | (h << 16);
-            }
-        }
+        for (int e = 0; e < 8; ++e) xf[e] = (in && k0 + e < A.K) ? Dt<DT>::to_f(row[k0 + e]) : 0.f;
     }
 }
 
-template <int DT>
-__device__ __forceinline__ float x_at(const Chunk<DT>& R, int t) {
-    if constexpr (DT == DT_F32) return __uint_as_float(R.x[t]);
-    else return meta_to_f<DT>((t & 1) ? (R.x[t >> 1] >> 16) : (R.x[t >> 1] & 0xffffu));
+// fp16 bit patterns reinterpreted: the storage type of DT_F16 is _Float16, so a raw
+// 16-bit pattern needs a bit cast rather than a value conversion.
+template <>
+__device__ __forceinline__ void load_x8<DT_F16>(const GemvArgs& A, bool vec, int b, int k0, float (&xf)[8]) {
+    const _Float16* row = reinterpret_cast<const _Float16*>(A.x) + (long)b * A.K;
+    const bool in = b < A.M;
+    if (vec) {
+        if (in && k0 < A.K) {
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 h = *reinterpret_cast<const h8*>(row + k0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xf[e] = (float)h[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xf[e] = 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[e] = (in && k0 + e < A.K) ? (float)row[k0 + e] : 0.f;
+    }
 }
 
 template <int DT, int MODE>
@@ -134,52 +128,30 @@ __global__ void __launch_bounds__(ANY_MAX_THREADS) gemv_any_kernel(const GemvArg
     const int b = bt * 16 + j;
     const bool vec = A.st_xvec != 0;
 
-    // chunk c's loads: the lane's activations, its codes' word(s), the (scale, zero)
-    auto fetch = [&](int c, Chunk<DT>& R) {
-        fetch_x<DT>(A, vec, b, c * 32 + 8 * kq, R);
-        R.lo = R.hi = R.s = R.z = 0u;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c = c0 + wave; c < c1; c += nw) {
+        float xf[8];
+        load_x8<DT>(A, vec, b, c * 32 + 8 * kq, xf);
+        float wh[8];
         if (vin) {
             const int g = (int)fdiv((uint32_t)c, A.divGS);
+            const float s = load_f<DT>(S.s, (long)r * A.G + g);
+            const float nzs = -load_f<DT>(S.z, (long)r * A.G + g) * s;
             const uint32_t* cw = wrow + (long)c * bits + wi;
-            R.lo = cw[0];
-            if (two_words) R.hi = cw[1];
-            if constexpr (DT == DT_F32) {
-                R.s = reinterpret_cast<const uint32_t*>(S.s)[(long)r * A.G + g];
-                R.z = reinterpret_cast<const uint32_t*>(S.z)[(long)r * A.G + g];
-            } else {
-                R.s = reinterpret_cast<const uint16_t*>(S.s)[(long)r * A.G + g];
-                R.z = reinterpret_cast<const uint16_t*>(S.z)[(long)r * A.G + g];
+            const uint32_t lo = cw[0];
+            const uint32_t hi = two_words ? cw[1] : 0u;
+            const uint32_t f = (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t q = (f >> (t * bits)) & mask;         // v_bfe_u32
+                wh[t] = fmaf((float)q, s, nzs);
             }
-        }
-    };
-    // chunk c's eight MFMA steps: A = activations, B = W-hat = fma(q, s, -z s)
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
-    auto consume = [&](const Chunk<DT>& R) {
-        const float s = meta_to_f<DT>(R.s);
-        const float nzs = -meta_to_f<DT>(R.z) * s;
-        const uint32_t f = (uint32_t)((((uint64_t)R.hi << 32) | R.lo) >> sh);
+        } else {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint32_t q = (f >> (t * bits)) & mask;          // v_bfe_u32
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x_at<DT>(R, t), fmaf((float)q, s, nzs), acc, 0, 0, 0);
+            for (int t = 0; t < 8; ++t) wh[t] = 0.f;
         }
-    };
-    // the wave's chunks c0 + wave + i nw, i < nmy, with DEPTH of them in flight: slot i % DEPTH
-    // is refilled with chunk i + DEPTH as soon as chunk i is consumed
-    const int nmy = c1 - c0 > wave ? (c1 - c0 - wave + nw - 1) / nw : 0;
-    Chunk<DT> ring[DEPTH];
 #pragma unroll
-    for (int i = 0; i < DEPTH; ++i)
-        if (i < nmy) fetch(c0 + wave + i * nw, ring[i]);
-    for (int i0 = 0; i0 < nmy; i0 += DEPTH) {
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d) {
-            const int i = i0 + d;
-            if (i < nmy) {
-                consume(ring[d]);
-                if (i + DEPTH < nmy) fetch(c0 + wave + (i + DEPTH) * nw, ring[d]);
-            }
-        }
+        for (int t = 0; t < 8; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[t], wh[t], acc, 0, 0, 0);
     }
 
     // the waves' tiles meet in LDS, added in wave order
