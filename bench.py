@@ -312,7 +312,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="timed step + roofline only (no sweeps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--sweeps", default="gemv,fused,gemm,fp32,stack,model,producer",
+    ap.add_argument("--sweeps", default="gemv,fused,ablation,gemm,fp32,stack,model,producer",
                     help="comma-separated extra sweeps after the timed step (ignored with --quick); "
                          "also 'batched': batched decode at the library's own plans; 'dtypes': fp16 against "
                          "bf16 activations")
@@ -446,6 +446,8 @@ def main():
             out["dtypes"] = dtype_sweep(torch, C, ops, dev, gate)
         if "fused" in todo:
             out["fused"] = fused_sweep(torch, C, ops, dev, gate)
+        if "ablation" in todo:
+            out["ablation"] = ablation_sweep(torch, C, ops, dev, gate)
         if "gemm" in todo:
             out["gemm"] = gemm_sweep(torch, C, ops, dev, gate)
         if "fp32" in todo:
@@ -740,6 +742,139 @@ def fused_sweep(torch, C, ops, dev, gate):
     torch.cuda.empty_cache()
     log(f"fused: {res}")
     return res
+
+
+# The reference ablation's models (Kernel/scripts/_common.py MODELS): hidden, intermediate,
+# heads, KV heads, family.
+ABLATION_MODELS = {"llama2-7b": (4096, 11008, 32, 32, "llama"), "opt-2.7b": (2560, 10240, 32, 32, "opt")}
+
+
+def ablation_sweep(torch, C, ops, dev, gate, bits=3):
+    """The decode ablation of Kernel/scripts/ablation_decode.py:66-103 at M = 1, W3, for one block of
+    Llama-2-7B and of OPT-2.7B: the block's projections unfused (gate and up as two GEMVs and a
+    torch SiLU-multiply; fc1 then a torch ReLU), then with the projection fusion (fused QKV, fused
+    gate-up, fc1 with the ReLU in the kernel), fixed K splits 2 / 4 / 8, the split-K policy
+    (autotune's pick) and the exhaustive-grid oracle, beside dense fp16 (torch F.linear, i.e.
+    hipBLASLt) on the same shapes.  The reference's rho rows have no counterpart: no launch here
+    depends on rho (the kernels are not persistent), which the library's decode plan shows.  Each
+    row is µs per block, graph-replayed over >= 1 GiB of block copies; every configuration is
+    checked against the oracle before it is timed."""
+    import torch.nn.functional as F
+    from dataclasses import replace
+    from crispybits_kernels.autotune import tune_gate_up, tune_gemv, tune_qkv
+    out = {}
+    for model, (H, I, nh, nkv, fam) in ABLATION_MODELS.items():
+        opt = fam == "opt"
+        hd = H // nh
+        shapes = {"q": (nh * hd, H), "k": (nkv * hd, H), "v": (nkv * hd, H), "o": (H, H)}
+        shapes.update({"fc1": (I, H), "fc2": (H, I)} if opt else {"gate": (I, H), "up": (I, H), "down": (H, I)})
+        base = {}
+        for seed, (name, (N, K)) in enumerate(shapes.items(), start=1):
+            w = make_weight(torch, N, K, bits, seed, dev)
+            if opt:
+                g = torch.Generator().manual_seed(100 + seed)
+                w = replace(w, bias=(torch.randn(N, generator=g) * 0.02).half().to(dev))
+            base[name] = w
+        block_bytes = sum(weight_bytes(w) for w in base.values())
+        blocks = [base] + [{n: replace(clone_weight(w), bias=w.bias) for n, w in base.items()}
+                           for _ in range(copies_for(block_bytes, least=2) - 1)]
+        xh, xi = randx(torch, 1, H, 1, dev), randx(torch, 1, I, 2, dev)
+        down = "fc2" if opt else "down"
+        up_mod = "fc1" if opt else "gu"
+        mods = ["qkv", "o", up_mod, down]
+
+        def unfused(b, sk=lambda m: 1):
+            outs = [ops.packed_linear(xh, b[n], sk(n), 1) for n in ("q", "k", "v", "o")]
+            if opt:
+                outs.append(torch.relu(ops.packed_linear(xh, b["fc1"], sk("fc1"), 1)))
+            else:
+                outs.append(F.silu(ops.packed_linear(xh, b["gate"], sk("gate"), 1)) *
+                            ops.packed_linear(xh, b["up"], sk("up"), 1))
+            outs.append(ops.packed_linear(xi, b[down], sk(down), 1))
+            return outs
+
+        def fused(b, sk=lambda m: 1):
+            outs = list(ops.fused_qkv(xh, b["q"], b["k"], b["v"], sk("qkv"), 1))
+            outs.append(ops.packed_linear(xh, b["o"], sk("o"), 1))
+            if opt:
+                outs.append(ops.packed_linear(xh, b["fc1"], sk("fc1"), 1, "relu"))
+            else:
+                outs.append(ops.fused_gate_up(xh, b["gate"], b["up"], sk("gu"), 1))
+            outs.append(ops.packed_linear(xi, b[down], sk(down), 1))
+            return outs
+
+        def refs():
+            w = base
+            r = [gate.linear64(xh, w[n]) for n in ("q", "k", "v", "o")]
+            if opt:
+                r.append(torch.relu(gate.linear64(xh, w["fc1"]) + w["fc1"].bias.double().cpu()))
+            else:
+                r.append(gate.linear64(xh, w["gate"], act="silu") * gate.linear64(xh, w["up"]))
+            r.append(gate.linear64(xi, w[down]))
+            if opt:
+                for i, n in enumerate(("q", "k", "v", "o")):
+                    r[i] = r[i] + w[n].bias.double().cpu()
+                r[5] = r[5] + w["fc2"].bias.double().cpu()
+            return r
+
+        ref = refs()
+        names = ["q", "k", "v", "o", "fc1" if opt else "gate*up", down]
+
+        def timed(tag, fn):
+            for nm, y, r in zip(names, fn(base), ref):
+                gate.check(f"ablation {model} W{bits} {tag}: {nm}", y, r)
+            return graph_launch_us(torch, lambda: [fn(b) for b in blocks], len(blocks), replays=4)
+
+        rows = [("1 base packed (unfused, P_K = 1)", timed("unfused", unfused)),
+                ("2 + projection fusion", timed("fused", fused))]
+        for pk in (2, 4, 8):
+            rows.append((f"5 fixed split-K P_K = {pk}", timed(f"P_K={pk}", lambda b, pk=pk: fused(b, lambda m: pk))))
+
+        def tune(m):
+            it = dict(warmup=5, iters=10, exhaustive=True)
+            if m == "qkv":
+                return tune_qkv(xh, base["q"], base["k"], base["v"], **it)
+            if m == "gu":
+                return tune_gate_up(xh, base["gate"], base["up"], **it)
+            return tune_gemv(xi if m == down else xh, base[m], act="relu" if m == "fc1" else None, **it)
+
+        reports = {m: tune(m) for m in mods}
+        pol = {m: r.best.split_k for m, r in reports.items()}
+        orc = {m: r.oracle.split_k for m, r in reports.items()}
+        rows.append(("6 split-K policy", timed("policy", lambda b: fused(b, lambda m: pol[m]))))
+        rows.append(("7 oracle (exhaustive grid)", timed("oracle", lambda b: fused(b, lambda m: orc[m]))))
+        gate.clear()
+
+        dense = [{n: torch.randn(N, K, device=dev, dtype=torch.float16) * 0.02 for n, (N, K) in shapes.items()}
+                 for _ in range(max(2, copies_for(sum(2 * N * K for N, K in shapes.values()), least=2)))]
+        bias = {n: base[n].bias for n in shapes} if opt else {n: None for n in shapes}
+
+        def fp16_block(d):
+            for n in ("q", "k", "v", "o"):
+                F.linear(xh, d[n], bias[n])
+            if opt:
+                torch.relu(F.linear(xh, d["fc1"], bias["fc1"]))
+            else:
+                F.silu(F.linear(xh, d["gate"])) * F.linear(xh, d["up"])
+            F.linear(xi, d[down], bias[down])
+
+        fp = graph_launch_us(torch, lambda: [fp16_block(d) for d in dense], len(dense), replays=4)
+        del dense
+        b0 = rows[0][1]
+        out[model] = {
+            "bits": bits, "M": 1, "group_size": GS, "block_copies": len(blocks),
+            "rows": [{"step": n, "us": round(us, 2), "x_vs_base": round(b0 / us, 3), "x_vs_fp16": round(fp / us, 3)}
+                     for n, us in rows],
+            "fp16_dense_us": round(fp, 2),
+            "policy_split_k": pol, "oracle_split_k": orc,
+            "regret": {m: round(r.regret, 4) for m, r in reports.items()},
+            "rho": "no launch depends on rho (non-persistent kernels)"}
+        for n, us in rows:
+            log(f"ablation {model}: {n:36s} {us:8.2f} us  {b0 / us:5.2f}x vs base  {fp / us:5.2f}x vs fp16")
+        log(f"ablation {model}: fp16 dense {fp:.2f} us")
+        del blocks, base
+        torch.cuda.empty_cache()
+    return out
 
 
 def fp32_sweep(torch, C, ops, dev, gate):

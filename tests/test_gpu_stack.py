@@ -151,7 +151,8 @@ def test_llama_stack_blocks_graph_replay(hip):
 
 
 def test_llama_stack_blocks_oracle_decode_and_prefill(hip):
-    """Two blocks of the stack (config-5 bits, Llama-2-7B widths) against the CPU oracle, the
+    """Three blocks of the stack (config-5 bits, Llama-2-7B widths: blocks 0, 1 and 3, the first
+    W4, W3 and W2 blocks of the bitmap) against the CPU oracle, the
     decode leg at M = 1 and the prefill leg at M = 2048: every linear of both blocks (fused QKV,
     o, fused gate-up, down) against the float64 product on the oracle's dequantized weights --
     W-hat for decode, W-hat rounded once to fp16 for the prefill GEMM (oracle/emulator.py).  The
@@ -160,13 +161,16 @@ def test_llama_stack_blocks_oracle_decode_and_prefill(hip):
     from oracle import emulator as E
 
     dev = torch.device("cuda", 0)
-    bitmap = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 32)][:2]
+    full = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 32)]
+    picked = [full.index(4), full.index(3), full.index(2)]
+    assert picked == [0, 1, 3]
     rng = np.random.default_rng(7)
     rows = np.sort(rng.choice(2048, 64, replace=False))
     gx = torch.Generator().manual_seed(11)
     xh = torch.randn(2048, H, generator=gx).half().to(dev)
     xi = torch.randn(2048, I, generator=gx).half().to(dev)
-    for i, bits in enumerate(bitmap):
+    for i in picked:
+        bits = full[i]
         pb, _ = _stack_block(i, bits, dev)
         cols, W64 = {}, {}
         for nm, N, K in LINEARS:
