@@ -315,7 +315,7 @@ def main():
     ap.add_argument("--sweeps", default="gemv,fused,ablation,gemm,fp32,stack,model,producer",
                     help="comma-separated extra sweeps after the timed step (ignored with --quick); "
                          "also 'batched': batched decode at the library's own plans; 'dtypes': fp16 against "
-                         "bf16 activations")
+                         "bf16 activations; 'splits': the split-K policy against every split request")
     ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm", "bstream"),
                     help="run the fixed launch sequence of a counter pass and exit: gemv (default: the "
                          "W3 decode GEMV after a calibration copy), gemm (the M=1024 W4 prefill GEMM) or "
@@ -448,6 +448,8 @@ def main():
             out["fused"] = fused_sweep(torch, C, ops, dev, gate)
         if "ablation" in todo:
             out["ablation"] = ablation_sweep(torch, C, ops, dev, gate)
+        if "splits" in todo:
+            out["split_policy"] = split_sweep(torch, C, ops, dev, gate)
         if "gemm" in todo:
             out["gemm"] = gemm_sweep(torch, C, ops, dev, gate)
         if "fp32" in todo:
@@ -742,6 +744,45 @@ def fused_sweep(torch, C, ops, dev, gate):
     torch.cuda.empty_cache()
     log(f"fused: {res}")
     return res
+
+
+# Shapes of the split-K policy sweep (K, N): the Llama-2-7B / 13B, Llama-3-8B and OPT widths,
+# and narrow outputs down to 64 rows.
+SPLIT_SWEEP_SHAPES = [(4096, 4096), (4096, 11008), (11008, 4096), (2560, 2560), (2560, 10240), (10240, 2560),
+                      (2048, 2048), (2048, 8192), (8192, 2048), (5120, 5120), (5120, 13824), (13824, 5120),
+                      (4096, 14336), (14336, 4096), (1024, 4096), (4096, 2048), (4096, 1024), (4096, 512),
+                      (4096, 256), (4096, 128), (4096, 64), (11008, 256), (11008, 128), (14336, 256),
+                      (28672, 512), (28672, 256)]
+
+
+def split_sweep(torch, C, ops, dev, gate, batches=(1, 8)):
+    """The split-K policy against every split request 1, 2, 3, 4, 6, 8 (W3, g = 128, fp16), at
+    batch 1 and 8 over SPLIT_SWEEP_SHAPES: µs per call graph-replayed over >= 1 GiB of weight
+    copies, the library's K splits for each request, and the policy's pick.  Each request's launch
+    is checked against the oracle before it is timed."""
+    rows = []
+    for K, N in SPLIT_SWEEP_SHAPES:
+        base = make_weight(torch, N, K, 3, 0, dev)
+        ws = [base] + [clone_weight(base) for _ in range(copies_for(weight_bytes(base), least=4) - 1)]
+        for M in batches:
+            x = randx(torch, M, K, 1, dev)
+            t, P = {}, {}
+            for sk in (1, 2, 3, 4, 6, 8):
+                gate.gemv(f"split sweep W3 M={M} {K}->{N} split_k={sk}", ops.packed_linear(x, ws[0], sk, 1), x, base)
+                P[sk] = C.decode_plan(torch.float16, M, K, GS, N, 3, "gemv", sk, 1)[1]
+                t[sk] = round(graph_launch_us(torch, lambda: [ops.packed_linear(x, w, sk, 1) for w in ws], len(ws),
+                                              replays=6), 2)
+            best = min(t, key=t.get)
+            pol = ops._k_splits(None, 1, M, N, K, x)
+            rows.append({"K": K, "N": N, "M": M, "us": t, "library_splits": P, "best_request": best,
+                         "policy_request": pol, "policy_regret": round(t[pol] / t[best] - 1, 4),
+                         "underfill_rule_request": ops.candidate_split_k(-(-M // ops.BATCH_TILE), N, ops.tile_n(),
+                                                                         ops.sm_count(), 1)})
+            log(f"split sweep W3 M={M} {K}->{N}: {t} best {best} policy {pol}")
+        del ws, base
+        gate.clear()
+        torch.cuda.empty_cache()
+    return rows
 
 
 # The reference ablation's models (Kernel/scripts/_common.py MODELS): hidden, intermediate,

@@ -7,12 +7,13 @@ Interface of Kernel/crispybits_kernels/autotune.py:1-169: ``TuneResult``, ``Tune
 ``install_bitmap(tuning=...)`` reads).  The search is this build's own and works in
 *launches*:
 
-* The candidate points are the split-K rule's pick for every rho in 1..max_rho and, with
-  ``exhaustive``, every split request of ``EXHAUSTIVE_PK`` at every rho.  Each point is
-  mapped to the launch the library makes for it (``_C.decode_plan``: kernel family, K
-  splits, workgroups, threads, LDS, launches per call); points that map to the same launch
-  are one candidate, timed once, and a candidate is a policy candidate when any rule pick
-  maps to it.  On the streaming kernels rho changes no launch, so it adds no timing.
+* The candidate points are the split-K policy's pick (``ops.policy_split_k``) for every rho
+  in 1..max_rho and, with ``exhaustive``, every split request of ``EXHAUSTIVE_PK`` at every
+  rho.  Each point is mapped to the launch the library makes for it (``_C.decode_plan``:
+  kernel family, K splits, workgroups, threads, LDS, launches per call); points that map to
+  the same launch are one candidate, timed once, and a candidate is a policy candidate when
+  any policy pick maps to it.  On the streaming kernels rho changes no launch, so it adds no
+  timing.
 * Time is kernel time: the summed dispatch durations of a call (a split call counts its
   combine launch), from the library's per-dispatch timer, so the ranking sees the kernels
   and not the host's launch rate.
@@ -30,7 +31,7 @@ from typing import Callable, Dict, List, Optional, Sequence, Tuple
 import torch
 
 from . import ops
-from .ops import (BATCH_TILE, PackedLinear, PackedLinearWeight, candidate_split_k, fused_gate_up, fused_qkv,
+from .ops import (BATCH_TILE, PackedLinear, PackedLinearWeight, fused_gate_up, fused_qkv, policy_split_k,
                   max_rho, new_workspace, packed_linear, sm_count, tile_n, virtual_rows)
 
 # Split requests of the exhaustive sweep: dense where the streaming kernels' launches differ
@@ -114,7 +115,7 @@ def _search(run: Callable[[int, int], object], kind: str, batch: int, k: int, gs
     chunks = ceil(k / 32)
     widest = max(bits) if isinstance(bits, (tuple, list)) else bits
     rhos = range(1, max(1, max_rho(widest, kind)) + 1)
-    points = [(rho, candidate_split_k(batch_tiles, v_rows, bn, sms, rho, max_split), True) for rho in rhos]
+    points = [(rho, policy_split_k(batch, v_rows, k, rho, max_split), True) for rho in rhos]
     if exhaustive:
         points += [(rho, pk, False) for rho in rhos for pk in EXHAUSTIVE_PK if max_split is None or pk <= max_split]
     candidates: Dict[Tuple, List] = {}            # launch -> [rho, split, policy], first point first

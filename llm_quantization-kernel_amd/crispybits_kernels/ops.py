@@ -8,9 +8,8 @@ RuntimeError behaviour.  How they run is this build's own:
 
 * **Call routing.**  A call is decode (the streaming GEMV kernels) when its flattened
   batch has at most ``decode_threshold`` rows, else prefill (the MFMA GEMM).  The K split
-  of a decode call is a pure function of plain integers (kind, rows, virtual rows, K,
-  requested split, rho, device), memoised in ``_rule_splits``, so a repeated call shape
-  costs a dictionary lookup on the host.
+  of a decode call is the caller's request, or with ``split_k=None`` the policy's
+  (``policy_split_k``: no split, retuned for MI355X -- see ``POLICY_SPLIT_K``).
 * **RoPE layout.**  ``rope_row_order`` / ``rope_inverse_order`` are closed forms (stored
   row 2i of a head is original row i, stored row 2i+1 is original row i + head_dim/2).
   The prefill fallback of ``fused_qkv`` rotates the projection while it is still in the
@@ -26,7 +25,8 @@ Retuned or additive, relative to the reference:
     (the reference uses 4, ops.py:23).
   * ``fused_qkv`` takes per-projection widths (the reference raises ValueError,
     ops.py:240-241); the kernel dispatches the width per workgroup.
-  * The split-K rule counts decode jobs per ``BATCH_TILE`` batch rows.
+  * The split-K rule counts decode jobs per ``BATCH_TILE`` batch rows, and the policy a
+    ``split_k=None`` call takes requests no split (``POLICY_SPLIT_K``, measured at 256 CUs).
   * ``set_backend`` takes "cuda" (alias "hip") or a module object with the ``_C``
     functions -- the hook the CPU tests use to inject the oracle.  No emulator ships in
     the product: ``set_backend("emulator")`` raises RuntimeError.
@@ -75,7 +75,7 @@ def set_backend(name):
                            "pass the module object to set_backend to use it")
     else:
         raise ValueError(name)
-    for cached in (tile_n, _sm_count_for, _rule_splits):
+    for cached in (tile_n, _sm_count_for):
         cached.cache_clear()
 
 
@@ -243,20 +243,33 @@ def candidate_split_k(batch: int, n: int, bn: int, sms: int, rho: int, max_split
     return parts if max_split is None else min(max_split, parts)
 
 
-@lru_cache(maxsize=None)
-def _rule_splits(rho: int, batch: int, v_rows: int, chunks: int, device_index: int) -> int:
-    tiles = -(-batch // BATCH_TILE)
-    return max(1, min(candidate_split_k(tiles, v_rows, tile_n(), _sm_count_for(device_index), rho), chunks))
+# The split a decode call requests when the caller passes split_k=None.  The reference's
+# policy is the underfill rule above (split K when fewer than rho * SMs decode jobs exist).
+# Retuned for MI355X it requests no split at any shape: a decode workgroup here already spreads
+# K over up to 16 slice waves, and a K split adds a round trip of fp32 partials through the L2
+# plus a second finish pass.  Measured (W3, graph replays over >= 1 GiB of rotating weights,
+# 25 shapes with N from 64 to 14336 and K from 1024 to 28672): at batch 1 a requested split never
+# beat split 1 (the underfill rule's picks cost up to +97 % at 256 CUs, e.g. 4096 -> 512: 3.9 us
+# unsplit, 7.7 us at its 8 splits); at batch 3..16 the batched planner adds splits itself where
+# its own fill rule finds idle CUs.  The underfill rule stays available as candidate_split_k.
+POLICY_SPLIT_K = 1
+
+
+def policy_split_k(batch: int, v_rows: int, k: int, rho: int = 1, max_split: Optional[int] = None) -> int:
+    """The policy's K split for a decode call of `batch` rows, `v_rows` virtual rows and K = `k`
+    (POLICY_SPLIT_K, within [1, ceil(k / 32)] and `max_split`)."""
+    del batch, v_rows, rho
+    pk = POLICY_SPLIT_K if max_split is None else min(POLICY_SPLIT_K, max_split)
+    return max(1, min(pk, -(-k // 32)))
 
 
 def _k_splits(split_k: Optional[int], rho: int, batch: int, v_rows: int, k: int, x: torch.Tensor) -> int:
     """K splits of a decode call: the caller's split clamped to [1, chunks], or for
-    split_k=None the underfill rule at this call's batch size."""
+    split_k=None the policy's (policy_split_k)."""
     chunks = -(-k // 32)
     if split_k is not None:
         return max(1, min(int(split_k), chunks))
-    dev = x.get_device()
-    return _rule_splits(int(rho), batch, v_rows, chunks, dev if dev >= 0 else 0)
+    return policy_split_k(batch, v_rows, k, rho)
 
 
 # ----------------------------------------------------------------------------- ops

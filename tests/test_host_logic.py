@@ -121,12 +121,14 @@ def test_policy_rule(emu):
     assert candidate_split_k(64, 4096, bn, S, 1) == 1
     assert candidate_split_k(1, 10 ** 6, bn, S, 1) == 1
     assert candidate_split_k(1, bn, bn, S, 2, max_split=8) == 8
-    # a decode call's split clamps to the chunk count and counts batch tiles of 16 rows
+    # a requested split clamps to the chunk count; split_k=None takes the policy, which
+    # requests no split on this GPU at any shape, rho or batch (and respects max_split)
     x = torch.empty(0)
-    assert ops._k_splits(None, 1, 1, 64, 64, x) == 2           # rule wants 64, K has 2 chunks
     assert ops._k_splits(5, 1, 1, 64, 4096, x) == 5
     assert ops._k_splits(99, 1, 1, 64, 100, x) == 4            # ceil(100 / 32) chunks
-    assert ops._k_splits(None, 1, 16, 4096, 4096, x) == ops._k_splits(None, 1, 1, 4096, 4096, x)
+    for batch, v_rows, k, rho in ((1, 64, 64, 1), (1, 512, 4096, 1), (8, 256, 28672, 2), (16, 11008, 4096, 4)):
+        assert ops._k_splits(None, rho, batch, v_rows, k, x) == ops.POLICY_SPLIT_K == 1
+    assert ops.policy_split_k(1, 64, 4096, 1, max_split=1) == 1
 
 
 def test_workspace_contract(emu):
