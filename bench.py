@@ -312,8 +312,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="timed step + roofline only (no sweeps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--sweeps", default="gemv,fused,ablation,gemm,fp32,stack,model,producer",
+    ap.add_argument("--sweeps", default="gemv,fused,probe,ablation,gemm,fp32,stack,model,producer",
                     help="comma-separated extra sweeps after the timed step (ignored with --quick); "
+                         "'probe': a read-only streaming launch over each decode call's bytes; "
                          "also 'batched': batched decode at the library's own plans; 'dtypes': fp16 against "
                          "bf16 activations; 'splits': the split-K policy against every split request")
     ap.add_argument("--pmc-workload", nargs="?", const="gemv", choices=("gemv", "gemm", "bstream"),
@@ -446,6 +447,8 @@ def main():
             out["dtypes"] = dtype_sweep(torch, C, ops, dev, gate)
         if "fused" in todo:
             out["fused"] = fused_sweep(torch, C, ops, dev, gate)
+        if "probe" in todo:
+            out["probe"] = probe_sweep(torch, C, dev, out.get("gemv_sweep"), out.get("fused"))
         if "ablation" in todo:
             out["ablation"] = ablation_sweep(torch, C, ops, dev, gate)
         if "splits" in todo:
@@ -645,6 +648,62 @@ def gemv_sweep(torch, C, ops, dev, gate):
             del ws, base
             gate.clear()
             torch.cuda.empty_cache()
+    return rows
+
+
+def probe_sweep(torch, C, dev, gemv_rows=None, fused=None):
+    """The floor a single launch sets: `C.stream_probe` (one streaming kernel, every 16-byte
+    piece read once) over the algorithmic bytes of each M = 1 decode call of the sweeps --
+    W2/W3/W4 at the three shapes, fused QKV at the fused sweep's widths, fused gate-up W3 --
+    graph-replayed over >= 1 GiB of distinct buffers like the GEMV rows, best of unroll in
+    {1, 2, 4, 8, 16} pieces per thread x {256, 1024} threads per workgroup; `probe_us` reads and
+    keeps nothing, `probe_store_us` also writes one word per workgroup after a workgroup
+    reduction (as a decode workgroup ends).  Each row carries the decode call's own µs from the
+    sweeps of the same run when they ran."""
+    sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+    meta = lambda N, K: N * math.ceil(K / GS) * 2 * 2                      # noqa: E731
+    packed = lambda N, K, b: N * math.ceil(K / 32) * b * 4                # noqa: E731
+    qkv_bits = [int(b) for b in (fused or {}).get("qkv", {}).get("bits", [4, 3, 3])]
+    cases = [(f"W{b} {K}->{N}", b, K, N, gemv_bytes(1, K, N, b)) for b in (4, 3, 2) for K, N in SHAPES]
+    cases.append(("fused QKV 4096->3x4096", qkv_bits, 4096, 3 * 4096,
+                  sum(packed(4096, 4096, b) + meta(4096, 4096) for b in qkv_bits) + 4096 * 2 + 3 * 4096 * 2))
+    cases.append(("fused gate-up 4096->2x11008", 3, 4096, 11008,
+                  2 * (packed(11008, 4096, 3) + meta(11008, 4096)) + 4096 * 2 + 11008 * 2))
+    gemv_us = {(r["bits"], r["K"], r["N"]): r["us"] for r in (gemv_rows or []) if r["M"] == 1}
+    rows = []
+    for name, b, K, N, nbytes in cases:
+        pool = [torch.zeros((nbytes + 15) // 16 * 4, dtype=torch.int32, device=dev)
+                for _ in range(copies_for(nbytes))]
+        torch.cuda.synchronize()
+        best = {}
+        for store in (False, True):
+            for unroll in (1, 2, 4, 8, 16):
+                for block in (256, 1024):
+                    us = graph_launch_us(torch, lambda: [C.stream_probe(t, unroll, block, store, sink) for t in pool],
+                                         len(pool), replays=4)
+                    if store not in best or us < best[store][0]:
+                        best[store] = (us, unroll, block)
+        us, unroll, block = best[False]
+        row = {"case": name, "bits": b, "K": K, "N": N, "bytes": nbytes, "probe_us": round(us, 3),
+               "probe_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+               "probe_pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+               "unroll": unroll, "block": block, "probe_store_us": round(best[True][0], 3),
+               "store_unroll": best[True][1], "store_block": best[True][2], "copies": len(pool)}
+        if name.startswith("fused QKV"):
+            call = (fused or {}).get("qkv", {}).get("us")
+        elif name.startswith("fused gate-up"):
+            call = (fused or {}).get("gate_up", {}).get("us")
+        else:
+            call = gemv_us.get((b, K, N))
+        if call:
+            row["call_us"] = call
+            row["call_over_probe"] = round(call / us, 3)
+        rows.append(row)
+        log(f"probe {name}: {us:.2f} us ({row['probe_GBps']:.0f} GB/s, unroll {unroll}, block {block}), "
+            f"with stores {best[True][0]:.2f} us"
+            + (f"; the call {call:.2f} us" if call else ""))
+        del pool
+        torch.cuda.empty_cache()
     return rows
 
 

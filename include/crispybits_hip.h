@@ -179,6 +179,17 @@ int cbk_unpack_codes(const int32_t* packed, int64_t N, int64_t K, int bits, int3
 int cbk_timer_start(int capacity);
 int cbk_timer_stop(double* total_ms, int* launches, double* durations_ms, int max_durations);
 
+/* Additive measurement hook (no counterpart in the reference): one launch that reads
+ * `bytes` (at most 2^30) of device memory at `src` once, as 16-byte pieces -- the floor a
+ * single launch needs to stream a decode call's bytes.  `unroll` (1, 2, 4, 8 or 16) is the
+ * pieces each thread requests before it uses any, `block` the workgroup size (a multiple of
+ * 64, at most 1024); the grid covers `bytes`.  store = 0: nothing is kept (sink[0] is
+ * practically never written; the write keeps the loads alive); store = 1: each workgroup
+ * reduces what it read and writes one word to sink[workgroup % 1024], as a decode
+ * workgroup writes its results.  `sink` holds 1024 writable uint32. */
+int cbk_stream_probe(const void* src, int64_t bytes, int unroll, int block, int store, uint32_t* sink,
+                     int device, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

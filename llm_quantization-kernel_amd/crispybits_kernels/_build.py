@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = os.environ.get("CRISPYBITS_ARCH", "gfx950")
 
 SOURCES = ["abi.cpp", "gemv_stream.hip", "gemv_any.hip", "gemm.hip", "gemm_f16.hip", "gemm_f32.hip",
-           "unpack.hip", "quant.hip"]
+           "unpack.hip", "quant.hip", "probe.hip"]
 
 # -packed-fp32-ops is disabled: the kernels never rely on v_pk_*_f32.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-munsafe-fp-atomics",

@@ -297,6 +297,8 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
     }
     const int rb = sp.rpw * sp.rw;
     if (mixed && (A.src[0].n % rb != 0 || A.src[1].n % rb != 0)) return sp;
+    // a wave's rows lie in one projection (the kernel resolves them once per wave)
+    if (mode == CBK_MODE_QKV && (A.src[0].n % sp.rpw != 0 || A.src[1].n % sp.rpw != 0)) return sp;
     const int64_t grid = ceil_div(A.V, rb) * sp.P;
     if (grid >= lim) return sp;
     sp.grid = (int)grid;
@@ -636,6 +638,7 @@ GemvArgs base_args(const void* x, int64_t M, int64_t K, int gs) {
     A.C = (int)ceil_div(K, 32);
     A.G = (int)ceil_div(K, gs);
     A.gs = gs;
+    A.divHD = make_fastdiv(1);
     return A;
 }
 
@@ -672,6 +675,7 @@ int qkv_common(const void* x, int dtype, int64_t M, int64_t K, const int32_t* wq
     set_proj(A, 2, wv, sv, zv, bv, out_v, nv, bits_v, K);
     A.V = (int)(nq + nk + nv);
     A.perm_hd = perm_hd;
+    A.divHD = make_fastdiv((uint32_t)(perm_hd > 0 ? perm_hd : 1));
     if (rope) {
         A.rope_cos = rope_cos;
         A.rope_sin = rope_sin;
@@ -955,6 +959,23 @@ int cbk_unpack_codes(const int32_t* packed, int64_t N, int64_t K, int bits, int3
     const hipError_t e = launch_unpack(reinterpret_cast<const uint32_t*>(packed), (int)N, (int)K, bits, codes,
                                        reinterpret_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "unpack_codes: launch");
+    return CBK_OK;
+}
+
+int cbk_stream_probe(const void* src, int64_t bytes, int unroll, int block, int store, uint32_t* sink,
+                     int device, void* stream) {
+    if (!src || !sink) return fail(CBK_EINVAL, "stream_probe: pointers must be non-null");
+    if (bytes <= 0 || bytes > (1ll << 30)) return fail(CBK_EINVAL, "stream_probe: bytes must be in [1, 2^30]");
+    if (unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8 && unroll != 16)
+        return fail(CBK_EINVAL, "stream_probe: unroll must be 1, 2, 4, 8 or 16");
+    if (block < 64 || block > 1024 || block % 64 != 0)
+        return fail(CBK_EINVAL, "stream_probe: block must be a multiple of 64 in [64, 1024]");
+    if (store != 0 && store != 1) return fail(CBK_EINVAL, "stream_probe: store must be 0 or 1");
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    const hipError_t e = launch_stream_probe(src, (uint32_t)bytes, unroll, block, store != 0, sink,
+                                             reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "stream_probe: launch");
     return CBK_OK;
 }
 

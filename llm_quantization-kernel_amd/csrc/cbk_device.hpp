@@ -9,6 +9,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 namespace cbk {
@@ -60,14 +61,6 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     if (act == ACT_RELU) return v > 0.f ? v : 0.f;
     if (act == ACT_SILU) return silu(v);
     return v;
-}
-
-// Stored (pair-interleaved) row r of a head -> original row (the inverse of
-// ops.rope_row_order; same map as common.cuh:66-70).
-__device__ __forceinline__ int rope_unperm(int r, int hd) {
-    if (hd <= 0) return r;
-    const int head = r / hd, p = r - head * hd;
-    return head * hd + ((p & 1) ? (p >> 1) + (hd >> 1) : (p >> 1));
 }
 
 // ---------------------------------------------------------------- invariant division
@@ -144,6 +137,7 @@ struct GemvArgs {
     const float* rope_cos; // [M, head_dim] or nullptr
     const float* rope_sin;
     int head_dim, perm_hd;
+    FastDiv divHD;         // by perm_hd (1 when the Q/K rows are not pair-interleaved)
     int mtiles, jobs;      // fp32 matrix-core kernel: 16-row batch tiles, jobs
     int bits[3];           // code width of each projection
     int pad_;
@@ -153,7 +147,10 @@ struct GemvArgs {
 // A projection's fields as values.  Each candidate field is pinned as an SGPR value
 // first (the empty asm), so LLVM selects between values rather than between addresses
 // inside the kernel-argument block -- an address select there would copy the whole
-// block to scratch.  `p` may differ between lanes (the select is then per lane).
+// block to scratch.  The select is bit masks, not a conditional: written as `?:` LLVM
+// sinks each pinned value into its own arm and the wave branches (a chain of scalar
+// branches in front of the first weight load of every fused-QKV wave).  `p` may differ
+// between lanes (the select is then per lane).
 template <typename T>
 __device__ __forceinline__ T pinned(T v) {
     asm("" : "+s"(v));
@@ -161,7 +158,12 @@ __device__ __forceinline__ T pinned(T v) {
 }
 template <typename T>
 __device__ __forceinline__ T pick3(int p, T a, T b, T c) {
-    return p == 0 ? pinned(a) : (p == 1 ? pinned(b) : pinned(c));
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "pick3 selects 32- or 64-bit values");
+    using U = typename std::conditional<sizeof(T) == 8, uint64_t, uint32_t>::type;
+    const U ua = __builtin_bit_cast(U, pinned(a)), ub = __builtin_bit_cast(U, pinned(b));
+    const U uc = __builtin_bit_cast(U, pinned(c));
+    const U m1 = (U)0 - (U)(p == 1), m2 = (U)0 - (U)(p == 2);
+    return __builtin_bit_cast(T, (U)((ua & ~(m1 | m2)) | (ub & m1) | (uc & m2)));
 }
 
 __device__ __forceinline__ Src src_of(const GemvArgs& A, int p) {
@@ -194,10 +196,11 @@ __device__ __forceinline__ void vmap(const GemvArgs& A, int v, int& proj, int& r
     if constexpr (MODE == MODE_GATEUP) {
         proj = v & 1; r = v >> 1;
     } else if constexpr (MODE == MODE_QKV) {
+        // branch-free: a = v past Q, b = v past K
         const int n0 = A.src[0].n, n1 = A.src[1].n;
-        if (v < n0) { proj = 0; r = v; }
-        else if (v < n0 + n1) { proj = 1; r = v - n0; }
-        else { proj = 2; r = v - n0 - n1; }
+        const int a = v >= n0, b = v >= n0 + n1;
+        proj = a + b;
+        r = v - (n0 & -a) - (n1 & -b);
     } else {
         proj = 0; r = v;
     }
@@ -219,14 +222,48 @@ __device__ __forceinline__ void vmap(const GemvArgs& A, int v, int& proj, int& r
 template <int MODE>
 constexpr int FINISH_ROWS = MODE == MODE_GEMV ? 1 : 2;
 
-// One QKV row with no rotation: bias, then the store at its original position.
+// QKV pair (v0, v0 + 1), v0 even.  When Q and K are stored pair-interleaved (perm_hd > 0,
+// widths multiples of the even perm_hd: host check), a Q or K pair is stored rows (r, r + 1)
+// of one head, r even, holding original rows o = head hd + (r - head hd) / 2 and o + hd / 2
+// (the inverse of ops.rope_row_order, common.cuh:66-70): with RoPE the two are rotated
+// together, without it they are stored back in place.  Otherwise rows keep their order and
+// the pair may straddle two projections (odd widths).  One projection lookup per row, the
+// head by an invariant division: no generic integer division.
 template <int DT>
-__device__ __forceinline__ void qkv_plain_row(const GemvArgs& A, int b, int v, float y) {
+__device__ __forceinline__ void qkv_finish(const GemvArgs& A, int b, int v0, float y0, float y1, bool two) {
     int p, r;
-    vmap<MODE_QKV>(A, v, p, r);
+    vmap<MODE_QKV>(A, v0, p, r);
     const Dst D = dst_of(A, p);
-    if (D.bias) y += load_f<DT>(D.bias, r);
-    store_f<DT>(D.y, (long)b * D.ld + rope_unperm(r, p < 2 ? A.perm_hd : 0), y);
+    if (p < 2 && A.perm_hd > 0) {
+        if (D.bias) {
+            y0 += load_f<DT>(D.bias, r);
+            y1 += load_f<DT>(D.bias, r + 1);
+        }
+        const int hd = A.perm_hd, half = hd >> 1;
+        const int head = (int)fdiv((uint32_t)r, A.divHD);
+        const int d = (r - head * hd) >> 1;               // < hd / 2
+        const long o = (long)b * D.ld + head * hd + d;    // original rows o and o + hd / 2
+        if (A.rope_cos != nullptr) {                      // head_dim == perm_hd (host check)
+            const float* cs = A.rope_cos + (long)b * hd;
+            const float* sn = A.rope_sin + (long)b * hd;
+            const float c0 = cs[d], s0 = sn[d], c1 = cs[d + half], s1 = sn[d + half];
+            store_f<DT>(D.y, o, y0 * c0 - y1 * s0);
+            store_f<DT>(D.y, o + half, y1 * c1 + y0 * s1);
+        } else {
+            store_f<DT>(D.y, o, y0);
+            store_f<DT>(D.y, o + half, y1);
+        }
+        return;
+    }
+    if (D.bias) y0 += load_f<DT>(D.bias, r);
+    store_f<DT>(D.y, (long)b * D.ld + r, y0);
+    if (two) {
+        int p1, r1;
+        vmap<MODE_QKV>(A, v0 + 1, p1, r1);
+        const Dst D1 = p1 == p ? D : dst_of(A, p1);
+        if (D1.bias) y1 += load_f<DT>(D1.bias, r1);
+        store_f<DT>(D1.y, (long)b * D1.ld + r1, y1);
+    }
 }
 
 template <int DT, int MODE>
@@ -238,28 +275,7 @@ __device__ __forceinline__ void finish(const GemvArgs& A, int b, int v0, float y
         if (bias) y0 += load_f<DT>(bias, v0);
         store_f<DT>(A.dst[0].y, (long)b * A.dst[0].ld + v0, apply_act(y0, A.act));
     } else {
-        int p, r;
-        vmap<MODE_QKV>(A, v0, p, r);
-        if (A.rope_cos != nullptr && p < 2) {
-            // Q and K widths are multiples of the even head_dim (host check), so row
-            // v0 + 1 is row r + 1 of the same projection and head
-            const Dst D = dst_of(A, p);
-            if (D.bias) {
-                y0 += load_f<DT>(D.bias, r);
-                y1 += load_f<DT>(D.bias, r + 1);
-            }
-            const int hd = A.head_dim, half = hd >> 1;
-            const int lo = rope_unperm(r, hd);            // original row of stored row r
-            const int d = lo % hd;                        // < hd / 2
-            const float* cs = A.rope_cos + (long)b * hd;
-            const float* sn = A.rope_sin + (long)b * hd;
-            const long o = (long)b * D.ld + lo;
-            store_f<DT>(D.y, o, y0 * cs[d] - y1 * sn[d]);
-            store_f<DT>(D.y, o + half, y1 * cs[d + half] + y0 * sn[d + half]);
-        } else {
-            qkv_plain_row<DT>(A, b, v0, y0);
-            if (two) qkv_plain_row<DT>(A, b, v0 + 1, y1);
-        }
+        qkv_finish<DT>(A, b, v0, y0, y1, two);
     }
 }
 

@@ -75,4 +75,8 @@ hipError_t launch_quant_pack(const QuantArgs& A, int dt, int mdt, int cus, hipSt
 // unpack.hip
 hipError_t launch_unpack(const uint32_t* packed, int N, int K, int bits, int32_t* codes, hipStream_t stream);
 
+// probe.hip: one read-only streaming launch over `bytes` (the measurement floor).
+hipError_t launch_stream_probe(const void* src, uint32_t bytes, int unroll, int block, bool store, uint32_t* sink,
+                               hipStream_t stream);
+
 }  // namespace cbk

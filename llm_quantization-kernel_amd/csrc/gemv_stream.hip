@@ -258,10 +258,6 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     for (int b = 0; b < MB; ++b) load_x(xr, tid < nrange && b < A.M, b, c0 + tid, A.K, xa[b]);
 
     // 1b. the wave's packed chunks and their (scale, zero) halves
-    ProjRes R[3];
-    R[0] = proj_res(A.src[0], A.G);
-    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.src[1], A.G);
-    if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.src[1], A.G); R[2] = proj_res(A.src[2], A.G); }
     int gi[CPL];
     bool cin[CPL];
 #pragma unroll
@@ -270,16 +266,25 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
         cin[i] = c < nrange;
         gi[i] = (int)fdiv((uint32_t)(c0 + c), A.divGS);       // group of the chunk
     }
+    // The wave's RPW rows, resolved once: v0 is a multiple of RPW, so gate-up rows alternate
+    // gate / up from an even row, and fused QKV rows lie in one projection (the host keeps
+    // the Q and K widths multiples of RPW).  A per-row map would put a chain of scalar
+    // branches between the row loads.
+    int proj0, r0;
+    vmap<MODE>(A, min(v0, A.V - 1), proj0, r0);
+    const Src S0 = MODE == MODE_QKV ? src_of(A, proj0) : A.src[0];
+    ProjRes R[2];
+    R[0] = proj_res(S0, A.G);
+    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.src[1], A.G);
     uint32_t w[RPW][CPL][BITS];
     uint32_t sz[RPW][CPL][2];
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
         const int v = v0 + j;
         const bool vin = v < A.V;
-        int proj, r;
-        vmap<MODE>(A, vin ? v : 0, proj, r);
-        const ProjRes& P = proj == 0 ? R[0] : (proj == 1 ? R[1] : R[2]);
-        const int wpr = src_of(A, proj).wpr;
+        const int r = MODE == MODE_GATEUP ? r0 + (j >> 1) : r0 + j;
+        const ProjRes& P = MODE == MODE_GATEUP ? R[j & 1] : R[0];
+        const int wpr = MODE == MODE_GATEUP ? A.src[j & 1].wpr : S0.wpr;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = ks * SLICE + lane + 64 * i;
@@ -372,13 +377,26 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
         }
     }
     lds_barrier();
+}
 
-    // 5. slices in order, then the finish stage (or the split's partials), a finish unit
-    //    per thread
+// 5. slices in order, then the finish stage (or the split's partials), a finish unit per
+//    thread: MB RB / U <= 16 RW units against 64 KS RW threads, so one pass.  Kept out of
+//    stream_body, so the mixed-width kernel carries one copy of it, not one per width.
+// 6. with P > 1 and arrival counters, the last split of the block combines.
+template <int MODE, int MB, int RPW, int DT>
+__device__ __forceinline__ void stream_tail(const GemvArgs& A, char* lds) {
+    const int tid = threadIdx.x;
+    const int KS = A.st_ks, RB = RPW * A.st_rw;
+    const int NCH = KS * SLICE;
+    const int blk = (int)fdiv(blockIdx.x, A.divP);
+    const int p = blockIdx.x - blk * A.P;
+    const int vbase = blk * RB;
+    const float* red = reinterpret_cast<const float*>(lds + (64 + XB_BYTES<DT>) * MB * NCH);
     constexpr int U = FINISH_ROWS<MODE>;
     const int NU = RB / U;
-    for (int t = tid; t < MB * NU; t += 64 * KS * RW) {
-        const int b = t / NU, row = U * (t - b * NU);
+    if (tid < MB * NU) {
+        const int b = MB == 1 ? 0 : (tid >= NU ? 1 : 0);
+        const int row = U * (tid - b * NU);
         const int v = vbase + row;
         if (b < A.M && v < A.V) {
             float y0 = 0.f, y1 = 0.f;
@@ -391,9 +409,9 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
             else put_unit(A, p, b, v, y0, y1, two);
         }
     }
-    // 6. with P > 1 and arrival counters, the last split of the block combines
-    if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
-        split_finish<DT, MODE>(A, vbase, RB, 64 * KS * RW);
+    if (A.P > 1 && A.split_cnt &&
+        split_arrive(A, blk, reinterpret_cast<int*>(const_cast<float*>(red))))
+        split_finish<DT, MODE>(A, vbase, RB, 64 * KS * A.st_rw);
 }
 
 // ------------------------------------------------------------------ batch rows 3..16
@@ -575,13 +593,28 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
         if (i < M) red[(ks * M + i) * RB + roff] = acc[q];
     }
     lds_barrier();
+}
 
-    // 5. slices in order, then the finish stage (or the split's partials), a finish unit
-    //    per thread
+// 5. slices in order, then the finish stage (or the split's partials), a finish unit per
+//    thread; out of bstream_body, so the mixed-width kernel carries one copy.  Unit t is
+//    (batch row t / NFU, row pair or row t % NFU), NFU = 16 RW / FU: the batch row is a
+//    shift and the invariant division by RW.
+// 6. with P > 1 and arrival counters, the last split of the block combines.
+template <int MODE, int BSU, int DT>
+__device__ __forceinline__ void bstream_tail(const GemvArgs& A, char* lds) {
+    const int tid = threadIdx.x;
+    const int KS = A.st_ks, RB = 16 * A.st_rw, M = A.M;
+    const int NU = KS * BSU, NCH = 4 * NU;
+    const int nthr = 64 * KS * A.st_rw;
+    const int blk = (int)fdiv(blockIdx.x, A.divP);
+    const int p = blockIdx.x - blk * A.P;
+    const int vbase = blk * RB;
+    float* red = reinterpret_cast<float*>(lds + 64 * NCH * M) + (DT == DT_BF16 ? 48 : 32) * NU;
     constexpr int FU = FINISH_ROWS<MODE>;
+    constexpr int LOG = FU == 2 ? 3 : 4;          // log2(16 / FU)
     const int NFU = RB / FU;
     for (int t = tid; t < M * NFU; t += nthr) {
-        const int b = t / NFU, ro = FU * (t - b * NFU);
+        const int b = (int)fdiv((uint32_t)(t >> LOG), A.divRW), ro = FU * (t - b * NFU);
         const int v = vbase + ro;
         if (v < A.V) {
             float y0 = 0.f, y1 = 0.f;
@@ -594,7 +627,6 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
             else put_unit(A, p, b, v, y0, y1, two);
         }
     }
-    // 6. with P > 1 and arrival counters, the last split of the block combines
     if (A.P > 1 && A.split_cnt && split_arrive(A, blk, reinterpret_cast<int*>(red)))
         split_finish<DT, MODE>(A, vbase, RB, nthr);
 }
@@ -612,6 +644,7 @@ __global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
         else if (bits == 3) bstream_body<3, MODE, BSU, DT>(A, lds);
         else bstream_body<4, MODE, BSU, DT>(A, lds);
     }
+    bstream_tail<MODE, BSU, DT>(A, lds);
 }
 
 // BITS = 0: fused QKV with a width per projection; the host keeps each
@@ -633,6 +666,7 @@ __global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
         else if (bits == 3) stream_body<3, MODE, MB, RPW, DT>(A, lds);
         else stream_body<4, MODE, MB, RPW, DT>(A, lds);
     }
+    stream_tail<MODE, MB, RPW, DT>(A, lds);
 }
 
 template <int MB, int RPW, int DT>

@@ -4,7 +4,7 @@
 // Replaces the reference's pybind11 module (Kernel/csrc/bindings.cpp:32-40): the same seven
 // functions with the same argument order -- packed_gemv, packed_gemm, fused_gate_up, fused_qkv,
 // sm_count, tile_n, max_rho -- tensors in and tensors out, plus the additive entries of this build
-// (unpack_codes, quantize_pack, decode_plan, timer_start / timer_stop).  Tensor checks restate
+// (unpack_codes, quantize_pack, decode_plan, timer_start / timer_stop, stream_probe).  Tensor checks restate
 // host_utils.h:38-87 and fail through TORCH_CHECK (RuntimeError in Python); "no bias / no RoPE /
 // no workspace" may be None or an empty tensor (ops.py:74-83).  Outputs and split-K partials come
 // from torch's caching allocator on x's device; the kernels run on torch's current HIP stream of
@@ -345,6 +345,17 @@ py::tuple timer_stop() {
     return py::make_tuple(total, py::cast(d));
 }
 
+// One streaming launch over the bytes of a CUDA tensor (the measurement floor of
+// cbk_stream_probe); `sink` is a CUDA int32 tensor of at least 1024 elements on the same device.
+void stream_probe(const Tensor& src, int64_t unroll, int64_t block, bool store, Tensor& sink) {
+    TORCH_CHECK(src.is_cuda() && src.is_contiguous(), "src must be a contiguous CUDA tensor");
+    TORCH_CHECK(sink.is_cuda() && sink.device() == src.device() && sink.scalar_type() == at::kInt &&
+                sink.is_contiguous() && sink.numel() >= 1024, "sink must be 1024 CUDA int32 on src's device");
+    const int dev = src.get_device();
+    ok(cbk_stream_probe(src.data_ptr(), src.numel() * src.element_size(), (int)unroll, (int)block, store ? 1 : 0,
+                        reinterpret_cast<uint32_t*>(sink.data_ptr<int32_t>()), dev, stream_of(dev)));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_ext, m) {
@@ -363,5 +374,7 @@ PYBIND11_MODULE(_ext, m) {
     m.def("decode_plan", &decode_plan, "The launch a decode call would make");
     m.def("timer_start", &timer_start, "Arm the per-launch kernel timer", py::arg("capacity") = 4096);
     m.def("timer_stop", &timer_stop, "Disarm the timer: (total ms, per-launch ms)");
+    m.def("stream_probe", &stream_probe, "One streaming launch over a tensor's bytes (the measurement floor)",
+          py::arg("src"), py::arg("unroll"), py::arg("block"), py::arg("store"), py::arg("sink"));
     m.attr("ABI_VERSION") = cbk_abi_version();
 }

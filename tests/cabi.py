@@ -32,6 +32,7 @@ SIGS = {
     "cbk_quantize_pack": (_I, [_P, _I, _L, _L, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
     "cbk_timer_start": (_I, [_I]),
     "cbk_timer_stop": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_double), _I]),
+    "cbk_stream_probe": (_I, [_P, _L, _I, _I, _I, _P, _I, _P]),
 }
 
 lib = ctypes.CDLL(_C.LIB_PATH)

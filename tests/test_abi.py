@@ -40,7 +40,7 @@ def test_op_module_binds_the_reference_functions():
     import torch
     from crispybits_kernels import _C
     for name in ("packed_gemv", "packed_gemm", "fused_gate_up", "fused_qkv", "sm_count", "tile_n", "max_rho",
-                 "unpack_codes", "quantize_pack", "decode_plan", "timer_start", "timer_stop"):
+                 "unpack_codes", "quantize_pack", "decode_plan", "timer_start", "timer_stop", "stream_probe"):
         assert callable(getattr(_C, name)), name
     x = torch.zeros(1, 256)
     w = torch.zeros(4, 32, dtype=torch.int32)
