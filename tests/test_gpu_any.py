@@ -148,6 +148,20 @@ def test_qkv_odd_widths(hip):
         close(ov, ref_linear(x, V64, vb), torch.float16)
 
 
+@pytest.mark.parametrize("widths,fam", [((102, 40, 26), "generic"), ((104, 40, 28), "stream"),
+                                        ((100, 36, 30), "stream")])
+def test_qkv_widths_per_wave(hip, widths, fam):
+    """Batch-1 fused QKV with one width: the streaming kernel resolves a wave's 4 rows to
+    one projection, so it takes Q and K widths that are multiples of 4 (any V width); other
+    widths go to the fp32 matrix-core kernel.  Both within the fp16 bar, with biases."""
+    K = 512
+    assert plan(torch.float16, 1, K, 128, widths, 3, "qkv")[0] == fam
+    ws = [make(n, K, 3, torch.float16, True, s + 1) for s, n in enumerate(widths)]
+    x = randx(1, K, torch.float16, seed=7)
+    for o, (w, W64, b64, _) in zip(fused_qkv(x, *(t[0] for t in ws)), ws):
+        close(o, ref_linear(x, W64, b64), torch.float16)
+
+
 # ------------------------------------------------------------------ split counters and the combine launch
 
 def _hip_runtime():
