@@ -482,12 +482,10 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     }
 
     // 1b. the wave's packed chunks and the (scale, zero) of each unit's group
-    ProjRes R[3];
-    R[0] = proj_res(A.src[0], A.G);
-    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.src[1], A.G);
-    if constexpr (MODE == MODE_QKV) { R[1] = proj_res(A.src[1], A.G); R[2] = proj_res(A.src[2], A.G); }
-    const ProjRes& P = proj == 0 ? R[0] : (proj == 1 ? R[1] : R[2]);
-    const int wpr = src_of(A, proj).wpr;
+    // the wave's projection, selected once (by masks: no branches in front of the loads)
+    const Src S = MODE == MODE_GEMV ? A.src[0] : src_of(A, proj);
+    const ProjRes P = proj_res(S, A.G);
+    const int wpr = S.wpr;
     // the (scale, zero) of unit 4 e + kq's group of row j: BSU / 4 2-byte gathers each per
     // wave (lanes of a row then share them by ds_bpermute), rather than one per unit
     static_assert(BSU % 4 == 0, "whole units per lane quarter");
