@@ -48,7 +48,7 @@ extern "C" {
 enum { CBK_F16 = 0, CBK_BF16 = 1, CBK_F32 = 2 };
 enum { CBK_ACT_NONE = 0, CBK_ACT_RELU = 1, CBK_ACT_SILU = 2 };
 enum { CBK_MODE_GEMV = 0, CBK_MODE_QKV = 1, CBK_MODE_GATEUP = 2 };
-enum { CBK_OK = 0, CBK_EINVAL = 1, CBK_EHIP = 2 };
+enum { CBK_OK = 0, CBK_EINVAL = 1, CBK_EHIP = 2, CBK_ENOTSUP = 3 };
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* cbk_last_error(void);
@@ -152,6 +152,18 @@ int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K,
                     const int32_t* packed, const void* scales, const void* zeros, const void* bias,
                     int64_t N, int bits, int group_size, int act, int use_matrix_cores,
                     void* out, int device, void* stream);
+
+/* Prefill gate-up: out[M,N] = RN_T(RN_T(silu(x . G-hat^T)) * RN_T(x . U-hat^T)) in one launch,
+ * bit-identical to two cbk_packed_gemm calls (the gate's with act = 2) followed by an
+ * elementwise product in T.  No counterpart in the reference's _C: it replaces the
+ * two-GEMM-and-multiply sequence of the reference's ops.fused_gate_up for batches above the
+ * decode threshold (Kernel/crispybits_kernels/ops.py:216-220).  fp16 / bf16 x only, with
+ * K % 8 == 0 and 16-byte aligned x, packed, scales and zeros; other calls return
+ * CBK_ENOTSUP (nothing launched) and take the two-GEMM sequence. */
+int cbk_packed_gemm_gate_up(const void* x, int dtype, int64_t M, int64_t K,
+                            const int32_t* packed_gate, const void* scales_gate, const void* zeros_gate,
+                            const int32_t* packed_up, const void* scales_up, const void* zeros_up,
+                            int64_t N, int bits, int group_size, void* out, int device, void* stream);
 
 /* Format producer on the device: group-affine quantization of w[N,K] (fp16 / bf16 /
  * fp32) to `bits`-bit codes, packed as the kernels read them, with fp16 / bf16 / fp32

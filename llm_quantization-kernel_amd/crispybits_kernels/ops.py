@@ -311,9 +311,10 @@ def fused_gate_up(x: torch.Tensor, gate: PackedLinearWeight, up: PackedLinearWei
                   split_k: Optional[int] = None, rho: int = 1, decode_threshold: int = DECODE_THRESHOLD,
                   workspace: Optional[torch.Tensor] = None):
     """silu(x G^T) * (x U^T).  Decode: one kernel over interleaved gate/up rows, the
-    product formed in fp32 and rounded once.  Prefill: two GEMMs (SiLU in the gate's
-    epilogue), multiplied in the activation dtype -- the reference's double rounding
-    (ops.py:216-220)."""
+    product formed in fp32 and rounded once.  Prefill: the reference's two GEMMs (SiLU in
+    the gate's epilogue) multiplied in the activation dtype, with its double rounding
+    (ops.py:216-220) -- for fp16 / bf16 activations as one GEMM launch whose epilogue forms
+    the product of the two rounded factors."""
     _check_ext()
     if gate.bits != up.bits:
         raise ValueError("fused Gate/Up requires the same precision for Gate and Up within a block")
@@ -323,7 +324,10 @@ def fused_gate_up(x: torch.Tensor, gate: PackedLinearWeight, up: PackedLinearWei
         pk = _k_splits(split_k, rho, M, 2 * gate.out_features, gate.in_features, x2)
         y = _C.fused_gate_up(x2, gate.packed, gate.scales, gate.zeros, up.packed, up.scales, up.zeros,
                              gate.bits, gate.in_features, gate.group_size, pk, rho, workspace)
-    else:
+    elif hasattr(_C, "packed_gemm_gate_up"):
+        y = _C.packed_gemm_gate_up(x2, gate.packed, gate.scales, gate.zeros, up.packed, up.scales, up.zeros,
+                                   gate.bits, gate.in_features, gate.group_size)
+    else:   # a backend with the reference's seven functions only (e.g. its emulator)
         y = _C.packed_gemm(x2, gate.packed, gate.scales, gate.zeros, None, gate.bits, gate.in_features,
                            gate.group_size, ACT["silu"], True)
         y.mul_(_C.packed_gemm(x2, up.packed, up.scales, up.zeros, None, up.bits, up.in_features,

@@ -917,6 +917,50 @@ int cbk_packed_gemm(const void* x, int dtype, int64_t M, int64_t K, const int32_
     return CBK_OK;
 }
 
+int cbk_packed_gemm_gate_up(const void* x, int dtype, int64_t M, int64_t K, const int32_t* packed_gate,
+                            const void* scales_gate, const void* zeros_gate, const int32_t* packed_up,
+                            const void* scales_up, const void* zeros_up, int64_t N, int bits, int group_size,
+                            void* out, int device, void* stream) {
+    int rc = check_x(x, dtype, M, K);
+    if (rc) return rc;
+    if ((rc = check_weight(packed_gate, scales_gate, zeros_gate, N, bits, group_size, "packed_gemm_gate_up(gate)")))
+        return rc;
+    if ((rc = check_weight(packed_up, scales_up, zeros_up, N, bits, group_size, "packed_gemm_gate_up(up)")))
+        return rc;
+    if (!out) return fail(CBK_EINVAL, "packed_gemm_gate_up: out must be non-null");
+    if (dtype != CBK_F16 && dtype != CBK_BF16)
+        return fail(CBK_ENOTSUP, "packed_gemm_gate_up: x must be fp16 or bf16 (the 16-bit matrix cores)");
+    GemmArgs A{};
+    A.x = x;
+    A.w = reinterpret_cast<const uint32_t*>(packed_gate);
+    A.s = scales_gate;
+    A.z = zeros_gate;
+    A.w2 = reinterpret_cast<const uint32_t*>(packed_up);
+    A.s2 = scales_up;
+    A.z2 = zeros_up;
+    A.out = out;
+    A.M = (int)M;
+    A.N = (int)N;
+    A.K = (int)K;
+    A.C = (int)ceil_div(K, 32);
+    A.G = (int)ceil_div(K, group_size);
+    A.gs = group_size;
+    A.wpr = (int)(A.C * bits);
+    A.bits = bits;
+    A.act = ACT_SILU;
+    A.divG = make_fastdiv((uint32_t)group_size);
+    A.xvec = (K % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+    if (!gemm_f16_supported(A))
+        return fail(CBK_ENOTSUP, "packed_gemm_gate_up: needs K %% 8 == 0 and 16-byte aligned x, packed, scales "
+                                 "and zeros");
+    if (M == 0) return CBK_OK;
+    DeviceGuard guard(device);
+    if (guard.err != hipSuccess) return hip_fail(guard.err, "set device");
+    const hipError_t e = launch_gemm_f16(A, dtype, reinterpret_cast<hipStream_t>(stream), true);
+    if (e != hipSuccess) return hip_fail(e, "packed_gemm_gate_up: launch");
+    return CBK_OK;
+}
+
 int cbk_quantize_pack(const void* w, int dtype, int64_t N, int64_t K, int bits, int group_size, int scheme,
                       int32_t* packed, void* scales, void* zeros, int meta_dtype, int device, void* stream) {
     if (!valid_dtype(dtype)) return fail(CBK_EINVAL, "quantize_pack: weights must be fp16/bf16/fp32");

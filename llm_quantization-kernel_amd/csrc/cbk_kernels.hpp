@@ -49,6 +49,9 @@ struct GemmArgs {
     int M, N, K, C, G, gs, wpr, bits, act;
     int xvec;               // x is 16-byte aligned and K % 8 == 0 (vector activation loads)
     FastDiv divG;           // by the group size
+    const uint32_t* w2;     // gate-up GEMM: the up projection's packed [N, wpr], scales, zeros
+    const void* s2;
+    const void* z2;
 };
 
 // gemm.hip: fp16 / bf16 on the 16-bit matrix cores, any alignment.
@@ -57,9 +60,10 @@ hipError_t launch_gemm_mfma(const GemmArgs& A, int dt, hipStream_t stream);
 // gemm_f32.hip: any dtype, fp32 operands on the fp32 matrix cores, W-hat unrounded.
 hipError_t launch_gemm_f32(const GemmArgs& A, int dt, hipStream_t stream);
 
-// gemm_f16.hip: fp16 or bf16 (dt), K % 8 == 0, 16-byte aligned x.
+// gemm_f16.hip: fp16 or bf16 (dt), K % 8 == 0, 16-byte aligned x.  gate_up: out =
+// silu(x . W-hat^T) * (x . W2-hat^T), each factor rounded to the dtype first (no bias).
 bool gemm_f16_supported(const GemmArgs& A);
-hipError_t launch_gemm_f16(const GemmArgs& A, int dt, hipStream_t stream);
+hipError_t launch_gemm_f16(const GemmArgs& A, int dt, hipStream_t stream, bool gate_up = false);
 
 // quant.hip: group-affine quantizer + bit packer (the format's producer).
 struct QuantArgs {

@@ -89,6 +89,7 @@ constexpr int W_OFF = NSTAGE * TILE;
 template <int BITS> constexpr int SZ_OFF = W_OFF + 2 * WGeo<BITS>::BUF;
 template <int BITS> constexpr int LDS_BYTES = SZ_OFF<BITS> + 2 * SZ_BUF;
 static_assert(LDS_BYTES<4> <= 160 * 1024, "LDS budget");
+static_assert(6 * 4 * 64 * 64 <= W_OFF, "the epilogue's exchanges fit the activation slots");
 
 __device__ __forceinline__ int swz(int r) { return r & (APR - 1); }
 
@@ -130,7 +131,8 @@ constexpr int OOR = 0x7FFFFFF0;
 // offsets are fixed; the stage / block / window offset is a scalar.
 template <int BITS>
 struct Loads {
-    __amdgpu_buffer_rsrc_t ar, wr, szr;
+    __amdgpu_buffer_rsrc_t ar, szr;
+    __amdgpu_buffer_rsrc_t wr[WGeo<BITS>::W_Q];   // per weight instruction (gate-up: gate or up)
     int avoff[A_Q];
     int atoff[A_Q];
     int woff[WGeo<BITS>::W_Q];
@@ -138,14 +140,26 @@ struct Loads {
     uint32_t a_lds, w_lds, sz_lds;   // LDS byte of the wave's first instruction in a slot / buffer
 };
 
-template <int BITS>
+// Gate-up (GU): the tile's rows 0..63 are gate rows n0 .. n0 + 63, rows 64..127 the up rows
+// of the same outputs.  A weight block's pieces of rows 0..63 fill exactly PPR of its
+// instructions (64 rows x PPR pieces), so every instruction reads one tensor; window
+// instruction v covers rows 32 (v & 3) .. +31, so waves 0, 1, 4, 5 read the gate's scales
+// and zeros and waves 2, 3, 6, 7 the up's.
+template <int BITS, bool GU>
 __device__ __forceinline__ void loads_setup(const GemmArgs& A, int m0, int n0, int nst, int wave, int lane,
                                             Loads<BITS>& L) {
     using G = WGeo<BITS>;
     L.ar = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * 2, 0x00020000);
-    L.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(A.w), (short)0, A.N * A.wpr * 4, 0x00020000);
-    L.szr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(SZ_Q * wave >= 4 ? A.z : A.s), (short)0,
-                                              A.N * A.G * 2, 0x00020000);
+    const bool up_sz = GU && (wave & 3) >= 2;
+    L.szr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(SZ_Q * wave >= 4 ? (up_sz ? A.z2 : A.z) : (up_sz ? A.s2 : A.s)), (short)0,
+        A.N * A.G * 2, 0x00020000);
+#pragma unroll
+    for (int t = 0; t < G::W_Q; ++t) {
+        const bool up_w = GU && G::W_Q * wave + t >= G::PPR;
+        L.wr[t] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(up_w ? A.w2 : A.w), (short)0,
+                                                    A.N * A.wpr * 4, 0x00020000);
+    }
 #pragma unroll
     for (int i = 0; i < A_Q; ++i) {
         const int q = 64 * (A_Q * wave + i) + lane;
@@ -159,13 +173,15 @@ __device__ __forceinline__ void loads_setup(const GemmArgs& A, int m0, int n0, i
     for (int t = 0; t < G::W_Q; ++t) {
         const int q = 64 * (G::W_Q * wave + t) + lane;
         const int r = min(q / G::PPR, BN - 1), p = q - (q / G::PPR) * G::PPR;
-        L.woff[t] = ((min(n0 + r, A.N - 1) * A.wpr * 4) & ~15) + 16 * p;
+        const int rr = GU ? (r & 63) : r;
+        L.woff[t] = ((min(n0 + rr, A.N - 1) * A.wpr * 4) & ~15) + 16 * p;
     }
 #pragma unroll
     for (int t = 0; t < SZ_Q; ++t) {
         const int q = 64 * (SZ_Q * wave + t) + lane;
         const int r = (q >> 1) & (BN - 1), p = q & 1;
-        L.szoff[t] = ((min(n0 + r, A.N - 1) * A.G) & ~7) * 2 + 16 * p;
+        const int rr = GU ? (r & 63) : r;
+        L.szoff[t] = ((min(n0 + rr, A.N - 1) * A.G) & ~7) * 2 + 16 * p;
     }
     L.a_lds = A_OFF + A_Q * wave * 1024;
     L.w_lds = W_OFF + G::W_Q * wave * 1024;
@@ -221,7 +237,7 @@ __device__ __forceinline__ void issue_slot(const Loads<BITS>& L, const Group& g,
         dma16(L.ar, lds, g.a_dst + k * 1024, TAIL && g.a_tail ? L.atoff[k] : L.avoff[k], g.a_soff);
     } else if constexpr (EVEN) {
         const int e = k - A_Q;
-        if (e < WQ) dma16(L.wr, lds, g.w_dst + e * 1024, L.woff[e], g.w_soff);
+        if (e < WQ) dma16(L.wr[e], lds, g.w_dst + e * 1024, L.woff[e], g.w_soff);
         else if (e < WQ + SZ_Q) dma16(L.szr, lds, g.sz_dst + (e - WQ) * 1024, L.szoff[e - WQ], g.sz_soff);
     }
 }
@@ -266,8 +282,8 @@ struct ZScan {
     u4 v[SCAN_U];
 };
 
-__device__ __forceinline__ void scan_issue(const GemmArgs& A, int c0, int lane, ZScan& zs) {
-    const uint16_t* z = reinterpret_cast<const uint16_t*>(A.z);
+__device__ __forceinline__ void scan_issue(const GemmArgs& A, const void* zt, int c0, int lane, ZScan& zs) {
+    const uint16_t* z = reinterpret_cast<const uint16_t*>(zt);
     const long beg = (long)c0 * A.G, end = (long)min(c0 + 32, A.N) * A.G;   // beg % 8 == 0
 #pragma unroll
     for (int u = 0; u < SCAN_U; ++u) {
@@ -277,8 +293,8 @@ __device__ __forceinline__ void scan_issue(const GemmArgs& A, int c0, int lane, 
 }
 
 template <int DT>
-__device__ __forceinline__ bool scan_finish(const GemmArgs& A, int c0, int lane, const ZScan& zs) {
-    const uint16_t* z = reinterpret_cast<const uint16_t*>(A.z);
+__device__ __forceinline__ bool scan_finish(const GemmArgs& A, const void* zt, int c0, int lane, const ZScan& zs) {
+    const uint16_t* z = reinterpret_cast<const uint16_t*>(zt);
     const long beg = (long)c0 * A.G, end = (long)min(c0 + 32, A.N) * A.G;
     bool ok = true;
 #pragma unroll
@@ -551,7 +567,10 @@ __device__ __forceinline__ void compute_loop(Ctx<BITS>& c, int nst, Group& g0, f
     }
 }
 
-template <int BITS, bool TAIL, bool GS128, int DT>
+// GU: the gate-up GEMM.  A tile covers 64 outputs n0 .. n0 + 63: slabs 0 and 1 are the
+// gate's columns n0 + 32 (slab & 1) .., slabs 2 and 3 the up's of the same outputs, so
+// each output's two sums end in one workgroup.
+template <int BITS, bool TAIL, bool GS128, int DT, bool GU>
 __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_f16_kernel(const GemmArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds_raw[];
@@ -560,14 +579,17 @@ gemm_f16_kernel(const GemmArgs A) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int slab = wave & 3, kh = wave >> 2;    // column slab, k half of every stage
     const int mtiles = (A.M + BM - 1) / BM;
-    const int m0 = (blockIdx.x % mtiles) * BM, n0 = (blockIdx.x / mtiles) * BN;
+    constexpr int TN = GU ? BN / 2 : BN;          // outputs per tile
+    const int m0 = (blockIdx.x % mtiles) * BM, n0 = (blockIdx.x / mtiles) * TN;
     const int nst = (A.K + BK - 1) / BK;
+    const bool up = GU && slab >= 2;              // the slab's tensor
+    const int c0 = n0 + (GU ? (slab & 1) : slab) * 32;   // the slab's first column
 
     // prologue: the zero scan's loads, then weight block 0, window 0 and stages 0, 1
     ZScan zs;
-    scan_issue(A, n0 + slab * 32, lane, zs);
+    scan_issue(A, up ? A.z2 : A.z, c0, lane, zs);
     Loads<BITS> L;
-    loads_setup<BITS>(A, m0, n0, nst, wave, lane, L);
+    loads_setup<BITS, GU>(A, m0, n0, nst, wave, lane, L);
     Sched sc;
     sc.nst = nst;
     sc.nblk = (nst + WBLK - 1) / WBLK;
@@ -586,9 +608,9 @@ gemm_f16_kernel(const GemmArgs A) {
     const int hk = lane >> 5;
     ColInfo ci;
     {
-        const int r = slab * 32 + r32;
-        const int col = min(n0 + r, A.N - 1);
-        const uintptr_t row = reinterpret_cast<uintptr_t>(A.w) + (uintptr_t)col * A.wpr * 4;
+        const int r = slab * 32 + r32;            // the column's row of the tile's weight buffers
+        const int col = min(c0 + r32, A.N - 1);
+        const uintptr_t row = reinterpret_cast<uintptr_t>(up ? A.w2 : A.w) + (uintptr_t)col * A.wpr * 4;
         ci.cix = 2 * hk + kh;
         ci.wlane = W_OFF + r * WGeo<BITS>::PITCH + (int)(row & 15) + ci.cix * (4 * BITS);
         ci.cg = (long)col * A.G;
@@ -598,7 +620,7 @@ gemm_f16_kernel(const GemmArgs A) {
         for (int kq = 0; kq < KSTEPS; ++kq)
             ci.aaddr[kq] = A_OFF + r32 * APR * 16 + 16 * ((8 * hk + KSTEPS * kh + kq) ^ swz(r32));
     }
-    const bool fast = scan_finish<DT>(A, n0 + slab * 32, lane, zs);
+    const bool fast = scan_finish<DT>(A, up ? A.z2 : A.z, c0, lane, zs);
 
     f16x acc[4];
 #pragma unroll
@@ -630,13 +652,43 @@ gemm_f16_kernel(const GemmArgs A) {
         for (int a = 0; a < 4; ++a) *reinterpret_cast<lacc*>(red + a * 64 * 64) = acc[a];
     }
     barrier_lds();
-    if (kh == 1) return;
+    if (!GU && kh == 1) return;
+    if (kh == 0) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a) acc[a] += *reinterpret_cast<lacc*>(red + a * 64 * 64);
+        for (int a = 0; a < 4; ++a) acc[a] += *reinterpret_cast<lacc*>(red + a * 64 * 64);
+    }
 
     // D layout of a 32x32 block: lane (j = lane & 31, h = lane >> 5), register
     // 4q + r holds row 8q + 4h + r, column j
-    const int n = n0 + slab * 32 + r32;
+    const int n = c0 + r32;
+    if constexpr (GU) {
+        // the up slabs hand RN(x . U^T) to the gate slabs of the same columns (LDS past
+        // the partial sums); every wave meets the barrier
+        lds_t* xu = lds + 4 * (4 * 64 * 64) + (slab & 1) * (4 * 64 * 64) + lane * 64;
+        if (kh == 0 && up) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[a][v] = Dt<DT>::to_f(Dt<DT>::from_f(acc[a][v]));
+                *reinterpret_cast<lacc*>(xu + a * 64 * 64) = acc[a];
+            }
+        }
+        barrier_lds();
+        if (kh == 1 || up || n >= A.N) return;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const f16x u = *reinterpret_cast<lacc*>(xu + a * 64 * 64);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + 32 * a + 8 * (v >> 2) + 4 * hk + (v & 3);
+                // silu(x G^T) rounded, times the rounded up factor: both products of two
+                // dtype values are exact in fp32, so the store rounds once
+                const float g = Dt<DT>::to_f(Dt<DT>::from_f(silu(acc[a][v] + 0.f)));
+                if (m < A.M) store_f<DT>(A.out, (long)m * A.N + n, g * u[v]);
+            }
+        }
+        return;
+    }
     if (n >= A.N) return;
     const float bias = A.b ? load_f<DT>(A.b, n) : 0.f;
 #pragma unroll
@@ -649,18 +701,24 @@ gemm_f16_kernel(const GemmArgs A) {
     }
 }
 
-template <int BITS, int DT>
+template <int BITS, int DT, bool GU>
 const void* kernel_for(bool tail, bool gs128) {
-    return tail ? (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, true, DT>)
-                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, false, DT>))
-                : (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, true, DT>)
-                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, false, DT>));
+    return tail ? (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, true, DT, GU>)
+                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, true, false, DT, GU>))
+                : (gs128 ? reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, true, DT, GU>)
+                       : reinterpret_cast<const void*>(&gemm_f16_kernel<BITS, false, false, DT, GU>));
 }
 
-template <int DT>
+template <int DT, bool GU>
 const void* kernel_for_bits(int bits, bool tail, bool gs128) {
-    return bits == 2 ? kernel_for<2, DT>(tail, gs128)
-                     : (bits == 3 ? kernel_for<3, DT>(tail, gs128) : kernel_for<4, DT>(tail, gs128));
+    return bits == 2 ? kernel_for<2, DT, GU>(tail, gs128)
+                     : (bits == 3 ? kernel_for<3, DT, GU>(tail, gs128) : kernel_for<4, DT, GU>(tail, gs128));
+}
+
+template <bool GU>
+const void* kernel_for_dt(int dt, int bits, bool tail, bool gs128) {
+    return dt == DT_BF16 ? kernel_for_bits<DT_BF16, GU>(bits, tail, gs128)
+                         : kernel_for_bits<DT_F16, GU>(bits, tail, gs128);
 }
 
 }  // namespace
@@ -672,18 +730,20 @@ bool gemm_f16_supported(const GemmArgs& A) {
     // within the 32-bit range of a buffer descriptor
     const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const long lim = 0x7FFFFFFF;                 // buffer offsets and ranges are 32-bit
-    return A.K % 8 == 0 && A.K >= 8 && A.gs % 32 == 0 && al16(A.x) && al16(A.w) && al16(A.s) && al16(A.z) &&
+    const bool up_ok = !A.w2 || (al16(A.w2) && al16(A.s2) && al16(A.z2));
+    return A.K % 8 == 0 && A.K >= 8 && A.gs % 32 == 0 && al16(A.x) && al16(A.w) && al16(A.s) && al16(A.z) && up_ok &&
            (long)A.M * A.K * 2 < lim && (long)A.N * A.wpr * 4 < lim && (long)A.N * A.G * 2 < lim;
 }
 
-hipError_t launch_gemm_f16(const GemmArgs& A, int dt, hipStream_t stream) {
+hipError_t launch_gemm_f16(const GemmArgs& A, int dt, hipStream_t stream, bool gate_up) {
     const bool tail = A.K % BK != 0, gs128 = A.gs == 128;
-    const void* f = dt == DT_BF16 ? kernel_for_bits<DT_BF16>(A.bits, tail, gs128)
-                                  : kernel_for_bits<DT_F16>(A.bits, tail, gs128);
+    const void* f = gate_up ? kernel_for_dt<true>(dt, A.bits, tail, gs128)
+                            : kernel_for_dt<false>(dt, A.bits, tail, gs128);
     const int lds = A.bits == 2 ? LDS_BYTES<2> : (A.bits == 3 ? LDS_BYTES<3> : LDS_BYTES<4>);
     hipError_t e = lds_limit_raise(f, lds);
     if (e != hipSuccess) return e;
-    const int tiles = ((A.M + BM - 1) / BM) * ((A.N + BN - 1) / BN);
+    const int tn = gate_up ? BN / 2 : BN;
+    const int tiles = ((A.M + BM - 1) / BM) * ((A.N + tn - 1) / tn);
     void* args[] = {const_cast<GemmArgs*>(&A)};
     return launch(f, dim3(tiles), dim3(THREADS), args, (size_t)lds, stream);
 }

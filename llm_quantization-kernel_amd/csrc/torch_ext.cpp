@@ -182,6 +182,38 @@ Tensor fused_gate_up(const Tensor& x, const Tensor& wg, const Tensor& sg, const 
     return out;
 }
 
+// Prefill gate-up: silu(x G^T) * (x U^T) with each factor rounded to x's dtype, in one
+// launch where the 16-bit matrix-core GEMM takes the call, else two GEMMs and a product.
+Tensor packed_gemm_gate_up(const Tensor& x, const Tensor& wg, const Tensor& sg, const Tensor& zg, const Tensor& wu,
+                           const Tensor& su, const Tensor& zu, int64_t bits, int64_t in_features,
+                           int64_t group_size) {
+    check_x(x, in_features);
+    check_weight(x, wg, sg, zg, bits, in_features, group_size, "packed_gemm_gate_up(gate)");
+    check_weight(x, wu, su, zu, bits, in_features, group_size, "packed_gemm_gate_up(up)");
+    TORCH_CHECK(wg.sizes() == wu.sizes(), "gate/up packed shapes must match");
+    const int64_t N = wg.size(0), M = x.size(0);
+    Tensor out = at::empty({M, N}, x.options());
+    if (M == 0) return out;
+    const int dev = x.get_device();
+    const int rc = cbk_packed_gemm_gate_up(x.data_ptr(), dtype_of(x.scalar_type()), M, in_features,
+                                           wg.data_ptr<int32_t>(), sg.data_ptr(), zg.data_ptr(),
+                                           wu.data_ptr<int32_t>(), su.data_ptr(), zu.data_ptr(), N, (int)bits,
+                                           (int)group_size, out.data_ptr(), dev, stream_of(dev));
+    if (rc != CBK_ENOTSUP) {
+        ok(rc);
+        return out;
+    }
+    ok(cbk_packed_gemm(x.data_ptr(), dtype_of(x.scalar_type()), M, in_features, wg.data_ptr<int32_t>(),
+                       sg.data_ptr(), zg.data_ptr(), nullptr, N, (int)bits, (int)group_size, CBK_ACT_SILU, 1,
+                       out.data_ptr(), dev, stream_of(dev)));
+    Tensor u = at::empty({M, N}, x.options());
+    ok(cbk_packed_gemm(x.data_ptr(), dtype_of(x.scalar_type()), M, in_features, wu.data_ptr<int32_t>(),
+                       su.data_ptr(), zu.data_ptr(), nullptr, N, (int)bits, (int)group_size, CBK_ACT_NONE, 1,
+                       u.data_ptr(), dev, stream_of(dev)));
+    out.mul_(u);
+    return out;
+}
+
 // ``bits`` is one width (the reference's signature) or a (q, k, v) sequence of widths.
 std::vector<Tensor> fused_qkv(const Tensor& x, const Tensor& wq, const Tensor& sq, const Tensor& zq, const OptT& bq,
                               const Tensor& wk, const Tensor& sk, const Tensor& zk, const OptT& bk, const Tensor& wv,
@@ -363,6 +395,8 @@ PYBIND11_MODULE(_ext, m) {
     m.def("packed_gemv", &packed_gemv, "Packed W2/W3/W4 decode GEMV (streaming, split-K by plan)");
     m.def("packed_gemm", &packed_gemm, "Packed W2/W3/W4 prefill GEMM (MFMA fp16/bf16, VALU fp32)");
     m.def("fused_gate_up", &fused_gate_up, "Fused gate/up decode GEMV with SiLU gating");
+    m.def("packed_gemm_gate_up", &packed_gemm_gate_up,
+          "Prefill gate-up: silu(x G^T) * (x U^T), one MFMA launch for fp16/bf16 x");
     m.def("fused_qkv", &fused_qkv, "Fused Q/K/V decode GEMV (GQA widths, biases, optional in-kernel RoPE)");
     m.def("sm_count", &sm_count, "Compute units of the current device");
     m.def("tile_n", &tile_n, "Virtual output rows per decode job tile (B_N of the underfill rule)");

@@ -5,7 +5,8 @@ numpy cores computed in float64 (a stricter checker than the reference's fp32
 einsum; parity with the HIP kernels is tolerance-based, see the tests).
 
 The module exposes the HIP backend's function names and argument order
-(packed_gemv, packed_gemm, fused_gate_up, fused_qkv, sm_count, tile_n, max_rho),
+(packed_gemv, packed_gemm, fused_gate_up, fused_qkv, sm_count, tile_n, max_rho, and
+packed_gemm_gate_up),
 taking and returning torch CPU tensors, so tests can inject it with
 ``crispybits_kernels.ops.set_backend(oracle.emulator)`` to exercise the host
 logic of ops.py / integration.py without a GPU.  Product code never imports it.
@@ -241,3 +242,12 @@ def packed_gemm(x, packed, scales, zeros, bias, bits, K, gs, act, use_tensor_cor
     W = gemm_weight64(packed.cpu().numpy(), _np(scales), _np(zeros), bits, K, gs, x.dtype, use_tensor_cores)
     y = _np(x) @ W.T + _bias64(bias, packed.shape[0])[None]
     return _out(act64(y, int(act)), x)
+
+
+def packed_gemm_gate_up(x, wg, sg, zg, wu, su, zu, bits, K, gs):
+    """The reference's prefill gate-up (ops.py:216-220): the gate GEMM with SiLU and the up
+    GEMM, each stored in x's dtype, multiplied in that dtype."""
+    assert wg.shape == wu.shape
+    g = packed_gemm(x, wg, sg, zg, None, bits, K, gs, 2, True)
+    u = packed_gemm(x, wu, su, zu, None, bits, K, gs, 0, True)
+    return g * u

@@ -28,6 +28,7 @@ SIGS = {
                                  _P, _P, _P, _P, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _L,
                                  _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "cbk_packed_gemm": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _L, _I, _I, _I, _I, _P, _I, _P]),
+    "cbk_packed_gemm_gate_up": (_I, [_P, _I, _L, _L, _P, _P, _P, _P, _P, _P, _L, _I, _I, _P, _I, _P]),
     "cbk_unpack_codes": (_I, [_P, _L, _L, _I, _P, _I, _P]),
     "cbk_quantize_pack": (_I, [_P, _I, _L, _L, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
     "cbk_timer_start": (_I, [_I]),

@@ -40,7 +40,8 @@ def test_op_module_binds_the_reference_functions():
     import torch
     from crispybits_kernels import _C
     for name in ("packed_gemv", "packed_gemm", "fused_gate_up", "fused_qkv", "sm_count", "tile_n", "max_rho",
-                 "unpack_codes", "quantize_pack", "decode_plan", "timer_start", "timer_stop", "stream_probe"):
+                 "packed_gemm_gate_up", "unpack_codes", "quantize_pack", "decode_plan", "timer_start",
+                 "timer_stop", "stream_probe"):
         assert callable(getattr(_C, name)), name
     x = torch.zeros(1, 256)
     w = torch.zeros(4, 32, dtype=torch.int32)
@@ -98,6 +99,34 @@ def test_gemm_and_unpack_argument_errors():
     assert "group_size" in _err()
     assert lib.cbk_unpack_codes(ALIGNED, 4, 64, 1, ALIGNED, 0, None) == 1
     assert "bits" in _err()
+
+
+def _gate_up(**kw):
+    a = dict(x=ALIGNED, dtype=0, M=4, K=256, pg=ALIGNED, sg=ALIGNED, zg=ALIGNED, pu=ALIGNED, su=ALIGNED,
+             zu=ALIGNED, N=64, bits=4, gs=128, out=ALIGNED, device=0, stream=None)
+    a.update(kw)
+    return _lib().cbk_packed_gemm_gate_up(*a.values())
+
+
+@pytest.mark.parametrize("kw,rc,msg", [
+    (dict(bits=5), 1, "bits must be 2/3/4"),
+    (dict(pu=None), 1, "packed_gemm_gate_up(up): packed/scales/zeros must be non-null"),
+    (dict(gs=48), 1, "group_size must be a positive multiple of 32"),
+    (dict(out=None), 1, "out must be non-null"),
+    (dict(dtype=2), 3, "x must be fp16 or bf16"),
+    (dict(K=260), 3, "K % 8 == 0"),
+    (dict(x=ALIGNED + 8), 3, "16-byte aligned"),
+    (dict(bits=2, zu=ALIGNED + 2), 3, "16-byte aligned"),
+])
+def test_gemm_gate_up_argument_errors(kw, rc, msg):
+    """Invalid arguments are CBK_EINVAL; calls the one-launch kernel cannot take are
+    CBK_ENOTSUP (the op binding then runs two GEMMs and a product); neither launches."""
+    assert _gate_up(**kw) == rc
+    assert msg in _err()
+
+
+def test_gemm_gate_up_empty_batch_is_a_no_op():
+    assert _gate_up(M=0) == 0
 
 
 @pytest.mark.parametrize("kw,msg", [

@@ -66,13 +66,32 @@ def test_decode_threshold_boundary(emu, monkeypatch):
 def test_fused_gate_up_decode_and_prefill(emu):
     g, Gd, _ = make(96, 256, 3, torch.float32, emu, seed=1)
     u, Ud, _ = make(96, 256, 3, torch.float32, emu, seed=2)
-    for M in (1, 12):
+    for M in (1, 12, ops.DECODE_THRESHOLD + 4):
         x = torch.randn(M, 256)
         ref = torch.nn.functional.silu(x @ Gd.T) * (x @ Ud.T)
         close(fused_gate_up(x, g, u, 2, 1), ref, torch.float32)
     g2, _, _ = make(96, 256, 2, torch.float32, emu)
     with pytest.raises(ValueError):
         fused_gate_up(torch.randn(1, 256), g2, u)
+
+
+def test_fused_gate_up_prefill_on_a_seven_function_backend(emu):
+    """A backend with only the reference's seven _C functions (its emulator, say) takes the
+    two-GEMM prefill sequence; the result equals the one-call path of this package's oracle."""
+    import types
+    from oracle import emulator
+    g, _, _ = make(96, 256, 4, torch.float16, emu, seed=1)
+    u, _, _ = make(96, 256, 4, torch.float16, emu, seed=2)
+    x = torch.randn(ops.DECODE_THRESHOLD + 3, 256).half()
+    full = fused_gate_up(x, g, u)
+    seven = types.SimpleNamespace(**{n: getattr(emulator, n) for n in (
+        "packed_gemv", "packed_gemm", "fused_gate_up", "fused_qkv", "sm_count", "tile_n", "max_rho",
+        "decode_plan")})
+    ops.set_backend(seven)
+    try:
+        assert torch.equal(fused_gate_up(x, g, u), full)
+    finally:
+        ops.set_backend(emulator)
 
 
 def _rope_tables(M, head_dim, device):
