@@ -505,6 +505,9 @@ def trace_summary(trace_csv, bench_json, untraced_json=None, steps=50, warmup=5)
             i += 6 * j["copies"]
         assert i == len(b), (i, len(b))
         return
+    if "gemm" in line and "gemv_sweep" not in line:
+        gemm_trace_tables(rows, line, key, dur)
+        return
     # the timed replays: the last run of steps x 96 decode launches whose (kernel, grid, block)
     # keys repeat with period 3 (the eager run and warm-up replays before it have the same keys;
     # the roofline's per-shape graphs after it do not)
@@ -516,7 +519,15 @@ def trace_summary(trace_csv, bench_json, untraced_json=None, steps=50, warmup=5)
             break
     else:
         raise SystemExit("timed region not found")
-    timed = seg
+    # the roofline's first per-shape graph replays one key 32 times, and its first launches
+    # continue the period: the timed run ends before the first two consecutive launches of one
+    # key (inside the timed run every launch differs from the next)
+    for p in range(i, min(i + n, len(rows) - 1)):
+        if key(rows[p]) == key(rows[p + 1]):
+            i = p - n
+            break
+    timed = rows[i:i + n]
+    assert all(key(timed[j]) == key(timed[j % 3]) for j in range(n)) and len(timed) == n
     d = [dur(r) for r in timed]
     kms = sum(d) / steps / 1e6
     span = (int(timed[-1]["End_Timestamp"]) - int(timed[0]["Start_Timestamp"])) / steps / 1e6
@@ -539,6 +550,37 @@ def trace_summary(trace_csv, bench_json, untraced_json=None, steps=50, warmup=5)
         r0 = timed[sh]
         print(f"| {K} -> {N} | `{name(r0)}` | {r0['Grid_Size_X']} | {r0['Workgroup_Size_X']} | {len(ds)} | "
               f"{statistics.mean(ds):.0f} | {min(ds)} | {max(ds)} |")
+
+
+def gemm_trace_tables(rows, line, key, dur):
+    """Per row of a `--sweeps gemm` run (gemm_sweep's order), the kernel durations of its timed
+    graph replays: a plain row makes 29 launches of one kernel and grid (the gate's call, the
+    untimed call, the warm replay, 5 replays of 4), the last 20 timed; a gate-up row makes 22
+    gate-up launches (the gate's call, then 3 + 3 + 5 x 3), the last 15 timed, then 42 plain
+    GEMM launches for the two-GEMM sequence (6 + 6 + 5 x 6), the last 30 timed."""
+    import itertools
+    import re
+    g = [r for r in rows if "gemm_f16_kernel" in r["Kernel_Name"]]
+    runs = [list(v) for _, v in itertools.groupby(g, key=key)]
+    tpl = lambda r: re.search(r"gemm_f16_kernel<([^>]*)>", r["Kernel_Name"]).group(1)
+    print("| M | K | N | width | kernel | grid (threads) | block | launches timed | avg ns | min ns | max ns "
+          "| TFLOP/s | graph-replay us (bench line) |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|---|---|")
+    i = 0
+    for j in line["gemm"]:
+        gu = j.get("kind") == "gate_up"
+        parts = [(runs[i], 22, 15), (runs[i + 1], 42, 30)] if gu else [(runs[i], 29, 20)]
+        i += len(parts)
+        for n, (run, total, timed) in enumerate(parts):
+            assert len(run) == total, (j, len(run), total)
+            t = [dur(r) for r in run[-timed:]]
+            flop = 2.0 * j["M"] * j["K"] * (2 * j["N"][0] if gu and n == 0 else (j["N"][0] if gu else j["N"]))
+            nn = f"2 x {j['N'][0]}" if gu and n == 0 else (f"{j['N'][0]} (x 2)" if gu else j["N"])
+            us = j["us"] if n == 0 else j["two_gemms_and_mul_us"]
+            print(f"| {j['M']} | {j['K']} | {nn} | W{j['bits']} | `gemm_f16_kernel<{tpl(run[0])}>` | "
+                  f"{run[0]['Grid_Size_X']} | {run[0]['Workgroup_Size_X']} | {timed} | {statistics.mean(t):.0f} | "
+                  f"{min(t)} | {max(t)} | {flop / (statistics.mean(t) * 1e-9) / 1e12:.0f} | {us} |")
+    assert i == len(runs), (i, len(runs))
 
 
 def read_traffic():
@@ -1064,6 +1106,35 @@ def gemm_sweep(torch, C, ops, dev, gate):
                              "pct_peak": round(100 * tfs / MFMA_F16_PEAK_TFS, 1)})
                 log(f"gemm M={M} K={K} N={N} W{bits}: {us:.1f} us {tfs:.1f} TFLOP/s")
                 del ws
+    # the Llama-2-7B MLP's gate-up at the prefill batches: one launch (ops.fused_gate_up)
+    # against the two GEMMs and the product it replaces, over 3 copies of the pair
+    K, N = STACK_H, STACK_I
+    for M in (1024, 2048):
+        x = randx(torch, M, K, 1, dev)
+        for bits in (4, 3, 2):
+            g0, u0 = make_weight(torch, N, K, bits, 4, dev), make_weight(torch, N, K, bits, 5, dev)
+            pairs = [(g0, u0)] + [(clone_weight(g0), clone_weight(u0)) for _ in range(2)]
+            r = gate.rows(M)
+            ref = gate.linear64(x, g0, r, round_w=x.dtype, act="silu") * gate.linear64(x, u0, r, round_w=x.dtype)
+            gate.check(f"gemm gate-up W{bits} M={M}", ops.fused_gate_up(x, g0, u0), ref, r)
+            gate.clear()
+
+            def two():
+                out = []
+                for g, u in pairs:
+                    y = C.packed_gemm(x, g.packed, g.scales, g.zeros, None, bits, K, 128, ops.ACT["silu"], True)
+                    out.append(y.mul_(C.packed_gemm(x, u.packed, u.scales, u.zeros, None, bits, K, 128,
+                                                    ops.ACT["none"], True)))
+                return out
+
+            us = graph_launch_us(torch, lambda: [ops.fused_gate_up(x, g, u) for g, u in pairs], len(pairs), replays=5)
+            us2 = graph_launch_us(torch, two, len(pairs), replays=5)
+            tfs = 2.0 * M * 2 * N * K / (us * 1e-6) / 1e12
+            rows.append({"M": M, "K": K, "N": [N, N], "bits": bits, "kind": "gate_up", "us": round(us, 2),
+                         "TFLOPs": round(tfs, 1), "pct_peak": round(100 * tfs / MFMA_F16_PEAK_TFS, 1),
+                         "two_gemms_and_mul_us": round(us2, 2)})
+            log(f"gemm gate-up M={M} W{bits}: {us:.1f} us (two GEMMs + mul {us2:.1f} us)")
+            del pairs, g0, u0
     return rows
 
 

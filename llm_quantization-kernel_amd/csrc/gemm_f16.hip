@@ -52,6 +52,7 @@ typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef __bf16 b2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16x __attribute__((ext_vector_type(16)));
+typedef float f4x __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -89,7 +90,10 @@ constexpr int W_OFF = NSTAGE * TILE;
 template <int BITS> constexpr int SZ_OFF = W_OFF + 2 * WGeo<BITS>::BUF;
 template <int BITS> constexpr int LDS_BYTES = SZ_OFF<BITS> + 2 * SZ_BUF;
 static_assert(LDS_BYTES<4> <= 160 * 1024, "LDS budget");
-static_assert(6 * 4 * 64 * 64 <= W_OFF, "the epilogue's exchanges fit the activation slots");
+// Epilogue: the kh = 1 partial sums at 0 (64 KB), the tile's fp32 sums from SUM_OFF.
+constexpr int SUM_OFF = 4 * 4 * 64 * 64;
+constexpr int SUM_PITCH = BN + 8;
+static_assert(SUM_OFF + BM * SUM_PITCH * 4 <= LDS_BYTES<2> && LDS_BYTES<2> <= LDS_BYTES<3>, "epilogue LDS");
 
 __device__ __forceinline__ int swz(int r) { return r & (APR - 1); }
 
@@ -253,6 +257,12 @@ template <int BITS, bool EVEN>
 __device__ __forceinline__ void wait_group() {
     if constexpr (EVEN) vmcnt<A_Q + WGeo<BITS>::W_Q + SZ_Q>();
     else vmcnt<A_Q>();
+}
+
+// The 16 storage bits of v rounded to the output dtype.
+template <int DT>
+__device__ __forceinline__ uint32_t raw16(float v) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, Dt<DT>::from_f(v));
 }
 
 __device__ __forceinline__ _Float16 half_of(uint32_t v) {
@@ -652,51 +662,73 @@ gemm_f16_kernel(const GemmArgs A) {
         for (int a = 0; a < 4; ++a) *reinterpret_cast<lacc*>(red + a * 64 * 64) = acc[a];
     }
     barrier_lds();
-    if (!GU && kh == 1) return;
+    // the kh = 0 waves add the partials and write the tile's sums row-major (fp32, pitch
+    // SUM_PITCH: 4 pitches = 32 banks apart, so the two row groups a store instruction
+    // touches hit distinct banks); tile column slab * 32 + r32 -- for GU the gate's 64
+    // columns, then the up's
+    typedef __attribute__((address_space(3))) float lf;
+    lf* sums = reinterpret_cast<lf*>(lds + SUM_OFF);
     if (kh == 0) {
 #pragma unroll
-        for (int a = 0; a < 4; ++a) acc[a] += *reinterpret_cast<lacc*>(red + a * 64 * 64);
-    }
-
-    // D layout of a 32x32 block: lane (j = lane & 31, h = lane >> 5), register
-    // 4q + r holds row 8q + 4h + r, column j
-    const int n = c0 + r32;
-    if constexpr (GU) {
-        // the up slabs hand RN(x . U^T) to the gate slabs of the same columns (LDS past
-        // the partial sums); every wave meets the barrier
-        lds_t* xu = lds + 4 * (4 * 64 * 64) + (slab & 1) * (4 * 64 * 64) + lane * 64;
-        if (kh == 0 && up) {
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[a][v] = Dt<DT>::to_f(Dt<DT>::from_f(acc[a][v]));
-                *reinterpret_cast<lacc*>(xu + a * 64 * 64) = acc[a];
-            }
-        }
-        barrier_lds();
-        if (kh == 1 || up || n >= A.N) return;
-#pragma unroll
         for (int a = 0; a < 4; ++a) {
-            const f16x u = *reinterpret_cast<lacc*>(xu + a * 64 * 64);
+            acc[a] += *reinterpret_cast<lacc*>(red + a * 64 * 64);
+            // D layout of a 32x32 block: lane (j = lane & 31, h = lane >> 5), register
+            // 4q + r holds row 8q + 4h + r, column j
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = m0 + 32 * a + 8 * (v >> 2) + 4 * hk + (v & 3);
-                // silu(x G^T) rounded, times the rounded up factor: both products of two
-                // dtype values are exact in fp32, so the store rounds once
-                const float g = Dt<DT>::to_f(Dt<DT>::from_f(silu(acc[a][v] + 0.f)));
-                if (m < A.M) store_f<DT>(A.out, (long)m * A.N + n, g * u[v]);
-            }
+            for (int v = 0; v < 16; ++v)
+                sums[(32 * a + 8 * (v >> 2) + 4 * hk + (v & 3)) * SUM_PITCH + slab * 32 + r32] = acc[a][v];
         }
-        return;
     }
-    if (n >= A.N) return;
-    const float bias = A.b ? load_f<DT>(A.b, n) : 0.f;
+    barrier_lds();
+
+    // every thread finishes runs of 8 consecutive outputs of a row: 16-byte stores when the
+    // output's rows are 16-byte aligned, else element stores
+    const bool vec = (reinterpret_cast<uintptr_t>(A.out) & 15) == 0 && (A.N & 7) == 0;
+    constexpr int RUNS = TN / 8;                  // runs per tile row
+    constexpr int ROWS = THREADS / RUNS;          // tile rows per pass
+    const int tc = 8 * (tid % RUNS);            // the thread's first tile column
+    const int n = n0 + tc;
+    float bias[8];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
+    for (int e = 0; e < 8; ++e) bias[e] = (!GU && A.b && n + e < A.N) ? load_f<DT>(A.b, n + e) : 0.f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int m = m0 + 32 * a + 8 * (v >> 2) + 4 * hk + (v & 3);
-            if (m < A.M) store_f<DT>(A.out, (long)m * A.N + n, apply_act(acc[a][v] + bias, A.act));
+    for (int pass = 0; pass < BM / ROWS; ++pass) {
+        const int r = pass * ROWS + tid / RUNS;
+        const int m = m0 + r;
+        typedef __attribute__((address_space(3))) const f4x lf4;
+        const f4x s0 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + tc);
+        const f4x s1 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + tc + 4);
+        float y[8];
+        if constexpr (GU) {
+            const f4x u0 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + 64 + tc);
+            const f4x u1 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + 64 + tc + 4);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                // the two GEMMs' outputs -- act(sum + 0) rounded, as a GEMM without bias forms
+                // them (signed zeros included) -- and their product: both factors are dtype
+                // values, so the product is exact in fp32 and the store rounds once
+                const float gv = Dt<DT>::to_f(Dt<DT>::from_f(silu((e < 4 ? s0[e] : s1[e - 4]) + 0.f)));
+                const float uv = Dt<DT>::to_f(Dt<DT>::from_f((e < 4 ? u0[e] : u1[e - 4]) + 0.f));
+                y[e] = gv * uv;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = apply_act((e < 4 ? s0[e] : s1[e - 4]) + bias[e], A.act);
+        }
+        if (m >= A.M) continue;
+        if (vec) {
+            if (n < A.N) {
+                uint32_t o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    o[e] = raw16<DT>(y[2 * e]) | (raw16<DT>(y[2 * e + 1]) << 16);
+                *reinterpret_cast<u4*>(reinterpret_cast<uint16_t*>(A.out) + (long)m * A.N + n) =
+                    u4{o[0], o[1], o[2], o[3]};
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (n + e < A.N) store_f<DT>(A.out, (long)m * A.N + n + e, y[e]);
         }
     }
 }

@@ -1,7 +1,7 @@
 """GPU parity of the one-launch prefill gate-up GEMM (cbk_packed_gemm_gate_up).
 
 Bars:
-  * bit-exact (torch.equal) against the sequence it replaces -- the gate GEMM with SiLU and
+  * bit-exact (every bit, signed zeros included) against the sequence it replaces -- the gate GEMM with SiLU and
     the up GEMM through cbk_packed_gemm, multiplied in the activation dtype (the reference's
     ops.py:216-220): the same dequantized weights, MFMA order and roundings;
   * against the CPU oracle (float64 products of W-hat rounded once to the dtype, each factor
@@ -61,6 +61,12 @@ def _check(y, ref, dtype):
     assert e < 1e-2
 
 
+def _same_bits(a, b):
+    """Bitwise equality (torch.equal takes -0.0 == +0.0)."""
+    iv = {2: torch.int16, 4: torch.int32}[a.element_size()]
+    return a.shape == b.shape and a.dtype == b.dtype and torch.equal(a.view(iv), b.view(iv))
+
+
 def _gate_up(x, g, u):
     return _C.packed_gemm_gate_up(x, g.packed, g.scales, g.zeros, u.packed, u.scales, u.zeros, g.bits,
                                   g.in_features, g.group_size)
@@ -86,9 +92,9 @@ def test_gate_up_gemm(hip, dtype, bits, M, K, N, gs):
     x = _x(M, K, dtype)
     y, launches = _timed_launches(lambda: _gate_up(x, g, u))
     assert launches == 1
-    assert torch.equal(y, _two_gemms(x, g, u))
+    assert _same_bits(y, _two_gemms(x, g, u))
     _check(y, _oracle(x, dg, du, bits, K, gs, dtype), dtype)
-    assert torch.equal(fused_gate_up(x, g, u), y)          # the ops path past the decode threshold
+    assert _same_bits(fused_gate_up(x, g, u), y)          # the ops path past the decode threshold
 
 
 @pytest.mark.parametrize("which", ["gate", "up"])
@@ -109,7 +115,7 @@ def test_gate_up_gemm_fractional_zeros(hip, which, bits):
     g, u = from_packed_dict(dg, "cuda", torch.float16), from_packed_dict(du, "cuda", torch.float16)
     x = _x(M, K, torch.float16)
     y = _gate_up(x, g, u)
-    assert torch.equal(y, _two_gemms(x, g, u))
+    assert _same_bits(y, _two_gemms(x, g, u))
     _check(y, _oracle(x, dg, du, bits, K, 128, torch.float16), torch.float16)
 
 
@@ -125,12 +131,12 @@ def test_gate_up_gemm_fallbacks(hip):
     assert xs.data_ptr() % 16 != 0
     y, launches = _timed_launches(lambda: _gate_up(xs, g, u))
     assert launches == 2                                   # two GEMM launches (the product is torch's)
-    assert torch.equal(y, _two_gemms(xs, g, u))
+    assert _same_bits(y, _two_gemms(xs, g, u))
     _check(y, _oracle(x, dg, du, 4, K, 128, torch.float16), torch.float16)   # another GEMM kernel's k order
     d32g, d32u = _dict(N, K, 4, torch.float32, 1), _dict(N, K, 4, torch.float32, 2)
     g32, u32 = from_packed_dict(d32g, "cuda", torch.float32), from_packed_dict(d32u, "cuda", torch.float32)
     x32 = x.float()
-    assert torch.equal(_gate_up(x32, g32, u32), _two_gemms(x32, g32, u32))
+    assert _same_bits(_gate_up(x32, g32, u32), _two_gemms(x32, g32, u32))
 
 
 def test_gate_up_gemm_empty_batch(hip):
@@ -148,6 +154,22 @@ def test_gate_up_gemm_baseline_stack_shape(hip, bits):
     g, u = from_packed_dict(dg, "cuda", torch.float16), from_packed_dict(du, "cuda", torch.float16)
     x = _x(M, K, torch.float16)
     y = _gate_up(x, g, u)
-    assert torch.equal(y, _two_gemms(x, g, u))
+    assert _same_bits(y, _two_gemms(x, g, u))
     rows = torch.tensor([0, 1, 127, 128, 1000, 2047])
     _check(y[rows.cuda()], _oracle(x[rows.cuda()], dg, du, bits, K, 128, torch.float16), torch.float16)
+
+
+def test_gate_up_gemm_signed_zero(hip):
+    """Regression: bench.py's gate-up inputs at M = 2048 (W3, weights from the device
+    producer) hold an output whose up factor is a signed zero; the one-launch epilogue must
+    form it as the up GEMM stores it (act(sum + 0) rounded), so every bit matches."""
+    import os
+    import sys
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+    dev = torch.device("cuda", 0)
+    x = bench.randx(torch, 2048, 4096, 1, dev)
+    g, u = bench.make_weight(torch, 11008, 4096, 3, 4, dev), bench.make_weight(torch, 11008, 4096, 3, 5, dev)
+    y = _gate_up(x, g, u)
+    assert _same_bits(y, _two_gemms(x, g, u))
+    assert bool((y == 0).any())

@@ -324,3 +324,87 @@ def test_fused_rope_hooks_prime_once_and_keep_the_model_exact(emu, tmp_path, mon
     with torch.no_grad():
         lb2 = block0_update(model)
     assert (la - lb2).abs().max() / la.abs().max() > 0.2, "a second rotation went unnoticed"
+
+
+def test_trace_summary_finds_the_timed_step(tmp_path, capsys):
+    """bench.py --trace-summary on a synthetic kernel trace of the default command: the eager
+    and warm-up runs and the timed replays share the step's period-3 keys, and the roofline's
+    first per-shape graph (32 launches of the first shape) continues that period for one
+    launch; the timed region ends before it and each shape gets its own kernel and grid."""
+    import csv
+    import json
+    import os
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, root)
+    import bench
+    grids = [(65536, 256, "<0, 3, 1, 8, 0>"), (176128, 256, "<0, 3, 1, 8, 0>"), (393216, 768, "<0, 3, 1, 4, 0>")]
+    durs = [4000, 6600, 7300]
+    launches = [(s, 10) for _ in range(56) for _ in range(32) for s in range(3)]     # step order: layer, shape
+    launches[-50 * 96:] = [(s, 0) for _ in range(50 * 32) for s in range(3)]          # the timed replays
+    launches += [(s, 20) for s in range(3) for _ in range(32)]                         # roofline graphs
+    path = tmp_path / "trace.csv"
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, ["Kernel_Name", "Grid_Size_X", "Workgroup_Size_X", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        t = 0
+        for s, extra in launches:
+            g, b, tpl = grids[s]
+            w.writerow({"Kernel_Name": f"void cbk::(anonymous namespace)::gemv_stream_kernel{tpl}(cbk::GemvArgs)",
+                        "Grid_Size_X": g, "Workgroup_Size_X": b, "Start_Timestamp": t,
+                        "End_Timestamp": t + durs[s] + extra})
+            t += 10000
+    line = {"ms_per_step": 0.6, "value": 1.0, "roofline": {"frac": 0.3, "avg_launch_us": 6.0,
+                                                           "bytes_per_launch_avg": 14509056}}
+    bj = tmp_path / "b.json"
+    bj.write_text(json.dumps(line) + "\n")
+    bench.trace_summary(str(path), str(bj))
+    out = capsys.readouterr().out.splitlines()
+    rows = [r for r in out if r.startswith("| 4096") or r.startswith("| 11008")]
+    assert len(rows) == 3
+    for (K, N), r, (g, b, _), d in zip(bench.SHAPES, rows, grids, durs):
+        cells = [c.strip() for c in r.strip("|").split("|")]
+        assert cells[0] == f"{K} -> {N}" and cells[2] == str(g) and cells[3] == str(b)
+        assert cells[4] == "1600" and cells[5] == str(d)              # only the timed replays
+
+
+def test_trace_summary_gemm_rows(tmp_path, capsys):
+    """bench.py --trace-summary on a synthetic trace of a `--sweeps gemm` run: each sweep row's
+    launches form one run of a kernel and grid (a gate-up row two: its own kernel, then the plain
+    GEMMs of the sequence it replaces, with elementwise kernels between them); the timed tail of
+    each run is reported."""
+    import csv
+    import json
+    import os
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, root)
+    import bench
+    plain = "void cbk::(anonymous namespace)::gemm_f16_kernel<4, false, true, 0, false>(cbk::GemmArgs)"
+    gu = "void cbk::(anonymous namespace)::gemm_f16_kernel<4, false, true, 0, true>(cbk::GemmArgs)"
+    seq = [(plain, 131072, 50000 if i >= 9 else 60000) for i in range(29)]
+    seq += [(gu, 704512, 200000 if i >= 7 else 250000) for i in range(22)]
+    for i in range(42):
+        seq.append((plain, 352256, 100000 if i >= 12 else 130000))
+        seq.append(("void at::native::elementwise_kernel<128, 4>(int, float)", 4096, 9000))
+    path = tmp_path / "trace.csv"
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, ["Kernel_Name", "Grid_Size_X", "Workgroup_Size_X", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        t = 0
+        for name, grid, d in seq:
+            w.writerow({"Kernel_Name": name, "Grid_Size_X": grid, "Workgroup_Size_X": 512, "Start_Timestamp": t,
+                        "End_Timestamp": t + d})
+            t += 300000
+    line = {"ms_per_step": 0.6, "value": 1.0, "roofline": {}, "gemm": [
+        {"M": 1024, "K": 4096, "N": 4096, "bits": 4, "us": 51.0},
+        {"M": 1024, "K": 4096, "N": [11008, 11008], "bits": 4, "kind": "gate_up", "us": 210.0,
+         "two_gemms_and_mul_us": 230.0}]}
+    bj = tmp_path / "b.json"
+    bj.write_text(json.dumps(line) + "\n")
+    bench.trace_summary(str(path), str(bj))
+    out = [r for r in capsys.readouterr().out.splitlines() if r.startswith("| 1024")]
+    cells = [[c.strip() for c in r.strip("|").split("|")] for r in out]
+    assert [c[7:9] for c in cells] == [["20", "50000"], ["15", "200000"], ["30", "100000"]]
+    assert cells[1][2] == "2 x 11008" and "true" in cells[1][4] and cells[2][2] == "11008 (x 2)"
+    assert cells[1][11] == str(round(2 * 1024 * 4096 * 2 * 11008 / 200e-6 / 1e12))
