@@ -90,10 +90,10 @@ constexpr int W_OFF = NSTAGE * TILE;
 template <int BITS> constexpr int SZ_OFF = W_OFF + 2 * WGeo<BITS>::BUF;
 template <int BITS> constexpr int LDS_BYTES = SZ_OFF<BITS> + 2 * SZ_BUF;
 static_assert(LDS_BYTES<4> <= 160 * 1024, "LDS budget");
-// Epilogue: the kh = 1 partial sums at 0 (64 KB), the tile's fp32 sums from SUM_OFF.
-constexpr int SUM_OFF = 4 * 4 * 64 * 64;
+// Epilogue: the two k halves' fp32 tile images, k half kh at kh * SUM_IMG.
 constexpr int SUM_PITCH = BN + 8;
-static_assert(SUM_OFF + BM * SUM_PITCH * 4 <= LDS_BYTES<2> && LDS_BYTES<2> <= LDS_BYTES<3>, "epilogue LDS");
+constexpr int SUM_IMG = BM * SUM_PITCH * 4;
+static_assert(2 * SUM_IMG <= LDS_BYTES<2> && LDS_BYTES<2> <= LDS_BYTES<3>, "epilogue LDS");
 
 __device__ __forceinline__ int swz(int r) { return r & (APR - 1); }
 
@@ -650,36 +650,24 @@ gemm_f16_kernel(const GemmArgs A) {
     else compute_loop<BITS, TAIL, GS128, DQ0>(c, nst, g0, acc);
     vmcnt<0>();                                   // the surplus loads land before the LDS is reused
 
-    // the two k halves' partial sums meet in LDS (the stage slots are free once every
-    // wave is past its last stage): the kh = 1 wave of a slab writes, the kh = 0 wave
-    // adds and stores
-    typedef __attribute__((address_space(3))) f16x lacc;
+    // both k halves write their partial sums row-major into a tile image of their own (fp32,
+    // pitch SUM_PITCH: 4 pitches = 32 banks apart, so the two row groups a store instruction
+    // touches hit distinct banks; tile column slab * 32 + r32 -- for GU the gate's 64 columns,
+    // then the up's); the stage slots and buffers are free once every wave is past its last stage
+    typedef __attribute__((address_space(3))) float lf;
     __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));    // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
-    lds_t* red = lds + slab * (4 * 64 * 64) + lane * 64;
-    if (kh == 1) {
+    lf* img = reinterpret_cast<lf*>(lds + kh * SUM_IMG);
 #pragma unroll
-        for (int a = 0; a < 4; ++a) *reinterpret_cast<lacc*>(red + a * 64 * 64) = acc[a];
+    for (int a = 0; a < 4; ++a) {
+        // D layout of a 32x32 block: lane (j = lane & 31, h = lane >> 5), register 4q + r holds
+        // row 8q + 4h + r, column j
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            img[(32 * a + 8 * (v >> 2) + 4 * hk + (v & 3)) * SUM_PITCH + slab * 32 + r32] = acc[a][v];
     }
     barrier_lds();
-    // the kh = 0 waves add the partials and write the tile's sums row-major (fp32, pitch
-    // SUM_PITCH: 4 pitches = 32 banks apart, so the two row groups a store instruction
-    // touches hit distinct banks); tile column slab * 32 + r32 -- for GU the gate's 64
-    // columns, then the up's
-    typedef __attribute__((address_space(3))) float lf;
-    lf* sums = reinterpret_cast<lf*>(lds + SUM_OFF);
-    if (kh == 0) {
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-            acc[a] += *reinterpret_cast<lacc*>(red + a * 64 * 64);
-            // D layout of a 32x32 block: lane (j = lane & 31, h = lane >> 5), register
-            // 4q + r holds row 8q + 4h + r, column j
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                sums[(32 * a + 8 * (v >> 2) + 4 * hk + (v & 3)) * SUM_PITCH + slab * 32 + r32] = acc[a][v];
-        }
-    }
-    barrier_lds();
+    const lf* sums = reinterpret_cast<const lf*>(lds);
 
     // every thread finishes runs of 8 consecutive outputs of a row: 16-byte stores when the
     // output's rows are 16-byte aligned, else element stores
@@ -696,12 +684,16 @@ gemm_f16_kernel(const GemmArgs A) {
         const int r = pass * ROWS + tid / RUNS;
         const int m = m0 + r;
         typedef __attribute__((address_space(3))) const f4x lf4;
-        const f4x s0 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + tc);
-        const f4x s1 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + tc + 4);
+        const f4x s0 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + tc) +
+                       *reinterpret_cast<lf4*>(sums + SUM_IMG / 4 + r * SUM_PITCH + tc);
+        const f4x s1 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + tc + 4) +
+                       *reinterpret_cast<lf4*>(sums + SUM_IMG / 4 + r * SUM_PITCH + tc + 4);
         float y[8];
         if constexpr (GU) {
-            const f4x u0 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + 64 + tc);
-            const f4x u1 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + 64 + tc + 4);
+            const f4x u0 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + 64 + tc) +
+                           *reinterpret_cast<lf4*>(sums + SUM_IMG / 4 + r * SUM_PITCH + 64 + tc);
+            const f4x u1 = *reinterpret_cast<lf4*>(sums + r * SUM_PITCH + 64 + tc + 4) +
+                           *reinterpret_cast<lf4*>(sums + SUM_IMG / 4 + r * SUM_PITCH + 64 + tc + 4);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 // the two GEMMs' outputs -- act(sum + 0) rounded, as a GEMM without bias forms
