@@ -105,10 +105,15 @@ __device__ __forceinline__ void vmcnt() {
 
 // Workgroup barrier without a memory fence: __syncthreads() would make the compiler
 // wait for every in-flight load of the wave (vmcnt(0)), draining the prefetch.
-// This only completes the wave's own LDS traffic (lgkmcnt(0)) before the barrier.
+// This only completes the wave's own LDS traffic (lgkmcnt(0)) before the barrier.  The
+// compiler-level memory clobbers on both sides keep LLVM from moving LDS accesses (or
+// the direct-to-LDS loads) across it: the wait and barrier intrinsics alone do not
+// order memory in the IR.
 __device__ __forceinline__ void barrier_lds() {
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));    // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // One 16-byte-per-lane direct-to-LDS buffer load into byte `dst` of the LDS.  A
@@ -655,8 +660,7 @@ gemm_f16_kernel(const GemmArgs A) {
     // touches hit distinct banks; tile column slab * 32 + r32 -- for GU the gate's 64 columns,
     // then the up's); the stage slots and buffers are free once every wave is past its last stage
     typedef __attribute__((address_space(3))) float lf;
-    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));    // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
+    barrier_lds();
     lf* img = reinterpret_cast<lf*>(lds + kh * SUM_IMG);
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
