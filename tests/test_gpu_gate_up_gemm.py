@@ -173,3 +173,47 @@ def test_gate_up_gemm_signed_zero(hip):
     y = _gate_up(x, g, u)
     assert _same_bits(y, _two_gemms(x, g, u))
     assert bool((y == 0).any())
+
+
+def test_gate_up_gemm_through_the_c_abi(hip):
+    """cbk_packed_gemm_gate_up called through ctypes (device pointers, a non-default stream)
+    writes the same bits as the op binding, and M = 0 launches nothing."""
+    import os
+    import sys
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import cabi
+    K, N, M = 768, 200, 96
+    dg, du = _dict(N, K, 3, torch.float16, 1), _dict(N, K, 3, torch.float16, 2)
+    g, u = from_packed_dict(dg, "cuda", torch.float16), from_packed_dict(du, "cuda", torch.float16)
+    x = _x(M, K, torch.float16)
+    ref = _gate_up(x, g, u)
+    out = torch.full_like(ref, float("nan"))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    rc = cabi.lib.cbk_packed_gemm_gate_up(x.data_ptr(), 0, M, K, g.packed.data_ptr(), g.scales.data_ptr(),
+                                          g.zeros.data_ptr(), u.packed.data_ptr(), u.scales.data_ptr(),
+                                          u.zeros.data_ptr(), N, 3, 128, out.data_ptr(), 0, s.cuda_stream)
+    assert rc == 0, cabi.last_error()
+    s.synchronize()
+    assert _same_bits(out, ref)
+    rc = cabi.lib.cbk_packed_gemm_gate_up(x.data_ptr(), 0, 0, K, g.packed.data_ptr(), g.scales.data_ptr(),
+                                          g.zeros.data_ptr(), u.packed.data_ptr(), u.scales.data_ptr(),
+                                          u.zeros.data_ptr(), N, 3, 128, out.data_ptr(), 0, s.cuda_stream)
+    assert rc == 0
+    s.synchronize()
+    assert _same_bits(out, ref)
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_gate_up_gemm_bf16_stack_shape(hip, bits):
+    """bf16 activations (bf16 scales and zeros) at the stack's prefill shape: bit-exact against
+    the two bf16 GEMMs and their bf16 product; oracle check on a row sample."""
+    K, N, M = 4096, 11008, 2048
+    dt = torch.bfloat16
+    dg, du = _dict(N, K, bits, dt, 21, scale=0.02), _dict(N, K, bits, dt, 22, scale=0.02)
+    g, u = from_packed_dict(dg, "cuda", dt), from_packed_dict(du, "cuda", dt)
+    x = _x(M, K, dt)
+    y = _gate_up(x, g, u)
+    assert _same_bits(y, _two_gemms(x, g, u))
+    rows = torch.tensor([0, 77, 1024, 2047])
+    _check(y[rows.cuda()], _oracle(x[rows.cuda()], dg, du, bits, K, 128, dt), dt)

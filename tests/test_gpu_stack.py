@@ -150,6 +150,31 @@ def test_llama_stack_blocks_graph_replay(hip):
         torch.cuda.synchronize()
 
 
+def test_llama_stack_blocks_prefill_graph_replay(hip):
+    """The same two blocks at a prefill batch (M = 256: the QKV, o and down GEMMs and the
+    one-launch gate-up GEMM) captured as one graph and replayed three times, with eager work
+    and synchronizations between, bit-identical to eager every time."""
+    dev = torch.device("cuda", 0)
+    bitmap = [int(b) for b in np.random.default_rng(0).choice([2, 3, 4], 32)][:2]
+    blocks = [_stack_block(i, bits, dev)[0] for i, bits in enumerate(bitmap)]
+    g = torch.Generator().manual_seed(3)
+    xh = torch.randn(256, H, generator=g).half().to(dev)
+    xi = torch.randn(256, I, generator=g).half().to(dev)
+    eager = [t.clone() for t in _step(blocks, xh, xi)]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = _step(blocks, xh, xi)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for j, (c, e) in enumerate(zip(captured, eager)):
+            assert torch.equal(c.view(torch.int16), e.view(torch.int16)), f"replay {rep}: output {j} differs"
+        _step(blocks, xh, xi)
+        torch.cuda.synchronize()
+
+
 def test_llama_stack_blocks_oracle_decode_and_prefill(hip):
     """Three blocks of the stack (config-5 bits, Llama-2-7B widths: blocks 0, 1 and 3, the first
     W4, W3 and W2 blocks of the bitmap) against the CPU oracle, the
