@@ -338,13 +338,17 @@ int bstream_rw(int64_t M, int bsu, bool gateup) {
     return rw;
 }
 
+// Waves a batched streaming workgroup may hold: 16, or 12 for bf16 with 8-unit slices (that
+// kernel is built for 768 threads, so it has 170 VGPRs).
+int bstream_max_waves(int bsu, bool bf) { return bf && bsu == 8 ? 12 : 16; }
+
 // K splits of the batched streaming kernel for slices of bsu units.
 int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu, bool bf) {
     const int64_t U = ceil_div(C, 4);
     int64_t P = std::max<int64_t>(1, std::min<int64_t>(split_k, U));
     while (P < U) {
         const int64_t ks = ceil_div(ceil_div(U, P), bsu);
-        if (ks * rw <= 16 && bstream_lds(ks, M, rw, bsu, bf) <= LDS_BUDGET) break;
+        if (ks * rw <= bstream_max_waves(bsu, bf) && bstream_lds(ks, M, rw, bsu, bf) <= LDS_BUDGET) break;
         ++P;
     }
     return (int)P;
@@ -364,7 +368,7 @@ BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu
     bp.bsu = bsu;
     bp.rw = rw;
     bp.ks = (int)ceil_div(ceil_div(U, P), bsu);
-    if (bp.ks * rw > 16) return bp;
+    if (bp.ks * rw > bstream_max_waves(bsu, bf)) return bp;
     bp.lds = (int)bstream_lds(bp.ks, A.M, rw, bsu, bf);
     if (bp.lds > LDS_BUDGET) return bp;
     const int rb = 16 * rw;
@@ -393,7 +397,6 @@ BStreamPlan bstream_fill(const GemvArgs& A, int mode, bool mixed, int P0, bool b
     int64_t best_key = INT64_MAX;
     for (int P = P0; P < P0 + BSTREAM_FILL_SPLITS; ++P) {
         for (int bsu : {4, 8}) {
-            if (bf && bsu == 8) continue;             // bf16 takes 4-unit slices (see plan_bstream)
             for (int rw = 1; rw <= 16; ++rw) {
                 const BStreamPlan c = bstream_make(A, mode, mixed, P, bsu, rw, bf);
                 if (!c.ok) continue;
@@ -416,7 +419,7 @@ BStreamPlan bstream_base(int64_t M, int64_t C, int split_k, bool gateup, bool bf
     bp.bsu = 4;
     bp.rw = bstream_rw(M, 4, gateup);
     bp.P = bstream_splits(C, M, split_k, bp.rw, 4, bf);
-    if (bp.P > std::max(split_k, 1) && !bf) {    // 4-unit slices would add a split: try 8
+    if (bp.P > std::max(split_k, 1)) {           // 4-unit slices would add a split: try 8
         const int rw8 = bstream_rw(M, 8, gateup);
         const int p8 = bstream_splits(C, M, split_k, rw8, 8, bf);
         if (p8 < bp.P) {
@@ -436,9 +439,10 @@ bool bstream_fills(const BStreamPlan& base, int64_t V) {
 BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k, int cus) {
     BStreamPlan bp;
     const int64_t lim = INT32_MAX;
-    // bf16 keeps to 4-unit slices: with 8 its per-unit prescale pushes the 1024-thread
-    // kernel past 128 VGPRs and it spills (W3 11008 -> 4096 batch 8: 22.7 us on 8-unit
-    // slices, 19.9 on 4-unit ones, 13.9 for fp16).
+    // bf16 with 8-unit slices runs a 768-thread build of the kernel (its per-unit prescale
+    // does not fit 128 VGPRs next to eight units of chunks; 170 hold it), so its plans keep to
+    // 12 waves (bstream_max_waves).  W3 11008 -> 4096 batch 8: 22.7 us on the 1024-thread
+    // build, which spilled, 19.3 on 4-unit slices, 14.8 on the 768-thread build (fp16 13.8).
     const bool bf = dtype == CBK_BF16;
     bool ok = A.M >= 3 && A.M <= 16 && (dtype == CBK_F16 || bf) && A.gs % 128 == 0 && A.K % 8 == 0 &&
               reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
@@ -461,17 +465,18 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     // blocks would give each CU 2.5 or more workgroups take 8-unit slices and the
     // fewest workgroups that still cover the CUs (W3 4096 -> 11008: batch 8 13.2 -> 11.1
     // us, batch 16 18.8 -> 14.5), and gate-up takes 8-unit slices (batch 4 20.4 -> 15.6).
-    if (bp.P == 1 && cus > 0 && !bf) {
+    if (bp.P == 1 && cus > 0) {
         const int64_t U8 = ceil_div(U, 8);
+        const int mw = bstream_max_waves(8, bf);
         if (mode == CBK_MODE_GEMV && !mixed && ceil_div(A.V, 16) >= (5 * (int64_t)cus) / 2) {
             int rw = (int)std::max<int64_t>(bstream_rw(A.M, 8, false), ceil_div(ceil_div(A.V, 16), cus));
-            if (U8 * rw <= 16 && bstream_lds(U8, A.M, rw, 8, bf) <= LDS_BUDGET) {
+            if (U8 * rw <= mw && bstream_lds(U8, A.M, rw, 8, bf) <= LDS_BUDGET) {
                 bp.bsu = 8;
                 bp.rw = rw;
             }
         } else if (gateup) {
             const int rw = bstream_rw(A.M, 8, true);
-            if (U8 * rw <= 16 && bstream_lds(U8, A.M, rw, 8, bf) <= LDS_BUDGET) {
+            if (U8 * rw <= mw && bstream_lds(U8, A.M, rw, 8, bf) <= LDS_BUDGET) {
                 bp.bsu = 8;
                 bp.rw = rw;
             }

@@ -629,8 +629,11 @@ __device__ __forceinline__ void bstream_tail(const GemvArgs& A, char* lds) {
         split_finish<DT, MODE>(A, vbase, RB, nthr);
 }
 
+// bf16 with 8-unit slices: 768 threads at most, so 170 VGPRs (its per-unit prescale does
+// not fit 128 next to eight units of streamed chunks); the planner keeps such workgroups to
+// 12 waves.
 template <int MODE, int BITS, int BSU, int DT>
-__global__ void __launch_bounds__(1024) gemv_bstream_kernel(const GemvArgs A) {
+__global__ void __launch_bounds__(DT == DT_BF16 && BSU == 8 ? 768 : 1024) gemv_bstream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
         bstream_body<BITS, MODE, BSU, DT>(A, lds);
