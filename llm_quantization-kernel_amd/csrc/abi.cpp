@@ -239,7 +239,7 @@ AnyPlan plan_any(int64_t M, int64_t V, int64_t K, int split_k) {
     return pl;
 }
 
-// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16 or bf16 x with 16-byte pieces, any group
+// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16 or bf16 x (fp32 x at batch 1) with 16-byte pieces, any group
 // size that is a multiple of 32, 32-bit byte offsets into every tensor, and for
 // mixed-width QKV workgroups that stay inside one projection.  The K range of a
 // split is cut into slices of 64 * STREAM_CPL chunks (one wave each, at most 8);
@@ -253,8 +253,9 @@ struct StreamPlan {
 };
 
 // Bytes the streaming kernel stages per chunk and batch row: 64 of operand pairs, then
-// (B, sum x), and for bf16 the chunk's power-of-two prescale as well.
-int stream_chunk_bytes(int dtype) { return dtype == CBK_BF16 ? 80 : 72; }
+// (B, sum x), and for bf16 the chunk's power-of-two prescale as well; fp32 stages two such
+// operand rows (hi, lo) per batch row.
+int stream_chunk_bytes(int dtype) { return dtype == CBK_F32 ? 160 : (dtype == CBK_BF16 ? 80 : 72); }
 
 // Slices a streaming job may hold: one wave each within the launch bound (16 waves),
 // and the staged activations per chunk and batch row plus the row-sum area (at most
@@ -277,10 +278,12 @@ int stream_splits(int64_t C, int split_k, int max_slices) {
 StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k) {
     StreamPlan sp;
     const int64_t lim = INT32_MAX;
-    bool ok = A.M >= 1 && A.M <= 2 && (dtype == CBK_F16 || dtype == CBK_BF16) && A.gs % 32 == 0 && A.K % 8 == 0 &&
-              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
+    // fp32 x streams at batch 1 (two fp16 operand rows per batch row)
+    const int xe = dtype == CBK_F32 ? 4 : 2;
+    bool ok = A.M >= 1 && A.M <= (dtype == CBK_F32 ? 1 : 2) && valid_dtype(dtype) && A.gs % 32 == 0 &&
+              A.K % 8 == 0 && reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * xe < lim;
     for (int i = 0; i < 3; ++i)
-        ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * 2 < lim;
+        ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * xe < lim;
     if (!ok) return sp;
     sp.mb = A.M;
     const int max_waves = 16;                           // the kernel's launch bound: 1024 threads
@@ -526,7 +529,7 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divGS = make_fastdiv((uint32_t)(A.gs / 32));
         L.family = CBK_KERNEL_STREAM;
-        L.f = gemv_stream_kernel_for(mode, A.bits[0], mixed, sp.mb, sp.rpw, dtype == CBK_BF16);
+        L.f = gemv_stream_kernel_for(mode, A.bits[0], mixed, sp.mb, sp.rpw, dtype);
         L.grid = sp.grid;
         L.block = 64 * sp.ks * sp.rw;
         L.lds = sp.lds;

@@ -24,7 +24,7 @@ hipError_t lds_limit_raise(const void* f, int bytes);
 constexpr int STREAM_CPL = CBK_STREAM_CPL;
 constexpr int STREAM_RPW = 4;
 constexpr int STREAM_RPW_WIDE = 8;
-const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw, bool bf16);
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw, int dt);
 // gemv_stream.hip: batch 3..16, fp16 or bf16, group size % 128 == 0.  A job is 16 * st_rw virtual
 // rows x one K split (over 128-code units); its workgroup has st_ks * st_rw waves, each
 // over 16 rows and one K slice of bsu (4 or 8) units.

@@ -2,8 +2,9 @@
 //
 // Replaces cb_gemv_kernel (Kernel/csrc/packed_gemv.cu:83-163) and, when the K
 // range is split, the partial write that cb_reduce_kernel (:166-180) combines,
-// for one or two activation rows (the decode step) in fp16 or bf16 with any group size
-// that is a multiple of 32.  Plain, fused-QKV and fused gate-up modes share the body; the
+// for one or two activation rows (the decode step) in fp16 or bf16, or one fp32 row (as two
+// fp16 operand rows), with any group size that is a multiple of 32.  Plain, fused-QKV and
+// fused gate-up modes share the body; the
 // outputs are finished per row (plain) or row pair (fused modes; finish, cbk_device.hpp).
 //
 // Job = (block of RB = RPW RW virtual rows, K split p).  A workgroup holds KS x RW
@@ -81,11 +82,12 @@ struct ProjRes {
     __amdgpu_buffer_rsrc_t w, s, z;
 };
 
-__device__ __forceinline__ ProjRes proj_res(const Src& p, int G) {
+// Descriptors of a projection's packed rows and of its scales and zeros (MB bytes each).
+__device__ __forceinline__ ProjRes proj_res(const Src& p, int G, int MB = 2) {
     ProjRes r;
     r.w = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.w), (short)0, p.n * p.wpr * 4, RAW);
-    r.s = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.s), (short)0, p.n * G * 2, RAW);
-    r.z = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.z), (short)0, p.n * G * 2, RAW);
+    r.s = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.s), (short)0, p.n * G * MB, RAW);
+    r.z = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.z), (short)0, p.n * G * MB, RAW);
     return r;
 }
 
@@ -179,14 +181,75 @@ __device__ __forceinline__ void convert_x_bf16(const uint32_t (&x)[16], u4 (&X)[
     f = __builtin_ldexpf(1.0f, c);
 }
 
-// Bytes staged per chunk and batch row after its 64 bytes of operand pairs: (B, sum x),
-// and for bf16 also 2^c (a 16-byte entry).
-template <int DT> constexpr int XB_BYTES = DT == DT_BF16 ? 16 : 8;
+// fp32 activations.  Activation chunk ca of batch row b as 32 fp32 words (8 pieces of 16
+// bytes; K % 8 == 0, so a piece lies wholly before or past K).
+__device__ __forceinline__ void load_x32(__amdgpu_buffer_rsrc_t xr, bool ok, int b, int ca, int K,
+                                         uint32_t (&x)[32]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int k = 32 * ca + 4 * i;
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, vofs(ok && k < K, 4 * (b * K + k)), 0, 0);
+        x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+    }
+}
+
+// An fp32 chunk as two fp16 operand rows.  The chunk is prescaled by 2^-c as a bf16 chunk is
+// (its largest magnitude into [2^14, 2^15)); each slot-scaled value v = x 2^(-c-e) is split
+// into hi = RN_fp16(v) and lo = RN_fp16(v - hi) (v - hi is exact in fp32), so hi + lo holds v
+// to 2^-22 of the chunk's largest value (subnormal lo parts lose bits only below 2^-39 of it).
+// Both rows meet the same decoded weights; their terms add before the scale 2^c.  The
+// weights' pairs 1024 + 2^e q lose their 1024 first (exact in fp16), so the dot products
+// carry no 1024 sum x term whose cancellation would cost fp32 bits: B = 0.
+__device__ __forceinline__ int chunk_exp_f32(const uint32_t (&x)[32]) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m = max(m, x[i] & 0x7F800000u);
+    return (int)(m >> 23);
+}
+
+template <int BITS>
+__device__ __forceinline__ void convert_x_f32(const uint32_t (&x)[32], u4 (&Xh)[4], u4 (&Xl)[4], float& Bh,
+                                              float& xsh, float& Bl, float& xsl, float& f) {
+    const int c = prescale_bf16(chunk_exp_f32(x));
+    uint32_t oh[16], ol[16];
+    float th = 0.f, tl = 0.f;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+        const int ka = Decode<BITS>::kappa(2 * p), kb = Decode<BITS>::kappa(2 * p + 1);
+        const int ea = Decode<BITS>::expo(2 * p), eb = Decode<BITS>::expo(2 * p + 1);
+        const float va = __builtin_ldexpf(__uint_as_float(x[ka]), -c - ea);
+        const float vb = __builtin_ldexpf(__uint_as_float(x[kb]), -c - eb);
+        const h2 hi = {(_Float16)va, (_Float16)vb};
+        const h2 lo = {(_Float16)(va - (float)hi.x), (_Float16)(vb - (float)hi.y)};
+        oh[p] = __builtin_bit_cast(uint32_t, hi);
+        ol[p] = __builtin_bit_cast(uint32_t, lo);
+        const h2 up = {(_Float16)(float)(1 << ea), (_Float16)(float)(1 << eb)};
+        th = __builtin_amdgcn_fdot2(hi, up, th, false);
+        tl = __builtin_amdgcn_fdot2(lo, up, tl, false);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        Xh[q] = u4{oh[4 * q], oh[4 * q + 1], oh[4 * q + 2], oh[4 * q + 3]};
+        Xl[q] = u4{ol[4 * q], ol[4 * q + 1], ol[4 * q + 2], ol[4 * q + 3]};
+    }
+    Bh = 0.f;
+    xsh = th;
+    Bl = 0.f;
+    xsl = tl;
+    f = __builtin_ldexpf(1.0f, c);
+}
+
+// Bytes staged per chunk and operand row after its 64 bytes of operand pairs: (B, sum x),
+// and for bf16 and fp32 also 2^c (a 16-byte entry).  fp32 stages two operand rows (hi, lo)
+// per batch row.
+template <int DT> constexpr int XB_BYTES = DT == DT_F16 ? 8 : 16;
+template <int DT> constexpr int SROWS = DT == DT_F32 ? 2 : 1;
 
 // A (scale, zero) half of the activations' dtype as a float.
 template <int DT>
 __device__ __forceinline__ float meta_f(uint32_t bits) {
     if constexpr (DT == DT_BF16) return __uint_as_float(bits << 16);
+    else if constexpr (DT == DT_F32) return __uint_as_float(bits);
     else return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
 }
 
@@ -251,11 +314,15 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     // 1a. the thread's activation chunk of every batch row (job chunk tid; the host
     // keeps RW >= CPL, so the 64 KS RW threads cover the KS * SLICE staged chunks);
     // batch rows past M read as zero
+    constexpr int XE = DT == DT_F32 ? 4 : 2;           // bytes of an activation / scale / zero
     const __amdgpu_buffer_rsrc_t xr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * 2, RAW);
-    uint32_t xa[MB][16];
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * XE, RAW);
+    uint32_t xa[MB][DT == DT_F32 ? 32 : 16];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) load_x(xr, tid < nrange && b < A.M, b, c0 + tid, A.K, xa[b]);
+    for (int b = 0; b < MB; ++b) {
+        if constexpr (DT == DT_F32) load_x32(xr, tid < nrange && b < A.M, b, c0 + tid, A.K, xa[b]);
+        else load_x(xr, tid < nrange && b < A.M, b, c0 + tid, A.K, xa[b]);
+    }
 
     // 1b. the wave's packed chunks and their (scale, zero) halves
     int gi[CPL];
@@ -274,8 +341,8 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     vmap<MODE>(A, min(v0, A.V - 1), proj0, r0);
     const Src S0 = MODE == MODE_QKV ? src_of(A, proj0) : A.src[0];
     ProjRes R[2];
-    R[0] = proj_res(S0, A.G);
-    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.src[1], A.G);
+    R[0] = proj_res(S0, A.G, XE);
+    if constexpr (MODE == MODE_GATEUP) R[1] = proj_res(A.src[1], A.G, XE);
     uint32_t w[RPW][CPL][BITS];
     uint32_t sz[RPW][CPL][2];
 #pragma unroll
@@ -289,29 +356,48 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
         for (int i = 0; i < CPL; ++i) {
             const int c = ks * SLICE + lane + 64 * i;
             const bool ok = vin && cin[i];
-            const int so = vofs(ok, 2 * (r * A.G + gi[i]));
+            const int so = vofs(ok, XE * (r * A.G + gi[i]));
             load_chunk<BITS>(P.w, vofs(ok, 4 * (r * wpr + (c0 + c) * BITS)), w[j][i]);
-            sz[j][i][0] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
-            sz[j][i][1] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
+            if constexpr (DT == DT_F32) {
+                sz[j][i][0] = __builtin_amdgcn_raw_buffer_load_b32(P.s, so, 0, 0);
+                sz[j][i][1] = __builtin_amdgcn_raw_buffer_load_b32(P.z, so, 0, 0);
+            } else {
+                sz[j][i][0] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
+                sz[j][i][1] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
+            }
         }
         // rows are issued in the order they are consumed, so row j's arithmetic
         // waits for its own loads only
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // 2. activations -> LDS: piece q of chunk c of batch row b at ((b * 4 + q) NCH + c) * 16,
-    // (B, sum x[, 2^c]) at 64 MB NCH + XB (b NCH + c); chunks past the split read as zero
-    // (they meet no weights)
+    // 2. activations -> LDS: piece q of chunk c of operand row b at ((b * 4 + q) NCH + c) * 16,
+    // (B, sum x[, 2^c]) at 64 MB SR NCH + XB (b NCH + c); chunks past the split read as zero
+    // (they meet no weights).  Operand row b is batch row b, or for fp32 half b & 1 (hi, lo)
+    // of batch row b >> 1.
     constexpr int XBB = XB_BYTES<DT>;
+    constexpr int SR = SROWS<DT>;                       // staged operand rows per batch row
     u4* Xl = reinterpret_cast<u4*>(lds);
-    char* XBl = lds + 64 * MB * NCH;
-    float* red = reinterpret_cast<float*>(lds + (64 + XBB) * MB * NCH);
+    char* XBl = lds + 64 * MB * SR * NCH;
+    float* red = reinterpret_cast<float*>(lds + (64 + XBB) * MB * SR * NCH);
     if (tid < NCH) {
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
             u4 X[4];
             float B, xs;
-            if constexpr (DT == DT_BF16) {
+            if constexpr (DT == DT_F32) {
+                u4 Xo[4];
+                float Bo, xso, f;
+                convert_x_f32<BITS>(xa[b], X, Xo, B, xs, Bo, xso, f);
+                *reinterpret_cast<float4*>(XBl + XBB * ((2 * b) * NCH + tid)) = make_float4(B, xs, f, 0.f);
+                *reinterpret_cast<float4*>(XBl + XBB * ((2 * b + 1) * NCH + tid)) = make_float4(Bo, xso, f, 0.f);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    Xl[((2 * b) * 4 + q) * NCH + tid] = X[q];
+                    Xl[((2 * b + 1) * 4 + q) * NCH + tid] = Xo[q];
+                }
+                continue;
+            } else if constexpr (DT == DT_BF16) {
                 float f;
                 convert_x_bf16<BITS>(xa[b], X, B, xs, f);
                 *reinterpret_cast<float4*>(XBl + XBB * (b * NCH + tid)) = make_float4(B, xs, f, 0.f);
@@ -326,17 +412,17 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
     lds_barrier();
 
     // 3. rows: each chunk is decoded once and meets every batch row's activations
-    u4 X[MB][CPL][4];
-    float2 XB[MB][CPL];
-    float XF[MB][CPL];                   // 2^c of a bf16 chunk
+    u4 X[MB * SR][CPL][4];
+    float2 XB[MB * SR][CPL];
+    float XF[MB * SR][CPL];              // 2^c of a bf16 or fp32 chunk
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
+    for (int b = 0; b < MB * SR; ++b) {
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = ks * SLICE + lane + 64 * i;
 #pragma unroll
             for (int q = 0; q < 4; ++q) X[b][i][q] = Xl[(b * 4 + q) * NCH + c];
-            if constexpr (DT == DT_BF16) {
+            if constexpr (DT != DT_F16) {
                 const float4 e = *reinterpret_cast<const float4*>(XBl + XBB * (b * NCH + c));
                 XB[b][i] = make_float2(e.x, e.y);
                 XF[b][i] = e.z;
@@ -355,13 +441,22 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
         for (int i = 0; i < CPL; ++i) {
             uint32_t h[16];
             Decode<BITS>::run(w[j][i], h, g);
+            if constexpr (DT == DT_F32) {
+                const h2 off = {(_Float16)1024.f, (_Float16)1024.f};
+#pragma unroll
+                for (int q = 0; q < 16; ++q) h[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, h[q]) - off);
+            }
             const float s = meta_f<DT>(sz[j][i][0]);
             const float z = meta_f<DT>(sz[j][i][1]);
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
-                const float d = pairs_dot(h, X[b][i]);
-                const float t = d - fmaf(z, XB[b][i].y, XB[b][i].x);
-                acc[b][j] = fmaf(s, DT == DT_BF16 ? t * XF[b][i] : t, acc[b][j]);
+                float t = 0.f;
+#pragma unroll
+                for (int r = 0; r < SR; ++r) {
+                    const int sr = SR * b + r;
+                    t += pairs_dot(h, X[sr][i]) - fmaf(z, XB[sr][i].y, XB[sr][i].x);
+                }
+                acc[b][j] = fmaf(s, DT == DT_F16 ? t : t * XF[SR * b][i], acc[b][j]);
             }
         }
     }
@@ -391,7 +486,7 @@ __device__ __forceinline__ void stream_tail(const GemvArgs& A, char* lds) {
     const int blk = (int)fdiv(blockIdx.x, A.divP);
     const int p = blockIdx.x - blk * A.P;
     const int vbase = blk * RB;
-    const float* red = reinterpret_cast<const float*>(lds + (64 + XB_BYTES<DT>) * MB * NCH);
+    const float* red = reinterpret_cast<const float*>(lds + (64 + XB_BYTES<DT>) * MB * SROWS<DT> * NCH);
     constexpr int U = FINISH_ROWS<MODE>;
     const int NU = RB / U;
     if (tid < MB * NU) {
@@ -700,7 +795,8 @@ const void* bstream_kernel(int mode, int bits, bool mixed) {
 
 template <int DT>
 const void* stream_kernel_dt(int mode, int bits, bool mixed, int mb, int rpw) {
-    if (mb > 1) return stream_kernel<2, STREAM_RPW, DT>(mode, bits, mixed);
+    if constexpr (DT != DT_F32)                        // fp32 streams at batch 1 only
+        if (mb > 1) return stream_kernel<2, STREAM_RPW, DT>(mode, bits, mixed);
     if (rpw == STREAM_RPW_WIDE && mode == MODE_GEMV && !mixed) {     // the host plans 8 rows for plain GEMVs only
         constexpr int W = STREAM_RPW_WIDE;
         return bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 2, 1, W, DT>)
@@ -710,9 +806,10 @@ const void* stream_kernel_dt(int mode, int bits, bool mixed, int mb, int rpw) {
     return stream_kernel<1, STREAM_RPW, DT>(mode, bits, mixed);
 }
 
-const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw, bool bf16) {
-    return bf16 ? stream_kernel_dt<DT_BF16>(mode, bits, mixed, mb, rpw)
-                : stream_kernel_dt<DT_F16>(mode, bits, mixed, mb, rpw);
+const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int rpw, int dt) {
+    return dt == DT_BF16 ? stream_kernel_dt<DT_BF16>(mode, bits, mixed, mb, rpw)
+                         : (dt == DT_F32 ? stream_kernel_dt<DT_F32>(mode, bits, mixed, mb, rpw)
+                                         : stream_kernel_dt<DT_F16>(mode, bits, mixed, mb, rpw));
 }
 
 const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu, bool bf16) {
