@@ -450,9 +450,10 @@ __device__ __forceinline__ void stream_body(const GemvArgs& A, char* lds) {
             const float z = meta_f<DT>(sz[j][i][1]);
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
-                float t = 0.f;
+                // operand row SR b (fp32: hi), then for fp32 its lo row
+                float t = pairs_dot(h, X[SR * b][i]) - fmaf(z, XB[SR * b][i].y, XB[SR * b][i].x);
 #pragma unroll
-                for (int r = 0; r < SR; ++r) {
+                for (int r = 1; r < SR; ++r) {
                     const int sr = SR * b + r;
                     t += pairs_dot(h, X[sr][i]) - fmaf(z, XB[sr][i].y, XB[sr][i].x);
                 }
