@@ -1021,7 +1021,8 @@ def ablation_sweep(torch, C, ops, dev, gate, bits=3):
 
 def fp32_sweep(torch, C, ops, dev, gate):
     """fp32 activations (fp32 scales, zeros and outputs; the reference's T = float): the W3 decode
-    at M in {1, 4, 8} over the three shapes on the fp32 matrix-core decode, graph-replayed over
+    at M in {1, 2, 4, 8} over the three shapes (the decode plan's kernel: streaming at batch 1-2 where
+    it takes them, else the fp32 matrix-core decode), graph-replayed over
     >= 1 GiB of weight copies, and the W4 prefill at M = 1024 (4096 x 4096) on the fp32 matrix-core
     GEMM, beside the fp16 prefill with the 16-bit matrix cores turned off (use_tensor_cores=False,
     the same fp32 kernel).  Every row checked against the oracle before it is timed."""
@@ -1031,7 +1032,7 @@ def fp32_sweep(torch, C, ops, dev, gate):
         base = make_weight(torch, N, K, 3, 0, dev)
         w32 = replace(base, scales=base.scales.float(), zeros=base.zeros.float())
         ws = [w32] + [clone_weight(w32) for _ in range(copies_for(weight_bytes(w32)) - 1)]
-        for M in (1, 4, 8):
+        for M in (1, 2, 4, 8):
             x = randx(torch, M, K, 1, dev).float()
             gate.gemv(f"fp32 decode W3 M={M} {K}->{N}", ops.packed_linear(x, ws[0]), x, w32)
             fam = C.decode_plan(torch.float32, M, K, GS, N, 3, "gemv", 1, 1)[0]

@@ -239,10 +239,10 @@ AnyPlan plan_any(int64_t M, int64_t V, int64_t K, int split_k) {
     return pl;
 }
 
-// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16 or bf16 x (fp32 x at batch 1) with 16-byte pieces, any group
+// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16, bf16 or fp32 x with 16-byte pieces, any group
 // size that is a multiple of 32, 32-bit byte offsets into every tensor, and for
 // mixed-width QKV workgroups that stay inside one projection.  The K range of a
-// split is cut into slices of 64 * STREAM_CPL chunks (one wave each, at most 8);
+// split is cut into slices of 64 * STREAM_CPL chunks (one wave each, within the launch bound);
 // rows go rpw to a wave, RW row groups to a workgroup.  A plain GEMV at batch 1 with
 // at most two slices (K <= 4096 at one split) takes 8 rows a wave in two row groups:
 // the same 16 rows per workgroup from half the waves (4096^2 W3: 4.5 -> 4.1 us per
@@ -257,11 +257,15 @@ struct StreamPlan {
 // operand rows (hi, lo) per batch row.
 int stream_chunk_bytes(int dtype) { return dtype == CBK_F32 ? 160 : (dtype == CBK_BF16 ? 80 : 72); }
 
-// Slices a streaming job may hold: one wave each within the launch bound (16 waves),
+// Waves a streaming workgroup may hold: the kernel's launch bound (1024 threads, or 512 for fp32
+// at batch 2, whose four operand rows need more than 128 VGPRs).
+int stream_max_waves(int mb, int dtype) { return dtype == CBK_F32 && mb == 2 ? 8 : 16; }
+
+// Slices a streaming job may hold: one wave each within the launch bound,
 // and the staged activations per chunk and batch row plus the row-sum area (at most
 // 16 slices x 2 rows x 16 rows x 4 bytes) in the LDS.
 int stream_max_slices(int mb, int dtype) {
-    const int waves = 16 / STREAM_CPL;
+    const int waves = stream_max_waves(mb, dtype) / STREAM_CPL;
     const int lds = (LDS_BUDGET - 16 * 2 * 16 * 4) / (64 * STREAM_CPL * stream_chunk_bytes(dtype) * mb);
     return std::max(1, std::min(waves, lds));
 }
@@ -278,15 +282,15 @@ int stream_splits(int64_t C, int split_k, int max_slices) {
 StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k) {
     StreamPlan sp;
     const int64_t lim = INT32_MAX;
-    // fp32 x streams at batch 1 (two fp16 operand rows per batch row)
+    // fp32 x streams at batch 1-2 (two fp16 operand rows per batch row)
     const int xe = dtype == CBK_F32 ? 4 : 2;
-    bool ok = A.M >= 1 && A.M <= (dtype == CBK_F32 ? 1 : 2) && valid_dtype(dtype) && A.gs % 32 == 0 &&
+    bool ok = A.M >= 1 && A.M <= 2 && valid_dtype(dtype) && A.gs % 32 == 0 &&
               A.K % 8 == 0 && reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * xe < lim;
     for (int i = 0; i < 3; ++i)
         ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * xe < lim;
     if (!ok) return sp;
     sp.mb = A.M;
-    const int max_waves = 16;                           // the kernel's launch bound: 1024 threads
+    const int max_waves = stream_max_waves(sp.mb, dtype);   // the kernel's launch bound
     const int64_t slice = 64 * STREAM_CPL;
     sp.P = stream_splits(A.C, split_k, stream_max_slices(sp.mb, dtype));
     if ((int64_t)A.C * sp.P >= (1ll << 32)) return sp;     // split bounds C p / P in 32 bits
@@ -294,6 +298,10 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
     if (sp.ks * STREAM_CPL > max_waves) return sp;
     sp.rw = sp.ks <= 2 ? 4 : 2;
     sp.rw = std::max(STREAM_CPL, std::min(sp.rw, max_waves / sp.ks));
+    // fp32 at batch 2 stages 320 bytes of activations per chunk: with one row group a
+    // workgroup (K > 8192 unsplit in 8 waves) every 4 rows restage all of x (W3 11008 -> 4096:
+    // 30.4 us, the fp32 matrix-core kernel 31.8), so it streams only with two or more
+    if (dtype == CBK_F32 && sp.mb == 2 && sp.rw < 2) return sp;
     if (sp.mb == 1 && sp.ks <= 2 && mode == CBK_MODE_GEMV && !mixed) {
         sp.rpw = STREAM_RPW_WIDE;
         sp.rw = std::max(STREAM_CPL, sp.rw / 2);

@@ -2,7 +2,7 @@
 //
 // Replaces cb_gemv_kernel (Kernel/csrc/packed_gemv.cu:83-163) and, when the K
 // range is split, the partial write that cb_reduce_kernel (:166-180) combines,
-// for one or two activation rows (the decode step) in fp16 or bf16, or one fp32 row (as two
+// for one or two activation rows (the decode step) in fp16, bf16 or fp32 (an fp32 row as two
 // fp16 operand rows), with any group size that is a multiple of 32.  Plain, fused-QKV and
 // fused gate-up modes share the body; the
 // outputs are finished per row (plain) or row pair (fused modes; finish, cbk_device.hpp).
@@ -750,8 +750,10 @@ __global__ void __launch_bounds__(DT == DT_BF16 && BSU == 8 ? 768 : 1024) gemv_b
 // the activations, which at K = 11008 leaves one workgroup per CU; they take the
 // batch-rows MFMA kernel instead.  RPW rows per wave (4, or 8 for the host's short-K
 // batch-1 plan: half the waves for the same rows per workgroup).
+// fp32 at batch 2 stages four operand rows, more than 128 VGPRs hold: a 512-thread build (256
+// VGPRs), and the host keeps its plans to 8 waves.
 template <int MODE, int BITS, int MB, int RPW, int DT>
-__global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
+__global__ void __launch_bounds__(DT == DT_F32 && MB == 2 ? 512 : 1024) gemv_stream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
         stream_body<BITS, MODE, MB, RPW, DT>(A, lds);
@@ -796,8 +798,7 @@ const void* bstream_kernel(int mode, int bits, bool mixed) {
 
 template <int DT>
 const void* stream_kernel_dt(int mode, int bits, bool mixed, int mb, int rpw) {
-    if constexpr (DT != DT_F32)                        // fp32 streams at batch 1 only
-        if (mb > 1) return stream_kernel<2, STREAM_RPW, DT>(mode, bits, mixed);
+    if (mb > 1) return stream_kernel<2, STREAM_RPW, DT>(mode, bits, mixed);
     if (rpw == STREAM_RPW_WIDE && mode == MODE_GEMV && !mixed) {     // the host plans 8 rows for plain GEMVs only
         constexpr int W = STREAM_RPW_WIDE;
         return bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 2, 1, W, DT>)

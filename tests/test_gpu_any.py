@@ -25,17 +25,23 @@ def plan(dtype, M, K, gs, out, bits, kind="gemv", split_k=1):
     return fam, splits, threads, launches
 
 
+def fp32_family(M, K):
+    """Decode family of an unsplit fp32 call: streaming at batch 1, and at batch 2 while K
+    fits two row groups a workgroup in the 8 waves of its 512-thread build (K <= 8192)."""
+    return "stream" if M == 1 or (M == 2 and K <= 8192) else "generic"
+
+
 # ------------------------------------------------------------------ fp32 activations
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("K,N", BASELINE)
-@pytest.mark.parametrize("M", [1, 4, 8])
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_fp32_decode_baseline_shapes(hip, bits, K, N, M):
-    """fp32 x at the BASELINE decode shapes: the streaming kernel at batch 1 (two fp16
-    operand rows per chunk), the fp32 matrix-core kernel at batch 4 and 8; one launch, within
-    the fp32 bar."""
+    """fp32 x at the BASELINE decode shapes: the streaming kernel at batch 1 and 2 (two fp16
+    operand rows per chunk and batch row; batch 2 only where a workgroup holds two row groups,
+    K <= 8192 unsplit), the fp32 matrix-core kernel otherwise; one launch, within the fp32 bar."""
     fam, splits, threads, launches = plan(torch.float32, M, K, 128, N, bits)
-    assert (fam, splits, launches) == ("stream" if M == 1 else "generic", 1, 1), (fam, splits, launches)
+    assert (fam, splits, launches) == (fp32_family(M, K), 1, 1), (fam, splits, launches)
     assert threads % 64 == 0 and 64 <= threads <= 1024
     w, W64, _, _ = make(N, K, bits, torch.float32, scale=0.02)
     x = randx(M, K, torch.float32, seed=10 + M)
@@ -43,15 +49,15 @@ def test_fp32_decode_baseline_shapes(hip, bits, K, N, M):
 
 
 @pytest.mark.parametrize("split_k", [2, 5, 64])
-@pytest.mark.parametrize("M", [1, 3, 16, 20])
+@pytest.mark.parametrize("M", [1, 2, 3, 16, 20])
 def test_fp32_decode_splits(hip, split_k, M):
-    """K splits of the fp32 decode (the streaming kernel at batch 1, the fp32 matrix-core
+    """K splits of the fp32 decode (the streaming kernel at batch 1-2, the fp32 matrix-core
     kernel above) combine inside the dispatch (the last split of each block adds the
     partials); the result matches the unsplit call within the bar and repeats bit for bit."""
     w, W64, b64, _ = make(600, 4128, 3, torch.float32, bias=True)
     x = randx(M, 4128, torch.float32, seed=M)
     fam, splits, _, launches = plan(torch.float32, M, 4128, 128, 600, 3, split_k=split_k)
-    assert fam == ("stream" if M == 1 else "generic") and splits == split_k and launches == 1
+    assert fam == fp32_family(M, 4128) and splits == split_k and launches == 1
     y = packed_linear(x, w, split_k, 1, "silu", decode_threshold=32)
     close(y, ref_linear(x, W64, b64, "silu"), torch.float32)
     assert torch.equal(packed_linear(x, w, split_k, 1, "silu", decode_threshold=32), y)
@@ -60,33 +66,38 @@ def test_fp32_decode_splits(hip, split_k, M):
 @pytest.mark.parametrize("dist", ["normal", "wide", "tiny", "outlier"])
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("K,N", BASELINE)
-def test_fp32_streaming_activation_ranges(hip, dist, bits, K, N):
-    """fp32 x at batch 1 on the streaming kernel: each 32-code chunk is prescaled by its own
+@pytest.mark.parametrize("M", [1, 2])
+def test_fp32_streaming_activation_ranges(hip, dist, bits, K, N, M):
+    """fp32 x at batch 1-2 on the streaming kernel: each 32-code chunk is prescaled by its own
     power of two and split into two fp16 operands (hi, lo), so fp32 activations of any range
     keep fp32 accuracy -- N(0,1), values spread over 2^-40..2^40 ("wide"), all below 1e-30
-    ("tiny") and a few channels 1e4 times the rest ("outlier") -- within the fp32 bar."""
-    assert plan(torch.float32, 1, K, 128, N, bits)[0] == "stream"
+    ("tiny") and a few channels 1e4 times the rest ("outlier") -- within the fp32 bar.  Batch 2
+    at K = 11008 streams with two K splits (unsplit it takes the fp32 matrix-core kernel)."""
+    split_k = 2 if M == 2 and K > 8192 else 1
+    assert plan(torch.float32, M, K, 128, N, bits, split_k=split_k)[0] == "stream"
     w, W64, _, _ = make(N, K, bits, torch.float32, scale=0.02)
-    g = torch.Generator().manual_seed(bits + K)
-    x = torch.randn(1, K, generator=g, dtype=torch.float64)
+    g = torch.Generator().manual_seed(bits + K + M)
+    x = torch.randn(M, K, generator=g, dtype=torch.float64)
     if dist == "wide":
-        x = x * torch.exp2(torch.randint(-40, 41, (1, K), generator=g).double())
+        x = x * torch.exp2(torch.randint(-40, 41, (M, K), generator=g).double())
     elif dist == "tiny":
         x = x * 1e-32
     elif dist == "outlier":
-        x[0, torch.randperm(K, generator=g)[:4]] *= 1e4
+        x[:, torch.randperm(K, generator=g)[:4]] *= 1e4
+        x[M - 1] *= 1e-3                                   # batch rows of different magnitude
     x = x.float().cuda()
-    close(packed_linear(x, w), ref_linear(x, W64), torch.float32)
+    close(packed_linear(x, w, split_k), ref_linear(x, W64), torch.float32)
 
 
 @pytest.mark.parametrize("gs", [32, 64, 256])
 @pytest.mark.parametrize("K", [200, 1000, 4128])
-def test_fp32_streaming_groups_and_ragged_k(hip, gs, K):
-    """Batch-1 fp32 streaming with group sizes 32..256 and K not a multiple of 32 (the last
-    chunk's pieces past K read as zero), bias and SiLU, against the oracle."""
+@pytest.mark.parametrize("M", [1, 2])
+def test_fp32_streaming_groups_and_ragged_k(hip, gs, K, M):
+    """Batch-1 and -2 fp32 streaming with group sizes 32..256 and K not a multiple of 32 (the
+    last chunk's pieces past K read as zero), bias and SiLU, against the oracle."""
     w, W64, b64, _ = make(300, K, 3, torch.float32, bias=True, gs=gs)
-    x = randx(1, K, torch.float32, seed=K)
-    assert plan(torch.float32, 1, K, gs, 300, 3)[0] == "stream"
+    x = randx(M, K, torch.float32, seed=K + M)
+    assert plan(torch.float32, M, K, gs, 300, 3)[0] == "stream"
     close(packed_linear(x, w, act="silu"), ref_linear(x, W64, b64, "silu"), torch.float32)
 
 
