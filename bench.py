@@ -701,8 +701,16 @@ def probe_sweep(torch, C, dev, gemv_rows=None, fused=None):
     {1, 2, 4, 8, 16} pieces per thread x {256, 1024} threads per workgroup; `probe_us` reads and
     keeps nothing, `probe_store_us` also writes one word per workgroup after a workgroup
     reduction (as a decode workgroup ends).  Each row carries the decode call's own µs from the
-    sweeps of the same run when they ran."""
+    sweeps of the same run when they ran.  The first row is the launch floor: the same kernel
+    with one 64-thread workgroup and one 16-byte piece, back to back in the graph, so nearly
+    all of its time is the dispatch and the end-of-kernel fences every launch pays."""
     sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+    tiny = [torch.zeros(4, dtype=torch.int32, device=dev) for _ in range(64)]
+    floor = graph_launch_us(torch, lambda: [C.stream_probe(t, 1, 64, True, sink) for t in tiny], len(tiny),
+                            replays=4)
+    rows = [{"case": "launch floor: one 64-thread workgroup, 16 bytes", "bits": None, "K": None, "N": None,
+             "bytes": 16, "probe_store_us": round(floor, 3), "block": 64, "unroll": 1, "copies": len(tiny)}]
+    log(f"probe launch floor: {floor:.2f} us per launch")
     meta = lambda N, K: N * math.ceil(K / GS) * 2 * 2                      # noqa: E731
     packed = lambda N, K, b: N * math.ceil(K / 32) * b * 4                # noqa: E731
     qkv_bits = [int(b) for b in (fused or {}).get("qkv", {}).get("bits", [4, 3, 3])]
@@ -712,7 +720,6 @@ def probe_sweep(torch, C, dev, gemv_rows=None, fused=None):
     cases.append(("fused gate-up 4096->2x11008", 3, 4096, 11008,
                   2 * (packed(11008, 4096, 3) + meta(11008, 4096)) + 4096 * 2 + 11008 * 2))
     gemv_us = {(r["bits"], r["K"], r["N"]): r["us"] for r in (gemv_rows or []) if r["M"] == 1}
-    rows = []
     for name, b, K, N, nbytes in cases:
         pool = [torch.zeros((nbytes + 15) // 16 * 4, dtype=torch.int32, device=dev)
                 for _ in range(copies_for(nbytes))]
