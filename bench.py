@@ -1028,8 +1028,8 @@ def ablation_sweep(torch, C, ops, dev, gate, bits=3):
 
 def fp32_sweep(torch, C, ops, dev, gate):
     """fp32 activations (fp32 scales, zeros and outputs; the reference's T = float): the W3 decode
-    at M in {1, 2, 4, 8} over the three shapes (the decode plan's kernel: streaming at batch 1-2 where
-    it takes them, else the fp32 matrix-core decode), graph-replayed over
+    at M in {1, 2, 4, 8} over the three shapes (the decode plan's kernel: the streaming kernel at
+    batch 1, the batched streaming kernel at 2..8), graph-replayed over
     >= 1 GiB of weight copies, and the W4 prefill at M = 1024 (4096 x 4096) on the fp32 matrix-core
     GEMM, beside the fp16 prefill with the 16-bit matrix cores turned off (use_tensor_cores=False,
     the same fp32 kernel).  Every row checked against the oracle before it is timed."""

@@ -239,7 +239,7 @@ AnyPlan plan_any(int64_t M, int64_t V, int64_t K, int split_k) {
     return pl;
 }
 
-// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16, bf16 or fp32 x with 16-byte pieces, any group
+// Streaming plan (gemv_stream.hip), batch 1 or 2: fp16 or bf16 x (fp32 x at batch 1) with 16-byte pieces, any group
 // size that is a multiple of 32, 32-bit byte offsets into every tensor, and for
 // mixed-width QKV workgroups that stay inside one projection.  The K range of a
 // split is cut into slices of 64 * STREAM_CPL chunks (one wave each, within the launch bound);
@@ -257,15 +257,11 @@ struct StreamPlan {
 // operand rows (hi, lo) per batch row.
 int stream_chunk_bytes(int dtype) { return dtype == CBK_F32 ? 160 : (dtype == CBK_BF16 ? 80 : 72); }
 
-// Waves a streaming workgroup may hold: the kernel's launch bound (1024 threads, or 512 for fp32
-// at batch 2, whose four operand rows need more than 128 VGPRs).
-int stream_max_waves(int mb, int dtype) { return dtype == CBK_F32 && mb == 2 ? 8 : 16; }
-
-// Slices a streaming job may hold: one wave each within the launch bound,
+// Slices a streaming job may hold: one wave each within the launch bound (16 waves),
 // and the staged activations per chunk and batch row plus the row-sum area (at most
 // 16 slices x 2 rows x 16 rows x 4 bytes) in the LDS.
 int stream_max_slices(int mb, int dtype) {
-    const int waves = stream_max_waves(mb, dtype) / STREAM_CPL;
+    const int waves = 16 / STREAM_CPL;
     const int lds = (LDS_BUDGET - 16 * 2 * 16 * 4) / (64 * STREAM_CPL * stream_chunk_bytes(dtype) * mb);
     return std::max(1, std::min(waves, lds));
 }
@@ -282,15 +278,18 @@ int stream_splits(int64_t C, int split_k, int max_slices) {
 StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int split_k) {
     StreamPlan sp;
     const int64_t lim = INT32_MAX;
-    // fp32 x streams at batch 1-2 (two fp16 operand rows per batch row)
+    // fp32 x streams at batch 1 (two fp16 operand rows); at batch 2 the batched kernel, which
+    // stages the four operand rows once per workgroup and takes the products on MFMAs, is as
+    // fast or faster at every shape (W3 4096^2 / 4096 -> 11008 / 11008 -> 4096: 6.74 / 12.37 /
+    // 14.60 us against 6.89 / 16.90 / 14.75 on a 512-thread build of this kernel)
     const int xe = dtype == CBK_F32 ? 4 : 2;
-    bool ok = A.M >= 1 && A.M <= 2 && valid_dtype(dtype) && A.gs % 32 == 0 &&
+    bool ok = A.M >= 1 && A.M <= (dtype == CBK_F32 ? 1 : 2) && valid_dtype(dtype) && A.gs % 32 == 0 &&
               A.K % 8 == 0 && reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * xe < lim;
     for (int i = 0; i < 3; ++i)
         ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * xe < lim;
     if (!ok) return sp;
     sp.mb = A.M;
-    const int max_waves = stream_max_waves(sp.mb, dtype);   // the kernel's launch bound
+    const int max_waves = 16;                           // the kernel's launch bound: 1024 threads
     const int64_t slice = 64 * STREAM_CPL;
     sp.P = stream_splits(A.C, split_k, stream_max_slices(sp.mb, dtype));
     if ((int64_t)A.C * sp.P >= (1ll << 32)) return sp;     // split bounds C p / P in 32 bits
@@ -298,10 +297,6 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
     if (sp.ks * STREAM_CPL > max_waves) return sp;
     sp.rw = sp.ks <= 2 ? 4 : 2;
     sp.rw = std::max(STREAM_CPL, std::min(sp.rw, max_waves / sp.ks));
-    // fp32 at batch 2 stages 320 bytes of activations per chunk: with one row group a
-    // workgroup (K > 8192 unsplit in 8 waves) every 4 rows restage all of x (W3 11008 -> 4096:
-    // 30.4 us, the fp32 matrix-core kernel 31.8), so it streams only with two or more
-    if (dtype == CBK_F32 && sp.mb == 2 && sp.rw < 2) return sp;
     if (sp.mb == 1 && sp.ks <= 2 && mode == CBK_MODE_GEMV && !mixed) {
         sp.rpw = STREAM_RPW_WIDE;
         sp.rw = std::max(STREAM_CPL, sp.rw / 2);
@@ -333,11 +328,12 @@ struct BStreamPlan {
     int P = 1, ks = 1, rw = 1, bsu = 4, grid = 0, lds = 0;
 };
 
-// LDS of a batched streaming workgroup: the staged activations, two per-unit sums (three
-// for bf16: its per-unit prescale) for 16 batch rows, and the row totals.
-int64_t bstream_lds(int64_t ks, int64_t M, int64_t rw, int bsu, bool bf) {
+// LDS of a batched streaming workgroup: the staged activations (xr operand rows per batch
+// row: 2 for fp32, hi and lo), two per-unit sums (three for bf16 and fp32: the per-unit
+// prescale) for 16 operand rows, and the row totals.
+int64_t bstream_lds(int64_t ks, int64_t M, int64_t rw, int bsu, bool bf, int xr = 1) {
     const int64_t nu = ks * bsu;
-    return 64 * 4 * nu * M + (bf ? 3 : 2) * 16 * nu * 4 + 4 * ks * M * 16 * rw;
+    return 64 * 4 * nu * M * xr + (bf ? 3 : 2) * 16 * nu * 4 + 4 * ks * M * 16 * rw;
 }
 
 // Row groups: enough threads to stage the activations two items per thread (4 bsu M
@@ -349,17 +345,17 @@ int bstream_rw(int64_t M, int bsu, bool gateup) {
     return rw;
 }
 
-// Waves a batched streaming workgroup may hold: 16, or 12 for bf16 with 8-unit slices (that
-// kernel is built for 768 threads, so it has 170 VGPRs).
+// Waves a batched streaming workgroup may hold: 16, or 12 for bf16 and fp32 (`bf`: a per-unit
+// prescale) with 8-unit slices (that kernel is built for 768 threads, so it has 170 VGPRs).
 int bstream_max_waves(int bsu, bool bf) { return bf && bsu == 8 ? 12 : 16; }
 
 // K splits of the batched streaming kernel for slices of bsu units.
-int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu, bool bf) {
+int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu, bool bf, int xr = 1) {
     const int64_t U = ceil_div(C, 4);
     int64_t P = std::max<int64_t>(1, std::min<int64_t>(split_k, U));
     while (P < U) {
         const int64_t ks = ceil_div(ceil_div(U, P), bsu);
-        if (ks * rw <= bstream_max_waves(bsu, bf) && bstream_lds(ks, M, rw, bsu, bf) <= LDS_BUDGET) break;
+        if (ks * rw <= bstream_max_waves(bsu, bf) && bstream_lds(ks, M, rw, bsu, bf, xr) <= LDS_BUDGET) break;
         ++P;
     }
     return (int)P;
@@ -370,7 +366,7 @@ int bstream_splits(int64_t C, int64_t M, int split_k, int rw, int bsu, bool bf) 
 // by at most two threads, an even number of row groups for gate-up, the LDS, one
 // projection per workgroup for mixed widths, 32-bit indices, and with P > 1 a counter
 // per row block in one window (the splits combine in the dispatch).
-BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu, int rw, bool bf) {
+BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu, int rw, bool bf, int xr = 1) {
     BStreamPlan bp;
     const int64_t U = ceil_div(A.C, 4);
     if (P < 1 || P > U || (int64_t)U * P >= (1ll << 32)) return bp;
@@ -380,7 +376,7 @@ BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu
     bp.rw = rw;
     bp.ks = (int)ceil_div(ceil_div(U, P), bsu);
     if (bp.ks * rw > bstream_max_waves(bsu, bf)) return bp;
-    bp.lds = (int)bstream_lds(bp.ks, A.M, rw, bsu, bf);
+    bp.lds = (int)bstream_lds(bp.ks, A.M, rw, bsu, bf, xr);
     if (bp.lds > LDS_BUDGET) return bp;
     const int rb = 16 * rw;
     if (mixed && (A.src[0].n % rb != 0 || A.src[1].n % rb != 0)) return bp;
@@ -403,13 +399,13 @@ BStreamPlan bstream_make(const GemvArgs& A, int mode, bool mixed, int P, int bsu
 constexpr int BSTREAM_CU_TARGET = 256;
 constexpr int BSTREAM_FILL_SPLITS = 4;
 
-BStreamPlan bstream_fill(const GemvArgs& A, int mode, bool mixed, int P0, bool bf) {
+BStreamPlan bstream_fill(const GemvArgs& A, int mode, bool mixed, int P0, bool bf, int xr = 1) {
     BStreamPlan best;
     int64_t best_key = INT64_MAX;
     for (int P = P0; P < P0 + BSTREAM_FILL_SPLITS; ++P) {
         for (int bsu : {4, 8}) {
             for (int rw = 1; rw <= 16; ++rw) {
-                const BStreamPlan c = bstream_make(A, mode, mixed, P, bsu, rw, bf);
+                const BStreamPlan c = bstream_make(A, mode, mixed, P, bsu, rw, bf, xr);
                 if (!c.ok) continue;
                 const int64_t dist = std::abs((int64_t)c.grid - BSTREAM_CU_TARGET);
                 const int64_t key = ((dist * 64 + (P - P0)) * 2 + (bsu == 8)) * 32 + rw;
@@ -425,14 +421,14 @@ BStreamPlan bstream_fill(const GemvArgs& A, int mode, bool mixed, int P0, bool b
 
 // The unsplit-first plan before any widening for the CU count: 4-unit slices with the
 // fewest splits that fit, or 8-unit slices where those need fewer splits.
-BStreamPlan bstream_base(int64_t M, int64_t C, int split_k, bool gateup, bool bf) {
+BStreamPlan bstream_base(int64_t M, int64_t C, int split_k, bool gateup, bool bf, int xr = 1) {
     BStreamPlan bp;
     bp.bsu = 4;
     bp.rw = bstream_rw(M, 4, gateup);
-    bp.P = bstream_splits(C, M, split_k, bp.rw, 4, bf);
+    bp.P = bstream_splits(C, M, split_k, bp.rw, 4, bf, xr);
     if (bp.P > std::max(split_k, 1)) {           // 4-unit slices would add a split: try 8
         const int rw8 = bstream_rw(M, 8, gateup);
-        const int p8 = bstream_splits(C, M, split_k, rw8, 8, bf);
+        const int p8 = bstream_splits(C, M, split_k, rw8, 8, bf, xr);
         if (p8 < bp.P) {
             bp.bsu = 8;
             bp.rw = rw8;
@@ -454,18 +450,21 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     // does not fit 128 VGPRs next to eight units of chunks; 170 hold it), so its plans keep to
     // 12 waves (bstream_max_waves).  W3 11008 -> 4096 batch 8: 22.7 us on the 1024-thread
     // build, which spilled, 19.3 on 4-unit slices, 14.8 on the 768-thread build (fp16 13.8).
-    const bool bf = dtype == CBK_BF16;
-    bool ok = A.M >= 3 && A.M <= 16 && (dtype == CBK_F16 || bf) && A.gs % 128 == 0 && A.K % 8 == 0 &&
-              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * 2 < lim;
+    // fp32 x stages two fp16 operand rows (hi, lo) per batch row (16 operand rows at most: batch
+    // 2..8) with a per-unit prescale like bf16's.
+    const bool bf = dtype != CBK_F16;
+    const int xr = dtype == CBK_F32 ? 2 : 1, xe = dtype == CBK_F32 ? 4 : 2;
+    bool ok = A.M >= 4 - xr && A.M * xr <= 16 && valid_dtype(dtype) && A.gs % 128 == 0 && A.K % 8 == 0 &&
+              reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * xe < lim;
     for (int i = 0; i < 3; ++i)
-        ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * 2 < lim;
+        ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * xe < lim;
     if (mode == CBK_MODE_QKV) ok = ok && A.src[0].n % 16 == 0 && A.src[1].n % 16 == 0;
     if (!ok) return bp;
     const bool gateup = mode == CBK_MODE_GATEUP;
     const int64_t U = ceil_div(A.C, 4);
-    bp = bstream_base(A.M, A.C, split_k, gateup, bf);
+    bp = bstream_base(A.M, A.C, split_k, gateup, bf, xr);
     if (bstream_fills(bp, A.V)) {
-        BStreamPlan fill = bstream_fill(A, mode, mixed, std::max(split_k, 1), bf);
+        BStreamPlan fill = bstream_fill(A, mode, mixed, std::max(split_k, 1), bf, xr);
         if (fill.ok) {
             fill.filled = true;
             return fill;
@@ -481,19 +480,19 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
         const int mw = bstream_max_waves(8, bf);
         if (mode == CBK_MODE_GEMV && !mixed && ceil_div(A.V, 16) >= (5 * (int64_t)cus) / 2) {
             int rw = (int)std::max<int64_t>(bstream_rw(A.M, 8, false), ceil_div(ceil_div(A.V, 16), cus));
-            if (U8 * rw <= mw && bstream_lds(U8, A.M, rw, 8, bf) <= LDS_BUDGET) {
+            if (U8 * rw <= mw && bstream_lds(U8, A.M, rw, 8, bf, xr) <= LDS_BUDGET) {
                 bp.bsu = 8;
                 bp.rw = rw;
             }
         } else if (gateup) {
             const int rw = bstream_rw(A.M, 8, true);
-            if (U8 * rw <= mw && bstream_lds(U8, A.M, rw, 8, bf) <= LDS_BUDGET) {
+            if (U8 * rw <= mw && bstream_lds(U8, A.M, rw, 8, bf, xr) <= LDS_BUDGET) {
                 bp.bsu = 8;
                 bp.rw = rw;
             }
         }
     }
-    return bstream_make(A, mode, mixed, bp.P, bp.bsu, bp.rw, bf);
+    return bstream_make(A, mode, mixed, bp.P, bp.bsu, bp.rw, bf, xr);
 }
 
 // Kernels (per device) whose dynamic-LDS limit has been raised to the whole budget.  The
@@ -555,7 +554,7 @@ DecodeLaunch plan_decode(GemvArgs& A, int dtype, int mode, bool mixed, int split
         A.divRW = make_fastdiv((uint32_t)A.st_rw);
         A.divG = make_fastdiv((uint32_t)(A.gs / 128));
         L.family = CBK_KERNEL_BSTREAM;
-        L.f = gemv_bstream_kernel_for(mode, A.bits[0], mixed, bp.bsu, dtype == CBK_BF16);
+        L.f = gemv_bstream_kernel_for(mode, A.bits[0], mixed, bp.bsu, dtype);
         L.grid = bp.grid;
         L.block = 64 * bp.ks * bp.rw;
         L.lds = bp.lds;
@@ -754,12 +753,13 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
     if (M <= 0 || V <= 0 || K <= 0 || group_size <= 0 || split_k < 1) return 0;
     int P = plan_any(M, V, K, split_k).P;
     if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M, dtype)));
-    if (M >= 3 && M <= 16) {  // 4-unit slices split at least as often as 8-unit ones; gate-up rows
+    const int xr = dtype == CBK_F32 ? 2 : 1;
+    if (M >= 4 - xr && M * xr <= 16) {  // 4-unit slices split at least as often as 8-unit ones; gate-up rows
         const int64_t C = ceil_div(K, 32);
-        const bool bf = dtype == CBK_BF16;
-        P = std::max(P, bstream_splits(C, M, split_k, bstream_rw(M, 4, true), 4, bf));
+        const bool bf = dtype != CBK_F16;
+        P = std::max(P, bstream_splits(C, M, split_k, bstream_rw(M, 4, true), 4, bf, xr));
         for (bool gateup : {false, true})     // bstream_fill takes at most P0 + 3 splits
-            if (bstream_fills(bstream_base(M, C, split_k, gateup, bf), V))
+            if (bstream_fills(bstream_base(M, C, split_k, gateup, bf, xr), V))
                 P = std::max<int64_t>(P, std::min<int64_t>(ceil_div(C, 4), split_k + BSTREAM_FILL_SPLITS - 1));
     }
     return P > 1 ? (int64_t)P * M * V : 0;

@@ -28,7 +28,7 @@ const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int r
 // gemv_stream.hip: batch 3..16, fp16 or bf16, group size % 128 == 0.  A job is 16 * st_rw virtual
 // rows x one K split (over 128-code units); its workgroup has st_ks * st_rw waves, each
 // over 16 rows and one K slice of bsu (4 or 8) units.
-const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu, bool bf16);
+const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu, int dt);
 
 // gemv_any.hip: any dtype / group size / alignment, on the fp32 matrix cores.  A job is
 // 16 virtual rows x 16 batch rows x one K split, one workgroup of 64 to ANY_MAX_THREADS

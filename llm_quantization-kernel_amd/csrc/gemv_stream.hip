@@ -2,7 +2,7 @@
 //
 // Replaces cb_gemv_kernel (Kernel/csrc/packed_gemv.cu:83-163) and, when the K
 // range is split, the partial write that cb_reduce_kernel (:166-180) combines,
-// for one or two activation rows (the decode step) in fp16, bf16 or fp32 (an fp32 row as two
+// for one or two activation rows (the decode step) in fp16 or bf16, or one fp32 row (as two
 // fp16 operand rows), with any group size that is a multiple of 32.  Plain, fused-QKV and
 // fused gate-up modes share the body; the
 // outputs are finished per row (plain) or row pair (fused modes; finish, cbk_device.hpp).
@@ -199,7 +199,8 @@ __device__ __forceinline__ void load_x32(__amdgpu_buffer_rsrc_t xr, bool ok, int
 // to 2^-22 of the chunk's largest value (subnormal lo parts lose bits only below 2^-39 of it).
 // Both rows meet the same decoded weights; their terms add before the scale 2^c.  The
 // weights' pairs 1024 + 2^e q lose their 1024 first (exact in fp16), so the dot products
-// carry no 1024 sum x term whose cancellation would cost fp32 bits: B = 0.
+// carry no 1024 sum x term whose cancellation would cost fp32 bits: B = 0.  convert_x_f32_at
+// takes the prescale exponent c (the batched kernel shares one per 128-code unit).
 __device__ __forceinline__ int chunk_exp_f32(const uint32_t (&x)[32]) {
     uint32_t m = 0;
 #pragma unroll
@@ -208,9 +209,8 @@ __device__ __forceinline__ int chunk_exp_f32(const uint32_t (&x)[32]) {
 }
 
 template <int BITS>
-__device__ __forceinline__ void convert_x_f32(const uint32_t (&x)[32], u4 (&Xh)[4], u4 (&Xl)[4], float& Bh,
-                                              float& xsh, float& Bl, float& xsl, float& f) {
-    const int c = prescale_bf16(chunk_exp_f32(x));
+__device__ __forceinline__ void convert_x_f32_at(const uint32_t (&x)[32], int c, u4 (&Xh)[4], u4 (&Xl)[4],
+                                                 float& xsh, float& xsl) {
     uint32_t oh[16], ol[16];
     float th = 0.f, tl = 0.f;
 #pragma unroll
@@ -232,10 +232,17 @@ __device__ __forceinline__ void convert_x_f32(const uint32_t (&x)[32], u4 (&Xh)[
         Xh[q] = u4{oh[4 * q], oh[4 * q + 1], oh[4 * q + 2], oh[4 * q + 3]};
         Xl[q] = u4{ol[4 * q], ol[4 * q + 1], ol[4 * q + 2], ol[4 * q + 3]};
     }
-    Bh = 0.f;
     xsh = th;
-    Bl = 0.f;
     xsl = tl;
+}
+
+template <int BITS>
+__device__ __forceinline__ void convert_x_f32(const uint32_t (&x)[32], u4 (&Xh)[4], u4 (&Xl)[4], float& Bh,
+                                              float& xsh, float& Bl, float& xsl, float& f) {
+    const int c = prescale_bf16(chunk_exp_f32(x));
+    convert_x_f32_at<BITS>(x, c, Xh, Xl, xsh, xsl);
+    Bh = 0.f;
+    Bl = 0.f;
     f = __builtin_ldexpf(1.0f, c);
 }
 
@@ -568,19 +575,23 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     // i) = (t mod NCH, t / NCH); the host keeps NCH * M <= 2 * nthr, so these are all of
     // them, and they are requested before the weights so that the staging waits for
     // them only
+    constexpr int XE = DT == DT_F32 ? 4 : 2;           // bytes of an activation / scale / zero
+    constexpr int OPR = DT == DT_F32 ? 2 : 1;          // operand rows per batch row (fp32: hi, lo)
+    const int MR = OPR * M;                            // staged operand rows (<= 16)
     const __amdgpu_buffer_rsrc_t xr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * 2, RAW);
-    uint32_t xa[2][16];
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(A.x), (short)0, A.M * A.K * XE, RAW);
+    uint32_t xa[2][DT == DT_F32 ? 32 : 16];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int t = tid + e * nthr, i = t / NCH, c = t - i * NCH;
-        load_x(xr, i < M && c < nrange, i, c0 + c, A.K, xa[e]);
+        if constexpr (DT == DT_F32) load_x32(xr, i < M && c < nrange, i, c0 + c, A.K, xa[e]);
+        else load_x(xr, i < M && c < nrange, i, c0 + c, A.K, xa[e]);
     }
 
     // 1b. the wave's packed chunks and the (scale, zero) of each unit's group
     // the wave's projection, selected once (by masks: no branches in front of the loads)
     const Src S = MODE == MODE_GEMV ? A.src[0] : src_of(A, proj);
-    const ProjRes P = proj_res(S, A.G);
+    const ProjRes P = proj_res(S, A.G, XE);
     const int wpr = S.wpr;
     // the (scale, zero) of unit 4 e + kq's group of row j: BSU / 4 2-byte gathers each per
     // wave (lanes of a row then share them by ds_bpermute), rather than one per unit
@@ -590,9 +601,14 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
     for (int e = 0; e < BSU / 4; ++e) {
         const int ul = ks * BSU + 4 * e + kq;
         const int gu = (int)fdiv((uint32_t)(u0 + ul), A.divG);   // the unit's group
-        const int so = vofs(vin && 4 * ul < nrange, 2 * (r * A.G + gu));
-        s_own[e] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
-        z_own[e] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
+        const int so = vofs(vin && 4 * ul < nrange, XE * (r * A.G + gu));
+        if constexpr (DT == DT_F32) {
+            s_own[e] = __builtin_amdgcn_raw_buffer_load_b32(P.s, so, 0, 0);
+            z_own[e] = __builtin_amdgcn_raw_buffer_load_b32(P.z, so, 0, 0);
+        } else {
+            s_own[e] = __builtin_amdgcn_raw_buffer_load_b16(P.s, so, 0, 0);
+            z_own[e] = __builtin_amdgcn_raw_buffer_load_b16(P.z, so, 0, 0);
+        }
     }
     uint32_t w[BSU][BITS];
 #pragma unroll
@@ -603,49 +619,79 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
         __builtin_amdgcn_sched_barrier(0);        // units issued in the order they are consumed
     }
 
-    // 2. activations -> LDS: piece m of chunk c of batch row i at ((m NCH + c) M + i) * 16;
-    // per unit and batch row its sums X (at XSu[u * 16 + i]) and XB (XBu[u * 16 + i]), and
-    // for bf16 the unit's prescale 2^c (XFu[u * 16 + i]; the four chunks of a unit share
-    // c, from their largest exponent, since the MFMA sums over the unit)
+    // 2. activations -> LDS: piece m of chunk c of operand row o at ((m NCH + c) MR + o) * 16;
+    // per unit and operand row its sums X (at XSu[u * 16 + o]) and XB (XBu[u * 16 + o]), and
+    // for bf16 and fp32 the unit's prescale 2^c (XFu[u * 16 + o]; the four chunks of a unit
+    // share c, from their largest exponent, since the MFMA sums over the unit).  Operand row o
+    // is batch row o, or for fp32 half o & 1 (hi, lo) of batch row o >> 1, whose decoded
+    // pairs lose their 1024 (XB = 0).
     u4* Xl = reinterpret_cast<u4*>(lds);
-    float* XSu = reinterpret_cast<float*>(lds + 64 * NCH * M);
+    float* XSu = reinterpret_cast<float*>(lds + 64 * NCH * MR);
     float* XBu = XSu + 16 * NU;
     float* XFu = XBu + 16 * NU;
-    float* red = XBu + (DT == DT_BF16 ? 32 : 16) * NU;
+    float* red = XBu + (DT != DT_F16 ? 32 : 16) * NU;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int t = tid + e * nthr, i = t / NCH, c = t - i * NCH;
         if (t >= NCH * M) break;                  // whole quads of threads leave together (NCH % 4 == 0)
-        u4 X[4];
-        float B, xs;
-        int cu = 0;
-        if constexpr (DT == DT_BF16) {
-            int E = chunk_exp_bf16(xa[e]);
+        if constexpr (DT == DT_F32) {
+            int E = chunk_exp_f32(xa[e]);
             E = max(E, __shfl_xor(E, 1, 64));
             E = max(E, __shfl_xor(E, 2, 64));
-            cu = prescale_bf16(E);
-            convert_x_bf16_at<BITS>(xa[e], cu, X, B, xs);
-        } else {
-            convert_x<BITS>(xa[e], X, B, xs);
-        }
+            const int cu = prescale_bf16(E);
+            u4 Xh[4], Xo[4];
+            float xsh, xso;
+            convert_x_f32_at<BITS>(xa[e], cu, Xh, Xo, xsh, xso);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) Xl[(m * NCH + c) * M + i] = X[m];
-        // the 4 chunks of a unit are 4 consecutive threads (NCH % 4 == 0)
-        B += __shfl_xor(B, 1, 64);
-        xs += __shfl_xor(xs, 1, 64);
-        B += __shfl_xor(B, 2, 64);
-        xs += __shfl_xor(xs, 2, 64);
-        if ((c & 3) == 0) {
-            XSu[(c >> 2) * 16 + i] = xs;
-            XBu[(c >> 2) * 16 + i] = B;
-            if constexpr (DT == DT_BF16) XFu[(c >> 2) * 16 + i] = __builtin_ldexpf(1.0f, cu);
+            for (int m = 0; m < 4; ++m) {
+                Xl[(m * NCH + c) * MR + 2 * i] = Xh[m];
+                Xl[(m * NCH + c) * MR + 2 * i + 1] = Xo[m];
+            }
+            xsh += __shfl_xor(xsh, 1, 64);
+            xso += __shfl_xor(xso, 1, 64);
+            xsh += __shfl_xor(xsh, 2, 64);
+            xso += __shfl_xor(xso, 2, 64);
+            if ((c & 3) == 0) {
+                const float f = __builtin_ldexpf(1.0f, cu);
+                XSu[(c >> 2) * 16 + 2 * i] = xsh;
+                XSu[(c >> 2) * 16 + 2 * i + 1] = xso;
+                XBu[(c >> 2) * 16 + 2 * i] = 0.f;
+                XBu[(c >> 2) * 16 + 2 * i + 1] = 0.f;
+                XFu[(c >> 2) * 16 + 2 * i] = f;
+                XFu[(c >> 2) * 16 + 2 * i + 1] = f;
+            }
+        } else {
+            u4 X[4];
+            float B, xs;
+            int cu = 0;
+            if constexpr (DT == DT_BF16) {
+                int E = chunk_exp_bf16(xa[e]);
+                E = max(E, __shfl_xor(E, 1, 64));
+                E = max(E, __shfl_xor(E, 2, 64));
+                cu = prescale_bf16(E);
+                convert_x_bf16_at<BITS>(xa[e], cu, X, B, xs);
+            } else {
+                convert_x<BITS>(xa[e], X, B, xs);
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m) Xl[(m * NCH + c) * M + i] = X[m];
+            // the 4 chunks of a unit are 4 consecutive threads (NCH % 4 == 0)
+            B += __shfl_xor(B, 1, 64);
+            xs += __shfl_xor(xs, 1, 64);
+            B += __shfl_xor(B, 2, 64);
+            xs += __shfl_xor(xs, 2, 64);
+            if ((c & 3) == 0) {
+                XSu[(c >> 2) * 16 + i] = xs;
+                XBu[(c >> 2) * 16 + i] = B;
+                if constexpr (DT == DT_BF16) XFu[(c >> 2) * 16 + i] = __builtin_ldexpf(1.0f, cu);
+            }
         }
     }
     lds_barrier();
 
-    // 3. units: A operands of batch row min(j, M - 1) (rows past M repeat a staged row;
+    // 3. units: A operands of operand row min(j, MR - 1) (rows past MR repeat a staged row;
     // their D rows are not stored)
-    const int ia = min(j, M - 1);
+    const int ia = min(j, MR - 1);
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < BSU; ++u) {
@@ -653,11 +699,16 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
         const int c = 4 * uj + kq;
         u4 a[4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) a[m] = Xl[(m * NCH + c) * M + ia];
+        for (int m = 0; m < 4; ++m) a[m] = Xl[(m * NCH + c) * MR + ia];
         const f4 X4 = *reinterpret_cast<const f4*>(XSu + uj * 16 + 4 * kq);
         const f4 XB4 = *reinterpret_cast<const f4*>(XBu + uj * 16 + 4 * kq);
         uint32_t h[16];
         Decode<BITS>::run(w[u], h, g);
+        if constexpr (DT == DT_F32) {
+            const h2 off = {(_Float16)1024.f, (_Float16)1024.f};
+#pragma unroll
+            for (int q = 0; q < 16; ++q) h[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, h[q]) - off);
+        }
         f4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -670,7 +721,7 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
         const uint32_t zu = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (j + 16 * (u & 3)), (int)z_own[u >> 2]);
         const float sc = meta_f<DT>(su);
         const float ze = meta_f<DT>(zu);
-        if constexpr (DT == DT_BF16) {
+        if constexpr (DT != DT_F16) {
             const f4 F4 = *reinterpret_cast<const f4*>(XFu + uj * 16 + 4 * kq);
 #pragma unroll
             for (int q = 0; q < 4; ++q) acc[q] = fmaf(sc, fmaf(-ze, X4[q], d[q] - XB4[q]) * F4[q], acc[q]);
@@ -680,11 +731,20 @@ __device__ __forceinline__ void bstream_body(const GemvArgs& A, char* lds) {
         }
     }
 
-    // 4. row totals per slice: lane (j, kq) holds batch rows 4 kq + q of row j
+    // 4. row totals per slice: lane (j, kq) holds operand rows 4 kq + q of row j (fp32: the
+    // hi and lo rows of batch rows 2 kq and 2 kq + 1)
+    if constexpr (DT == DT_F32) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int i = 4 * kq + q;
-        if (i < M) red[(ks * M + i) * RB + roff] = acc[q];
+        for (int h = 0; h < 2; ++h) {
+            const int i = 2 * kq + h;
+            if (i < M) red[(ks * M + i) * RB + roff] = acc[2 * h] + acc[2 * h + 1];
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = 4 * kq + q;
+            if (i < M) red[(ks * M + i) * RB + roff] = acc[q];
+        }
     }
     lds_barrier();
 }
@@ -703,7 +763,8 @@ __device__ __forceinline__ void bstream_tail(const GemvArgs& A, char* lds) {
     const int blk = (int)fdiv(blockIdx.x, A.divP);
     const int p = blockIdx.x - blk * A.P;
     const int vbase = blk * RB;
-    float* red = reinterpret_cast<float*>(lds + 64 * NCH * M) + (DT == DT_BF16 ? 48 : 32) * NU;
+    constexpr int OPR = DT == DT_F32 ? 2 : 1;
+    float* red = reinterpret_cast<float*>(lds + 64 * NCH * M * OPR) + (DT != DT_F16 ? 48 : 32) * NU;
     constexpr int FU = FINISH_ROWS<MODE>;
     constexpr int LOG = FU == 2 ? 3 : 4;          // log2(16 / FU)
     const int NFU = RB / FU;
@@ -725,11 +786,11 @@ __device__ __forceinline__ void bstream_tail(const GemvArgs& A, char* lds) {
         split_finish<DT, MODE>(A, vbase, RB, nthr);
 }
 
-// bf16 with 8-unit slices: 768 threads at most, so 170 VGPRs (its per-unit prescale does
-// not fit 128 next to eight units of streamed chunks); the planner keeps such workgroups to
-// 12 waves.
+// bf16 and fp32 with 8-unit slices: 768 threads at most, so 170 VGPRs (the per-unit
+// prescale does not fit 128 next to eight units of streamed chunks); the planner keeps such
+// workgroups to 12 waves.
 template <int MODE, int BITS, int BSU, int DT>
-__global__ void __launch_bounds__(DT == DT_BF16 && BSU == 8 ? 768 : 1024) gemv_bstream_kernel(const GemvArgs A) {
+__global__ void __launch_bounds__(DT != DT_F16 && BSU == 8 ? 768 : 1024) gemv_bstream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
         bstream_body<BITS, MODE, BSU, DT>(A, lds);
@@ -750,10 +811,8 @@ __global__ void __launch_bounds__(DT == DT_BF16 && BSU == 8 ? 768 : 1024) gemv_b
 // the activations, which at K = 11008 leaves one workgroup per CU; they take the
 // batch-rows MFMA kernel instead.  RPW rows per wave (4, or 8 for the host's short-K
 // batch-1 plan: half the waves for the same rows per workgroup).
-// fp32 at batch 2 stages four operand rows, more than 128 VGPRs hold: a 512-thread build (256
-// VGPRs), and the host keeps its plans to 8 waves.
 template <int MODE, int BITS, int MB, int RPW, int DT>
-__global__ void __launch_bounds__(DT == DT_F32 && MB == 2 ? 512 : 1024) gemv_stream_kernel(const GemvArgs A) {
+__global__ void __launch_bounds__(1024) gemv_stream_kernel(const GemvArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     if constexpr (BITS != 0) {
         stream_body<BITS, MODE, MB, RPW, DT>(A, lds);
@@ -798,7 +857,8 @@ const void* bstream_kernel(int mode, int bits, bool mixed) {
 
 template <int DT>
 const void* stream_kernel_dt(int mode, int bits, bool mixed, int mb, int rpw) {
-    if (mb > 1) return stream_kernel<2, STREAM_RPW, DT>(mode, bits, mixed);
+    if constexpr (DT != DT_F32)                        // fp32 streams at batch 1 only
+        if (mb > 1) return stream_kernel<2, STREAM_RPW, DT>(mode, bits, mixed);
     if (rpw == STREAM_RPW_WIDE && mode == MODE_GEMV && !mixed) {     // the host plans 8 rows for plain GEMVs only
         constexpr int W = STREAM_RPW_WIDE;
         return bits == 2 ? reinterpret_cast<const void*>(&gemv_stream_kernel<MODE_GEMV, 2, 1, W, DT>)
@@ -814,8 +874,11 @@ const void* gemv_stream_kernel_for(int mode, int bits, bool mixed, int mb, int r
                                          : stream_kernel_dt<DT_F16>(mode, bits, mixed, mb, rpw));
 }
 
-const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu, bool bf16) {
-    if (bf16) return bsu == 8 ? bstream_kernel<8, DT_BF16>(mode, bits, mixed) : bstream_kernel<4, DT_BF16>(mode, bits, mixed);
+const void* gemv_bstream_kernel_for(int mode, int bits, bool mixed, int bsu, int dt) {
+    if (dt == DT_BF16)
+        return bsu == 8 ? bstream_kernel<8, DT_BF16>(mode, bits, mixed) : bstream_kernel<4, DT_BF16>(mode, bits, mixed);
+    if (dt == DT_F32)
+        return bsu == 8 ? bstream_kernel<8, DT_F32>(mode, bits, mixed) : bstream_kernel<4, DT_F32>(mode, bits, mixed);
     return bsu == 8 ? bstream_kernel<8, DT_F16>(mode, bits, mixed) : bstream_kernel<4, DT_F16>(mode, bits, mixed);
 }
 

@@ -167,3 +167,5 @@ def test_partial_query():
     assert lib.cbk_gemv_partial_floats(0, 2, 4096, 4096, 128, 4) == 4 * 2 * 4096
     # fp16 batch 16 x K 16384 needs more LDS than one workgroup holds -> forced split
     assert lib.cbk_gemv_partial_floats(0, 16, 64, 16384, 128, 1) > 0
+    # fp32 batch 8 stages 16 operand rows: K 11008 needs at least 3 splits for the LDS
+    assert lib.cbk_gemv_partial_floats(2, 8, 4096, 11008, 128, 1) >= 3 * 8 * 4096

@@ -25,10 +25,13 @@ def plan(dtype, M, K, gs, out, bits, kind="gemv", split_k=1):
     return fam, splits, threads, launches
 
 
-def fp32_family(M, K):
-    """Decode family of an unsplit fp32 call: streaming at batch 1, and at batch 2 while K
-    fits two row groups a workgroup in the 8 waves of its 512-thread build (K <= 8192)."""
-    return "stream" if M == 1 or (M == 2 and K <= 8192) else "generic"
+def fp32_family(M, K, gs=128):
+    """Decode family of an fp32 call: streaming at batch 1, the batched streaming kernel at
+    batch 2..8 (two operand rows per batch row, 16 at most; groups of whole 128-code units), the
+    fp32 matrix-core kernel otherwise."""
+    if M == 1:
+        return "stream"
+    return "bstream" if 2 <= M <= 8 and gs % 128 == 0 else "generic"
 
 
 # ------------------------------------------------------------------ fp32 activations
@@ -37,27 +40,35 @@ def fp32_family(M, K):
 @pytest.mark.parametrize("K,N", BASELINE)
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_fp32_decode_baseline_shapes(hip, bits, K, N, M):
-    """fp32 x at the BASELINE decode shapes: the streaming kernel at batch 1 and 2 (two fp16
-    operand rows per chunk and batch row; batch 2 only where a workgroup holds two row groups,
-    K <= 8192 unsplit), the fp32 matrix-core kernel otherwise; one launch, within the fp32 bar."""
+    """fp32 x at the BASELINE decode shapes: the streaming kernel at batch 1 (two fp16 operand
+    rows per chunk) and the batched streaming kernel at batch 2, 4 and 8 (two operand rows per
+    batch row; K splits combined in the dispatch where the staged rows need them); one launch,
+    within the fp32 bar."""
     fam, splits, threads, launches = plan(torch.float32, M, K, 128, N, bits)
-    assert (fam, splits, launches) == (fp32_family(M, K), 1, 1), (fam, splits, launches)
+    assert (fam, launches) == (fp32_family(M, K), 1), (fam, splits, launches)
+    assert splits == 1 or fam == "bstream", (fam, splits)
     assert threads % 64 == 0 and 64 <= threads <= 1024
     w, W64, _, _ = make(N, K, bits, torch.float32, scale=0.02)
     x = randx(M, K, torch.float32, seed=10 + M)
-    close(packed_linear(x, w), ref_linear(x, W64), torch.float32)
+    close(packed_linear(x, w, decode_threshold=16), ref_linear(x, W64), torch.float32)
 
 
 @pytest.mark.parametrize("split_k", [2, 5, 64])
-@pytest.mark.parametrize("M", [1, 2, 3, 16, 20])
+@pytest.mark.parametrize("M", [1, 2, 3, 8, 16, 20])
 def test_fp32_decode_splits(hip, split_k, M):
-    """K splits of the fp32 decode (the streaming kernel at batch 1-2, the fp32 matrix-core
-    kernel above) combine inside the dispatch (the last split of each block adds the
-    partials); the result matches the unsplit call within the bar and repeats bit for bit."""
+    """K splits of the fp32 decode (the streaming kernel at batch 1, the batched streaming
+    kernel at 2-8, the fp32 matrix-core kernel above) combine inside the dispatch (the last
+    split of each block adds the partials); the result matches the unsplit call within the bar
+    and repeats bit for bit.  The batched kernel may add up to 3 splits to fill the CUs."""
     w, W64, b64, _ = make(600, 4128, 3, torch.float32, bias=True)
     x = randx(M, 4128, torch.float32, seed=M)
     fam, splits, _, launches = plan(torch.float32, M, 4128, 128, 600, 3, split_k=split_k)
-    assert fam == fp32_family(M, 4128) and splits == split_k and launches == 1
+    assert fam == fp32_family(M, 4128) and launches == 1, (fam, splits, launches)
+    units = -(-4128 // 128)
+    if fam == "bstream":
+        assert min(split_k, units) <= splits <= split_k + 3, splits
+    else:
+        assert splits == split_k, splits
     y = packed_linear(x, w, split_k, 1, "silu", decode_threshold=32)
     close(y, ref_linear(x, W64, b64, "silu"), torch.float32)
     assert torch.equal(packed_linear(x, w, split_k, 1, "silu", decode_threshold=32), y)
@@ -66,17 +77,50 @@ def test_fp32_decode_splits(hip, split_k, M):
 @pytest.mark.parametrize("dist", ["normal", "wide", "tiny", "outlier"])
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("K,N", BASELINE)
-@pytest.mark.parametrize("M", [1, 2])
-def test_fp32_streaming_activation_ranges(hip, dist, bits, K, N, M):
-    """fp32 x at batch 1-2 on the streaming kernel: each 32-code chunk is prescaled by its own
+def test_fp32_streaming_activation_ranges(hip, dist, bits, K, N):
+    """fp32 x at batch 1 on the streaming kernel: each 32-code chunk is prescaled by its own
     power of two and split into two fp16 operands (hi, lo), so fp32 activations of any range
     keep fp32 accuracy -- N(0,1), values spread over 2^-40..2^40 ("wide"), all below 1e-30
-    ("tiny") and a few channels 1e4 times the rest ("outlier") -- within the fp32 bar.  Batch 2
-    at K = 11008 streams with two K splits (unsplit it takes the fp32 matrix-core kernel)."""
-    split_k = 2 if M == 2 and K > 8192 else 1
-    assert plan(torch.float32, M, K, 128, N, bits, split_k=split_k)[0] == "stream"
+    ("tiny") and a few channels 1e4 times the rest ("outlier") -- within the fp32 bar."""
+    assert plan(torch.float32, 1, K, 128, N, bits)[0] == "stream"
     w, W64, _, _ = make(N, K, bits, torch.float32, scale=0.02)
-    g = torch.Generator().manual_seed(bits + K + M)
+    g = torch.Generator().manual_seed(bits + K)
+    x = torch.randn(1, K, generator=g, dtype=torch.float64)
+    if dist == "wide":
+        x = x * torch.exp2(torch.randint(-40, 41, (1, K), generator=g).double())
+    elif dist == "tiny":
+        x = x * 1e-32
+    elif dist == "outlier":
+        x[0, torch.randperm(K, generator=g)[:4]] *= 1e4
+    x = x.float().cuda()
+    close(packed_linear(x, w), ref_linear(x, W64), torch.float32)
+
+
+@pytest.mark.parametrize("gs", [32, 64, 256])
+@pytest.mark.parametrize("K", [200, 1000, 4128])
+@pytest.mark.parametrize("M", [1, 2])
+def test_fp32_streaming_groups_and_ragged_k(hip, gs, K, M):
+    """Batch-1 and -2 fp32 with group sizes 32..256 and K not a multiple of 32 (the last
+    chunk's pieces past K read as zero), bias and SiLU, against the oracle: the streaming kernel
+    at batch 1; at batch 2 the batched kernel for groups of 256, the fp32 matrix-core kernel for
+    groups of 32 and 64."""
+    w, W64, b64, _ = make(300, K, 3, torch.float32, bias=True, gs=gs)
+    x = randx(M, K, torch.float32, seed=K + M)
+    assert plan(torch.float32, M, K, gs, 300, 3)[0] == fp32_family(M, K, gs)
+    close(packed_linear(x, w, act="silu"), ref_linear(x, W64, b64, "silu"), torch.float32)
+
+
+@pytest.mark.parametrize("dist", ["normal", "wide", "tiny", "outlier"])
+@pytest.mark.parametrize("K,N", BASELINE)
+@pytest.mark.parametrize("M", [2, 3, 5, 8])
+def test_fp32_batched_activation_ranges(hip, dist, K, N, M):
+    """fp32 x at batch 2..8 on the batched streaming kernel: each batch row is staged as two fp16
+    operand rows (hi, lo) behind one power-of-two prescale per 128-code unit, so fp32 activations
+    of any range keep fp32 accuracy (the activation ranges of the batch-1 test; batch rows of
+    different magnitude), within the fp32 bar."""
+    assert plan(torch.float32, M, K, 128, N, 3)[0] == "bstream"
+    w, W64, _, _ = make(N, K, 3, torch.float32, scale=0.02)
+    g = torch.Generator().manual_seed(K + M)
     x = torch.randn(M, K, generator=g, dtype=torch.float64)
     if dist == "wide":
         x = x * torch.exp2(torch.randint(-40, 41, (M, K), generator=g).double())
@@ -84,21 +128,22 @@ def test_fp32_streaming_activation_ranges(hip, dist, bits, K, N, M):
         x = x * 1e-32
     elif dist == "outlier":
         x[:, torch.randperm(K, generator=g)[:4]] *= 1e4
-        x[M - 1] *= 1e-3                                   # batch rows of different magnitude
+        x[M - 1] *= 1e-3
     x = x.float().cuda()
-    close(packed_linear(x, w, split_k), ref_linear(x, W64), torch.float32)
+    close(packed_linear(x, w, decode_threshold=16), ref_linear(x, W64), torch.float32)
 
 
-@pytest.mark.parametrize("gs", [32, 64, 256])
-@pytest.mark.parametrize("K", [200, 1000, 4128])
-@pytest.mark.parametrize("M", [1, 2])
-def test_fp32_streaming_groups_and_ragged_k(hip, gs, K, M):
-    """Batch-1 and -2 fp32 streaming with group sizes 32..256 and K not a multiple of 32 (the
-    last chunk's pieces past K read as zero), bias and SiLU, against the oracle."""
-    w, W64, b64, _ = make(300, K, 3, torch.float32, bias=True, gs=gs)
+@pytest.mark.parametrize("gs", [128, 256])
+@pytest.mark.parametrize("K", [1000, 4128, 11008])
+@pytest.mark.parametrize("M", [3, 4, 7, 8])
+def test_fp32_batched_groups_and_ragged_k(hip, gs, K, M):
+    """Batch 3..8 fp32 on the batched streaming kernel with groups of 128 and 256 and K not a
+    multiple of 32 or 128 (pieces past K read as zero), bias and SiLU, against the oracle."""
+    w, W64, b64, _ = make(300, K, 4, torch.float32, bias=True, gs=gs)
     x = randx(M, K, torch.float32, seed=K + M)
-    assert plan(torch.float32, M, K, gs, 300, 3)[0] == "stream"
-    close(packed_linear(x, w, act="silu"), ref_linear(x, W64, b64, "silu"), torch.float32)
+    assert plan(torch.float32, M, K, gs, 300, 4)[0] == "bstream"
+    y = packed_linear(x, w, act="silu", decode_threshold=16)
+    close(y, ref_linear(x, W64, b64, "silu"), torch.float32)
 
 
 @pytest.mark.parametrize("B", [1, 2, 5, 16])
