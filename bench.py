@@ -223,8 +223,8 @@ def _median_ms(fn, warm=2, runs=5):
 
 
 def cpu_baseline(torch, dev, base, xs):
-    """The reference's CPU path on the host cores (BASELINE.md section 3 protocol) on the same seeded
-    inputs as the GPU: the oracle's restatement of reference.py unpack_codes -> dequantize
+    """The reference's CPU path on the host cores (dequantize + matmul, and the matmul alone) on
+    the same seeded inputs as the GPU: the oracle's restatement of reference.py unpack_codes -> dequantize
     (reference.py:30-34,58-67; unpack by code slot, oracle.reference.unpack_codes_by_slot, then
     (q - z) s in fp32) followed by x.float() @ W.T (test_correctness.py:23-31), torch on every core
     this process may use.  Two numbers per config: dequant + matmul per call, and the matmul alone
