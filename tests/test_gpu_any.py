@@ -207,10 +207,10 @@ def test_batches_past_16(hip, M, bits):
     close(packed_linear(x, w, 1, 1, decode_threshold=64), ref_linear(x, W64), torch.float16)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("M", [1, 2, 6])
 def test_unaligned_activations(hip, dtype, M):
-    """A contiguous x whose rows do not start on 16-byte boundaries (a view 2 bytes into
+    """A contiguous x whose rows do not start on 16-byte boundaries (a view one element into
     its buffer): the streaming kernels refuse it and the fp32 matrix-core kernel takes
     element loads."""
     w, W64, _, _ = make(300, 1000, 3, dtype)
