@@ -240,6 +240,25 @@ def test_prefill_gemm(hip, bits, M, act, dtype):
     close(packed_linear(x, w, act=act), ref_linear(x, W64, b64, act), tol_dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K", [404, 1000])
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_prefill_matrix_core_contract_off_the_fast_kernel(hip, dtype, K, act):
+    """16-bit x that the staged matrix-core GEMM does not take (K % 8 != 0, or rows 2 bytes off
+    16-byte alignment) runs on the matrix-core fallback (csrc/gemm.hip) under the same contract,
+    W-hat rounded to T (packed_gemm.cu:56,60), against the oracle's rounded W-hat."""
+    w, W64, b64, d = make(200, K, 3, dtype, bias=True)
+    x = randx(70, K, dtype)
+    if K % 8 == 0:
+        xs = torch.empty(70 * K + 1, dtype=dtype, device="cuda")[1:].view(70, K)
+        xs.copy_(x)
+        x = xs
+        assert x.data_ptr() % 16 != 0
+    y = _C.packed_gemm(x, w.packed, w.scales, w.zeros, w.bias, 3, K, 128, ops.ACT[act], True)
+    tol_dtype = torch.bfloat16 if dtype == torch.bfloat16 else torch.float16
+    close(y, gemm_ref(x, d, dtype, 3, K, 128, b64, act, True), tol_dtype)
+
+
 @pytest.mark.parametrize("gs", [32, 64, 256])
 def test_prefill_group_sizes(hip, gs):
     w, _, _, d = make(300, 640, 3, torch.float16, gs=gs)
