@@ -313,8 +313,8 @@ StreamPlan plan_stream(const GemvArgs& A, int dtype, int mode, bool mixed, int s
     return sp;
 }
 
-// Batched streaming plan (gemv_stream.hip, bstream), batch 3..16: fp16 or bf16 x with
-// 16-byte pieces, group sizes that are multiples of 128 (a unit of 128 codes is one
+// Batched streaming plan (gemv_stream.hip, bstream), batch 3..16 for fp16 or bf16 x and
+// 2..8 for fp32 x, with 16-byte pieces, group sizes that are multiples of 128 (a unit of 128 codes is one
 // group), 32-bit offsets, and rows that keep every 16-row tile inside one projection
 // (fused QKV: Q and K widths multiples of 16; mixed widths: of the workgroup's rows).
 // K is split over units; a split's units are cut into slices of bsu units (one wave
@@ -454,7 +454,8 @@ BStreamPlan plan_bstream(const GemvArgs& A, int dtype, int mode, bool mixed, int
     // 2..8) with a per-unit prescale like bf16's.
     const bool bf = dtype != CBK_F16;
     const int xr = dtype == CBK_F32 ? 2 : 1, xe = dtype == CBK_F32 ? 4 : 2;
-    bool ok = A.M >= 4 - xr && A.M * xr <= 16 && valid_dtype(dtype) && A.gs % 128 == 0 && A.K % 8 == 0 &&
+    const int mmin = dtype == CBK_F32 ? 2 : 3;         // below: the batch-1/2 streaming kernel
+    bool ok = A.M >= mmin && A.M * xr <= 16 && valid_dtype(dtype) && A.gs % 128 == 0 && A.K % 8 == 0 &&
               reinterpret_cast<uintptr_t>(A.x) % 16 == 0 && (int64_t)A.M * A.K * xe < lim;
     for (int i = 0; i < 3; ++i)
         ok = ok && (int64_t)A.src[i].n * A.src[i].wpr * 4 < lim && (int64_t)A.src[i].n * A.G * xe < lim;
@@ -754,7 +755,7 @@ int64_t cbk_gemv_partial_floats(int dtype, int64_t M, int64_t V, int64_t K, int 
     int P = plan_any(M, V, K, split_k).P;
     if (M <= 2) P = std::max(P, stream_splits(ceil_div(K, 32), split_k, stream_max_slices((int)M, dtype)));
     const int xr = dtype == CBK_F32 ? 2 : 1;
-    if (M >= 4 - xr && M * xr <= 16) {  // 4-unit slices split at least as often as 8-unit ones; gate-up rows
+    if (M >= (dtype == CBK_F32 ? 2 : 3) && M * xr <= 16) {  // 4-unit slices split at least as often as 8-unit ones; gate-up rows
         const int64_t C = ceil_div(K, 32);
         const bool bf = dtype != CBK_F16;
         P = std::max(P, bstream_splits(C, M, split_k, bstream_rw(M, 4, true), 4, bf, xr));

@@ -518,6 +518,8 @@ __device__ __forceinline__ void stream_tail(const GemvArgs& A, char* lds) {
 }
 
 // ------------------------------------------------------------------ batch rows 3..16
+// (fp32: 2..8, each batch row staged as two fp16 operand rows, hi and lo, so the 16 MFMA
+// batch rows hold 8 batch rows; a lane adds its hi and lo rows' totals at the end)
 // Job = (block of RB = 16 RW virtual rows, K split p over 128-code units).  A
 // workgroup holds KS x RW waves: wave (ks, rw) takes 16 rows of the block over K
 // slice ks, BSU (4 or 8) units; lane (j = l & 15, kq = l >> 4) owns chunk 4 u + kq of row j
