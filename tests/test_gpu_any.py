@@ -146,9 +146,11 @@ def test_fp32_batched_groups_and_ragged_k(hip, gs, K, M):
     close(y, ref_linear(x, W64, b64, "silu"), torch.float32)
 
 
-@pytest.mark.parametrize("B", [1, 2, 5, 16])
+@pytest.mark.parametrize("B", [1, 2, 5, 8, 16])
 @pytest.mark.parametrize("split_k", [1, 3])
 def test_fp32_fused_gate_up(hip, B, split_k):
+    """Fused gate-up with fp32 x -- the streaming kernel at batch 1, the batched streaming kernel
+    at 2..8, the fp32 matrix-core kernel at 16 -- with and without K splits, against the oracle."""
     g, G64, _, _ = make(11008 // 8, 4096, 3, torch.float32, seed=4)
     u, U64, _, _ = make(11008 // 8, 4096, 3, torch.float32, seed=5)
     x = randx(B, 4096, torch.float32, seed=B)
@@ -158,7 +160,7 @@ def test_fp32_fused_gate_up(hip, B, split_k):
 
 
 @pytest.mark.parametrize("bits", [3, (4, 2, 3)])
-@pytest.mark.parametrize("B", [1, 4, 17])
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 17])
 @pytest.mark.parametrize("rope,head_dim", [(False, 0), (False, 64), (True, 64)])
 def test_fp32_fused_qkv(hip, bits, B, rope, head_dim):
     """Fused QKV (GQA widths, bias, mixed widths, RoPE on pair-interleaved Q/K) through the
